@@ -1,0 +1,136 @@
+"""ctypes binding of ``libg2ptq_hip.so`` (the C ABI declared in include/g2ptq_hip.h).
+
+There is no fallback: if the library is missing or cannot be loaded, every
+entry point raises.  Build it with ``python -m g2ptq_amd.build``.
+"""
+import ctypes
+import os
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libg2ptq_hip.so")
+
+FLAG_BAD_SCALE = 1
+FLAG_NAN_OUTPUT = 2
+VARIANT_GPTQ, VARIANT_GPTAQ, VARIANT_G2PTQ = 0, 1, 2
+
+_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int
+_f32 = ctypes.c_float
+_sz = ctypes.c_size_t
+_szp = ctypes.POINTER(ctypes.c_size_t)
+
+# name -> argtypes (all functions return int status except the two string ones)
+SIGNATURES = {
+    "g2ptq_abi_version": [],
+    "g2ptq_find_params": [_p, _p, _i64, _i64, _i64, _i32, _i32, _p, _p, _i64, _p],
+    "g2ptq_find_params_mse": [_p, _p, _i64, _i64, _i64, _i32, _i32, _f32, _i32, _f32, _p, _p, _i64, _p],
+    "g2ptq_fake_quantize": [_p, _p, _i64, _i64, _i64, _i64, _p, _p, _i64, _i32, _p, _i64, _p, _i64, _p],
+    "g2ptq_hessian_workspace": [_i64, _i64, _i32, _szp],
+    "g2ptq_hessian_update": [_p, _p, _i64, _i64, _i64, _f32, _f32, _p, _i64, _p, _sz],
+    "g2ptq_gptaq_update": [_p, _p, _p, _i64, _i64, _i64, _i64, _f32, _f32, _p, _p, _i64, _p, _sz],
+    "g2ptq_weighted_hessian_update": [_p, _p, _i64, _i64, _i64, _p, _i64, _i64, _f32, _f32, _p, _i64,
+                                      _i64, _p, _f32, _f32, _p, _sz],
+    "g2ptq_prepare_hessian": [_p, _p, _i64, _i64, _p, _i64, _p, _p, _i64, _p, _sz],
+    "g2ptq_factor_workspace": [_i64, _i64, _szp],
+    "g2ptq_inv_chol_upper": [_p, _p, _i64, _i64, _f32, _p, _p, _p, _p, _sz],
+    "g2ptq_block_sweep": [_p, _i32, _i64, _i64, _i64, _i32, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p],
+    "g2ptq_compensate_workspace": [_i32, _i64, _i64, _i64, _i64, _szp],
+    "g2ptq_compensate": [_p, _i32, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _i32, _i32, _i64, _i32,
+                         _i32, _f32, _f32, _p, _p, _p, _p, _p, _p, _p, _p, _sz],
+    "g2ptq_gptaq_p": [_p, _p, _p, _i64, _i64, _f32, _p, _p, _sz],
+    "g2ptq_trust_region": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _f32, _i32, _p, _p, _p, _p, _sz],
+    "g2ptq_trust_region_workspace": [_i64, _i64, _i64, _szp],
+    "g2ptq_act_order": [_p, _p, _i64, _i64, _i32, _p, _p, _p, _sz],
+    "g2ptq_permute_cols": [_p, _p, _p, _i64, _i64, _p],
+    "g2ptq_permute_sym": [_p, _p, _p, _i64, _i64, _p],
+    "g2ptq_cast_check": [_p, _p, _p, _i64, _i32, _p],
+    "g2ptq_to_f32": [_p, _p, _p, _i64, _i32],
+    "g2ptq_gemm_f32": [_p, _i64, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _i32, _p, _i64, _i64,
+                       _p, _i64, _i64, _f32, _f32],
+}
+STRING_FUNCS = ("g2ptq_status_string", "g2ptq_last_error")
+
+_LIB = None
+
+
+class HipLibraryError(RuntimeError):
+    pass
+
+
+def load():
+    """Load the library once; raise if it is missing (no CPU fallback exists)."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not os.path.exists(LIB_PATH):
+        raise HipLibraryError(
+            f"{LIB_PATH} not found: build it with `python -m g2ptq_amd.build` "
+            "(the quantization path has no non-HIP fallback)")
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, args in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = ctypes.c_int
+    for name in STRING_FUNCS:
+        fn = getattr(lib, name)
+        fn.restype = ctypes.c_char_p
+    lib.g2ptq_status_string.argtypes = [ctypes.c_int]
+    lib.g2ptq_last_error.argtypes = []
+    _LIB = lib
+    return lib
+
+
+def call(name, *args):
+    """Call an int-returning entry point and raise on a nonzero status."""
+    lib = load()
+    status = getattr(lib, name)(*args)
+    if status != 0:
+        detail = lib.g2ptq_last_error().decode(errors="replace")
+        kind = lib.g2ptq_status_string(status).decode()
+        if status == -1:
+            raise ValueError(f"{name}: {kind}: {detail}")
+        raise RuntimeError(f"{name}: {kind}: {detail}")
+    return status
+
+
+def query_size(name, *args):
+    out = ctypes.c_size_t(0)
+    call(name, *args, ctypes.byref(out))
+    return out.value
+
+
+def ptr(t):
+    """Device pointer of a tensor (None → NULL)."""
+    if t is None:
+        return None
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def stream_ptr(device=None):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+_WORKSPACES = {}
+
+
+def workspace(nbytes, device):
+    """A cached uint8 device buffer of at least ``nbytes`` bytes.
+
+    Buffers are cached per device and reused across calls; callers enqueue on
+    the current stream, so stream order protects reuse.
+    """
+    nbytes = max(int(nbytes), 256)
+    dev = torch.device(device)
+    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    buf = _WORKSPACES.get(key)
+    if buf is None or buf.numel() < nbytes:
+        _WORKSPACES[key] = None
+        buf = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        _WORKSPACES[key] = buf
+    return buf
+
+
+def release_workspaces():
+    _WORKSPACES.clear()

@@ -1,0 +1,279 @@
+// Per-layer lazy-batch compensation driver, GPTAQ's P and the G2PTQ trust region.
+//
+// The block loop stays on the host (it is a dependency chain of kernels);
+// each block is: fit the parameters of groups that start in the block
+// (dynamic groups) → fused sweep (one launch for every row of every layer in
+// the batch) → block-tail update of the remaining columns as fp32 MFMA GEMMs.
+#include "sweep.hpp"
+
+namespace g2ptq {
+namespace {
+
+size_t al256(size_t x) { return (x + 255) / 256 * 256; }
+
+// GPTAQ: zero the lower triangle including the diagonal (torch.triu(t, 1)).
+__global__ void triu1_kernel(float* t, int64_t C) {
+  const int64_t b = blockIdx.z;
+  const int64_t i = (int64_t)blockIdx.y * 16 + (threadIdx.x >> 4);
+  const int64_t j0 = (int64_t)blockIdx.x * 64;
+  if (i >= C) return;
+  float* tb = t + b * C * C;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int64_t j = j0 + (threadIdx.x & 15) + 16 * q;
+    if (j < C && j <= i) tb[i * C + j] = 0.f;
+  }
+}
+
+// diag(A⁻¹)[c] = Σ_i U[i][c]² (A⁻¹ = UᵀU), one thread per column.
+__global__ void inv_diag_kernel(const float* __restrict__ U, int64_t C, float* dA) {
+  const int64_t b = blockIdx.y;
+  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (c >= C) return;
+  const float* Ub = U + b * C * C;
+  float s = 0.f;
+  for (int64_t i = 0; i <= c; ++i) {
+    const float u = Ub[i * C + c];
+    s += u * u;
+  }
+  dA[b * C + c] = s;
+}
+
+__device__ float block_sum(float v, float* red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  float s = 0.f;
+  for (int i = 0; i < (int)(blockDim.x >> 6); ++i) s += red[i];
+  return s;
+}
+
+// One workgroup per output row of a row group: β from the row statistics,
+// then Z = β·T1 and GH = β·GA in place (Z holds T1, GH holds GA on entry).
+__global__ __launch_bounds__(256) void trust_row_kernel(const float* __restrict__ Grad,
+                                                        const float* __restrict__ Q0,
+                                                        const float* __restrict__ W0,
+                                                        const float* __restrict__ dA, int64_t Rg,
+                                                        int64_t C, float two_alpha, float* beta,
+                                                        float* Z, float* GH) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;  // over BG*Rg
+  const int64_t bg = row / Rg;
+  const float* g = Grad + row * C;
+  const float* q0 = Q0 + row * C;
+  const float* w0 = W0 + row * C;
+  const float* da = dA + bg * C;
+  float* z = Z + row * C;
+  float* gh = GH + row * C;
+  float cs = 0.f;
+  for (int64_t j = threadIdx.x; j < C; j += 256) cs += g[j] * gh[j];
+  const float crow = block_sum(cs, red);
+  const float tiny = 1.17549435e-38f;  // torch.finfo(torch.float32).tiny
+  float bs = 0.f;
+  for (int64_t j = threadIdx.x; j < C; j += 256) {
+    const float ga = gh[j], d = da[j];
+    const float e = q0[j] - w0[j];
+    const float loss = fabsf((e * ga + (e * e) / 2.f) / d);
+    const float tl = two_alpha * loss;
+    float c = crow - (ga * ga) / d;
+    c = c < tl ? tl : c;
+    c = c < tiny ? tiny : c;
+    float u = 1.f - tl / c;
+    u = u < 0.f ? 0.f : u;
+    bs += 1.f - sqrtf(u);
+  }
+  const float bsum = block_sum(bs, red);
+  const float bt = bsum / (float)C;
+  if (threadIdx.x == 0) beta[row] = bt;
+  for (int64_t j = threadIdx.x; j < C; j += 256) {
+    z[j] = z[j] * bt;
+    gh[j] = gh[j] * bt;
+  }
+}
+
+}  // namespace
+}  // namespace g2ptq
+
+using namespace g2ptq;
+
+extern "C" int g2ptq_compensate_workspace(int variant, int64_t B, int64_t R, int64_t C,
+                                          int64_t blocksize, size_t* bytes) {
+  (void)variant;
+  (void)C;
+  G2PTQ_CHECK(bytes != nullptr, "compensate_workspace: null out");
+  *bytes = al256((size_t)B * R * std::max<int64_t>(blocksize, 1) * 4);
+  return G2PTQ_OK;
+}
+
+extern "C" int g2ptq_compensate(void* stream, int variant, int64_t B, int64_t R, int64_t C,
+                                int64_t bs, float* W, const float* U, const float* P,
+                                const float* Z, float* GH, int bits, int sym, int64_t groupsize,
+                                int static_groups, int mse_grid, float mse_norm,
+                                float mse_maxshrink, const int* colgroup, float* scale_tab,
+                                float* zero_tab, float* Q, float* Wint, float* Scale, int* flags,
+                                void* ws, size_t ws_bytes) {
+  G2PTQ_CHECK(W && U && scale_tab && zero_tab && Q, "compensate: null pointer");
+  G2PTQ_CHECK(bits >= 2 && bits <= 16, "compensate: bits=%d unsupported", bits);
+  G2PTQ_CHECK(bs >= 1 && bs <= kMaxBlock, "compensate: blocksize %lld not in [1, %d]",
+              (long long)bs, kMaxBlock);
+  G2PTQ_CHECK(groupsize == -1 || groupsize > 0, "compensate: bad groupsize");
+  G2PTQ_CHECK(variant != G2PTQ_VARIANT_GPTAQ || P, "compensate: GPTAQ needs P");
+  G2PTQ_CHECK(variant != G2PTQ_VARIANT_G2PTQ || (Z && GH), "compensate: G2PTQ needs Z and GH");
+  G2PTQ_CHECK(B >= 1 && B < 65536 && R >= 1 && C >= 1, "compensate: bad sizes");
+  size_t need = 0;
+  g2ptq_compensate_workspace(variant, B, R, C, bs, &need);
+  G2PTQ_CHECK(ws && ws_bytes >= need, "compensate: workspace %zu < %zu", ws_bytes, need);
+  hipStream_t s = as_stream(stream);
+  const int maxq = (1 << (bits - 1)) - 1;
+  const bool dynamic = groupsize > 0 && !static_groups;
+  float* E = static_cast<float*>(ws);
+  const int64_t RC = R * C, CC = C * C;
+
+  for (int64_t i1 = 0; i1 < C; i1 += bs) {
+    const int64_t i2 = std::min(i1 + bs, C), n = i2 - i1;
+    if (dynamic) {
+      for (int64_t gs = (i1 + groupsize - 1) / groupsize * groupsize; gs < i2; gs += groupsize) {
+        const int64_t gi = gs / groupsize;
+        const int64_t width = std::min(groupsize, C - gs);
+        if (mse_grid > 0)
+          G2PTQ_TRY(launch_find_params_mse(s, W + gs, B * R, width, C, maxq, sym, mse_norm,
+                                           mse_grid, mse_maxshrink, scale_tab + gi * B * R,
+                                           zero_tab + gi * B * R, 1, flags));
+        else
+          G2PTQ_TRY(launch_find_params(s, W + gs, B * R, width, C, maxq, sym,
+                                       scale_tab + gi * B * R, zero_tab + gi * B * R, 1, flags));
+      }
+    }
+    SweepArgs a{};
+    a.R = R; a.n = (int)n; a.maxq = maxq;
+    a.W = W + i1; a.wb = RC; a.wr = C; a.wc = 1;
+    a.U = U + i1 * C + i1; a.ub = CC; a.uj = C;
+    a.P = P ? P + i1 * C + i1 : nullptr;
+    a.Zg = Z ? Z + i1 : nullptr; a.zb = RC; a.zr = C; a.zc = 1;
+    a.GH = GH ? GH + i1 : nullptr; a.GHout = nullptr; a.gb = RC; a.gr = C; a.gc = 1;
+    a.S = scale_tab; a.Z0 = zero_tab; a.sb = R; a.sr = 1; a.sg = B * R;
+    a.colgroup = colgroup ? colgroup + i1 : nullptr;
+    a.col0 = i1;
+    a.gsize = groupsize > 0 ? groupsize : 0;
+    a.Q = Q + i1; a.qb = RC; a.qr = C; a.qc = 1;
+    a.I = Wint ? Wint + i1 : nullptr; a.ib = RC; a.ir = C; a.ic = 1;
+    a.Sc = Scale ? Scale + i1 : nullptr; a.cb = RC; a.cr = C; a.cc = 1;
+    a.CW = nullptr;
+    if (variant == G2PTQ_VARIANT_G2PTQ) {
+      a.E = nullptr;
+      a.E2 = E; a.e2b = R * n; a.e2r = n; a.e2c = 1;
+      a.dist0 = bs - 1;
+    } else {
+      a.E = E; a.eb = R * n; a.er = n; a.ec = 1;
+      a.E2 = nullptr;
+    }
+    a.flags = flags;
+    G2PTQ_TRY(launch_sweep(s, variant, a, B));
+    if (i2 >= C) break;
+
+    // Block tail: W[:, :, i2:] -= E · U[i1:i2, i2:]  (+ variant terms).
+    GemmF32 t;
+    t.M = R; t.N = C - i2; t.K = n; t.batch = B;
+    t.A = E; t.lda = n; t.sA = R * n;
+    t.B = U + i1 * C + i2; t.ldb = C; t.sB = CC;
+    t.C = W + i2; t.ldc = C; t.sC = RC;
+    t.D = W + i2; t.ldd = C; t.sD = RC;
+    t.alpha = -1.f; t.beta = 1.f;
+    if (variant == G2PTQ_VARIANT_G2PTQ) {
+      // W -= bs·GH[:, i2:] + (E − Z·D)·U_slab, with E2 = E − Z·D from the sweep.
+      t.X = GH + i2; t.ldx = C; t.sX = RC; t.gamma = -(float)bs;
+    }
+    G2PTQ_TRY(gemm_f32(s, t));
+    if (variant == G2PTQ_VARIANT_GPTAQ) {
+      GemmF32 p = t;  // W += Q1 · P[i1:i2, i2:]
+      p.A = Q + i1; p.lda = C; p.sA = RC;
+      p.B = P + i1 * C + i2;
+      p.alpha = 1.f;
+      G2PTQ_TRY(gemm_f32(s, p));
+    } else if (variant == G2PTQ_VARIANT_G2PTQ) {
+      GemmF32 z = t;  // GH[:, i2:] -= Z1 · U_slab
+      z.A = Z + i1; z.lda = C; z.sA = RC;
+      z.C = GH + i2; z.D = GH + i2;
+      z.X = nullptr; z.gamma = 0.f;
+      G2PTQ_TRY(gemm_f32(s, z));
+    }
+  }
+  return G2PTQ_OK;
+}
+
+extern "C" int g2ptq_gptaq_p(void* stream, const float* Dx, const float* U, int64_t B, int64_t C,
+                             float alpha, float* P, void* ws, size_t ws_bytes) {
+  G2PTQ_CHECK(Dx && U && P, "gptaq_p: null pointer");
+  const size_t need = al256((size_t)B * C * C * 4);
+  G2PTQ_CHECK(ws && ws_bytes >= need, "gptaq_p: workspace %zu < %zu", ws_bytes, need);
+  hipStream_t s = as_stream(stream);
+  float* T = static_cast<float*>(ws);
+  const int64_t CC = C * C;
+  GemmF32 a;  // T = Dx · Uᵀ
+  a.M = C; a.N = C; a.K = C; a.batch = B;
+  a.A = Dx; a.lda = C; a.sA = CC;
+  a.B = U; a.ldb = C; a.sB = CC; a.b_kcontig = 1;
+  a.D = T; a.ldd = C; a.sD = CC;
+  G2PTQ_TRY(gemm_f32(s, a));
+  dim3 grid((unsigned)cdiv(C, 64), (unsigned)cdiv(C, 16), (unsigned)B);
+  hipLaunchKernelGGL(triu1_kernel, grid, dim3(256), 0, s, T, C);
+  G2PTQ_LAUNCHED();
+  GemmF32 b;  // P = alpha · triu(T, 1) · U
+  b.M = C; b.N = C; b.K = C; b.batch = B;
+  b.A = T; b.lda = C; b.sA = CC;
+  b.B = U; b.ldb = C; b.sB = CC;
+  b.D = P; b.ldd = C; b.sD = CC;
+  b.alpha = alpha;
+  G2PTQ_TRY(gemm_f32(s, b));
+  return G2PTQ_OK;
+}
+
+extern "C" int g2ptq_trust_region_workspace(int64_t BG, int64_t Rg, int64_t C, size_t* bytes) {
+  (void)Rg;
+  G2PTQ_CHECK(bytes != nullptr, "trust_region_workspace: null out");
+  *bytes = al256((size_t)BG * C * 4);
+  return G2PTQ_OK;
+}
+
+extern "C" int g2ptq_trust_region(void* stream, const float* Grad, const float* U,
+                                  const float* Q0, const float* W0, int64_t BG, int64_t Rg,
+                                  int64_t C, float alpha, int enabled, float* beta, float* Z,
+                                  float* GH, void* ws, size_t ws_bytes) {
+  G2PTQ_CHECK(beta && Z && GH, "trust_region: null output");
+  hipStream_t s = as_stream(stream);
+  const int64_t n = BG * Rg * C;
+  if (!enabled) {
+    G2PTQ_TRY(fill_f32(s, beta, BG * Rg, 0.f));
+    G2PTQ_TRY(fill_f32(s, Z, n, 0.f));
+    G2PTQ_TRY(fill_f32(s, GH, n, 0.f));
+    return G2PTQ_OK;
+  }
+  G2PTQ_CHECK(Grad && U && Q0 && W0, "trust_region: null input");
+  size_t need = 0;
+  g2ptq_trust_region_workspace(BG, Rg, C, &need);
+  G2PTQ_CHECK(ws && ws_bytes >= need, "trust_region: workspace %zu < %zu", ws_bytes, need);
+  float* dA = static_cast<float*>(ws);
+  const int64_t CC = C * C, RC = Rg * C;
+  GemmF32 a;  // Z ← T1 = Grad · Uᵀ
+  a.M = Rg; a.N = C; a.K = C; a.batch = BG;
+  a.A = Grad; a.lda = C; a.sA = RC;
+  a.B = U; a.ldb = C; a.sB = CC; a.b_kcontig = 1;
+  a.D = Z; a.ldd = C; a.sD = RC;
+  G2PTQ_TRY(gemm_f32(s, a));
+  GemmF32 b;  // GH ← GA = T1 · U = Grad · A⁻¹
+  b.M = Rg; b.N = C; b.K = C; b.batch = BG;
+  b.A = Z; b.lda = C; b.sA = RC;
+  b.B = U; b.ldb = C; b.sB = CC;
+  b.D = GH; b.ldd = C; b.sD = RC;
+  G2PTQ_TRY(gemm_f32(s, b));
+  hipLaunchKernelGGL(inv_diag_kernel, dim3((unsigned)cdiv(C, 256), (unsigned)BG), dim3(256), 0, s,
+                     U, C, dA);
+  G2PTQ_LAUNCHED();
+  hipLaunchKernelGGL(trust_row_kernel, dim3((unsigned)(BG * Rg)), dim3(256), 0, s, Grad, Q0, W0,
+                     dA, Rg, C, (float)(2.0 * (double)alpha), beta, Z, GH);
+  G2PTQ_LAUNCHED();
+  return G2PTQ_OK;
+}

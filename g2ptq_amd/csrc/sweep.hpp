@@ -1,0 +1,43 @@
+// Block-sweep argument block shared by the run_eager entry point and the
+// per-layer compensation driver.
+#pragma once
+#include "common.hpp"
+
+namespace g2ptq {
+
+constexpr int kMaxBlock = 128;  // largest supported lazy-batch block width
+
+// Element (b, r, c) of a strided 3-D operand lives at p + b*sb + r*sr + c*sc.
+struct SweepArgs {
+  int64_t R;     // rows per layer
+  int n;         // block width (columns), 1..kMaxBlock
+  int maxq;
+  const float* W; int64_t wb, wr, wc;          // block input values
+  const float* U; int64_t ub, uj;              // U(b, j, k) = U[b*ub + j*uj + k]
+  const float* P;                              // GPTAQ, same strides as U
+  const float* Zg; int64_t zb, zr, zc;         // G2PTQ z
+  const float* GH; int64_t gb, gr, gc;         // G2PTQ ghinv (block input)
+  float* GHout;                                // block ghinv written back (nullable; same strides)
+  // Quantizer parameters: scale of (b, r, column j) = S[b*sb + r*sr + group(j)*sg]
+  // with group(j) = colgroup[j] if colgroup, else (col0 + j) / gsize (gsize <= 0: 0).
+  const float* S; const float* Z0; int64_t sb, sr, sg;
+  const int* colgroup; int64_t col0; int64_t gsize;
+  float* Q; int64_t qb, qr, qc;                // dequantized output
+  float* I; int64_t ib, ir, ic;                // integer codes (nullable)
+  float* E; int64_t eb, er, ec;                // scaled errors (nullable)
+  float* Sc; int64_t cb, cr, cc;               // per-column scale (nullable)
+  float* CW; int64_t cwb, cwr;                 // GPTAQ last pre-quant column (nullable)
+  float* E2; int64_t e2b, e2r, e2c;            // G2PTQ: err - z*(dist0 - j) (nullable)
+  int64_t dist0;                               // G2PTQ: blocksize - 1
+  int* flags;
+};
+
+int launch_sweep(hipStream_t stream, int variant, const SweepArgs& a, int64_t B);
+int launch_find_params(hipStream_t stream, const float* x, int64_t rows, int64_t cols,
+                       int64_t ldx, int maxq, int sym, float* scale, float* zero, int64_t ldp,
+                       int* flags);
+int launch_find_params_mse(hipStream_t stream, const float* x, int64_t rows, int64_t cols,
+                           int64_t ldx, int maxq, int sym, float norm, int grid, float maxshrink,
+                           float* scale, float* zero, int64_t ldp, int* flags);
+
+}  // namespace g2ptq

@@ -1,0 +1,153 @@
+"""GPTAQ per-layer quantizer on MI355X.
+
+Drop-in for ``GPTAQ`` and ``run_eager`` of gptq_utils/gptaq_utils.py
+(:74-399 of the reference).  The asymmetric-calibration cross term
+``dXXT = (2/n)(X_fp − X)ᵀX`` is accumulated in the same MFMA pass as the
+Hessian; ``P = α·triu(dXXT·Uᵀ, 1)·U`` and the compensation (``+w̃·P`` inside a
+block, ``+Q·P`` in the block tail) run in libg2ptq_hip.so.
+"""
+import torch
+
+from . import _core, _lib
+from .gptq_utils import _compensate
+from .graph_utils import run_graph, validate_tensors
+
+
+def run_eager(weight, hinv, p, scale, zero, maxq, backend, column_weight=None, int_weight=None,
+              error=None):
+    """gptq_utils/gptaq_utils.py:74-100 (transposed block layout (B, bs, R))."""
+    validate_tensors(f"{backend} GPTAQ", weight, hinv, p, scale, zero, column_weight, int_weight,
+                     error)
+    _core.check_backend(backend)
+    B, bs, R = weight.shape
+    _lib.call("g2ptq_block_sweep", _core.stream(), _lib.VARIANT_GPTAQ, B, bs, R, int(maxq),
+              _lib.ptr(weight), _lib.ptr(hinv), _lib.ptr(p), _lib.ptr(scale), _lib.ptr(zero),
+              None, None, _lib.ptr(column_weight), _lib.ptr(int_weight), _lib.ptr(error), None)
+    return weight, int_weight, error
+
+
+class GPTAQ:
+    """gptq_utils/gptaq_utils.py:103-399."""
+
+    def __init__(self, layers, offload_hessians: bool = False):
+        self.layers = layers
+        self.num_layers = len(layers)
+        self.offload_hessians = offload_hessians
+        weight = layers[0].weight
+        self.dev = weight.device
+        self.rows, self.columns = weight.shape
+        H_device = "cpu" if offload_hessians else self.dev
+        self.H = _core.alloc((self.num_layers, self.columns, self.columns), H_device)
+        self.dXXT = _core.alloc((self.num_layers, self.columns, self.columns), H_device)
+        self.nsamples = torch.tensor([0] * self.num_layers, device=self.dev)
+        self._n = [0] * self.num_layers
+        self.fp_inp = [[] for _ in range(self.num_layers)]
+
+    def _maybe_onload_hessian(self):
+        """gptaq_utils.py:123-128."""
+        return _core.onload_attrs(self, ("H", "dXXT"), enabled=self.offload_hessians,
+                                  device=self.dev)
+
+    def add_batch(self, idx, inp, out):
+        """gptaq_utils.py:130-148 (``fp_inp[idx]`` is a FIFO of (tokens, C) tensors)."""
+        fp = self.fp_inp[idx][0].to(inp.device, non_blocking=True)
+        if len(inp.shape) == 2:
+            inp = inp.unsqueeze(0)
+        tmp = inp.shape[0]
+        X = _core.as_bf16_tokens(inp)
+        Xfp = _core.as_bf16_tokens(fp.to(inp.dtype))
+        if Xfp.shape != X.shape:
+            raise ValueError(f"fp_inp shape {tuple(Xfp.shape)} != input {tuple(X.shape)}")
+        n = self._n[idx]
+        beta = _core.f32(n / (n + tmp))
+        n += tmp
+        self._n[idx] = n
+        self.nsamples[idx] += tmp
+        _core.gptaq_update(self.H[idx], self.dXXT[idx], X, Xfp, _core.sqrt_scale_sq(n), beta)
+        del self.fp_inp[idx][0]
+
+    def _run_compensation_block(self, weight, hinv, p, scale, zero, backend, graph):
+        """gptaq_utils.py:150-191."""
+        quantizer = self.quantizer[0]
+        weight = weight.transpose(1, 2).contiguous()
+        params = {
+            "weight": weight,
+            "hinv": hinv.contiguous(),
+            "p": p.contiguous(),
+            "scale": scale.transpose(1, 2).contiguous(),
+            "zero": zero.transpose(1, 2).contiguous(),
+            "maxq": quantizer.maxq,
+            "backend": backend,
+            "column_weight": torch.empty(weight.shape[0], weight.shape[2], dtype=weight.dtype,
+                                         device=weight.device),
+            "int_weight": torch.empty_like(weight),
+            "error": torch.empty_like(weight),
+        }
+        if graph:
+            out = run_graph(run_eager, params,
+                            input_names=("weight", "hinv", "p", "scale", "zero"),
+                            output_names=("weight", "int_weight", "error"),
+                            name="GPTAQ compensation block")
+        else:
+            out = run_eager(**params)
+        return tuple(t.transpose(1, 2).contiguous() for t in out)
+
+    def _run_compensation(self, W, Hinv, P, blocksize, groupsize, static_groups, qparam_perm,
+                          backend, graph, H_diag=None):
+        """gptaq_utils.py:193-261."""
+        _core.check_backend(backend)
+        if H_diag is not None:
+            raise NotImplementedError("hclip (H_diag) is not implemented by the HIP path")
+        flags = torch.zeros(1, dtype=torch.int32, device=W.device)
+        out = _compensate(_lib.VARIANT_GPTAQ, self.quantizer, W, Hinv, blocksize, groupsize,
+                          static_groups, qparam_perm, flags, graph, P=P.contiguous())
+        self._last_flags = flags
+        return out
+
+    def fasterquant(self, blocksize=128, percdamp=0.01, groupsize=-1, actorder=False,
+                    static_groups=False, alpha=0.25, export_compressed_tensors=False,
+                    backend="hip", graph=False):
+        """gptaq_utils.py:263-391."""
+        _core.check_backend(backend)
+        _core.check_export(export_compressed_tensors)
+        if self.quantizer[0].hclip:
+            raise NotImplementedError("hclip (Hessian-diagonal clip search) is not implemented")
+        W = _core.stack_weights_f32(self.layers)
+        B, R, C = W.shape
+        W_flat = W.view(B * R, C)
+        flags = torch.zeros(1, dtype=torch.int32, device=self.dev)
+        with self._maybe_onload_hessian():
+            H = self.H
+            self.H = None
+            _core.fit_static_params(self.quantizer, W_flat, groupsize, static_groups, flags)
+            _core.prepare_hessian(H, W, Dx=self.dXXT)
+            perm = invperm = None
+            if actorder:
+                perm, invperm = _core.act_order(H, 0)
+                W = _core.permute_cols(W, perm)
+                H = _core.permute_sym(H, perm)
+                self.dXXT.copy_(_core.permute_sym(self.dXXT, perm))
+            Hinv, _ = _core.factor(H, percdamp)
+            P = torch.empty_like(Hinv)
+            ws = _lib.workspace(B * C * C * 4 + 256, self.dev)
+            _lib.call("g2ptq_gptaq_p", _core.stream(), _lib.ptr(self.dXXT), _lib.ptr(Hinv), B, C,
+                      _core.f32(alpha), _lib.ptr(P), _lib.ptr(ws), ws.numel())
+        Q, W_int, Scale = _compensate(_lib.VARIANT_GPTAQ, self.quantizer, W, Hinv, blocksize,
+                                      groupsize, static_groups,
+                                      perm if static_groups and actorder else None, flags, graph,
+                                      P=P)
+        if actorder:
+            Q = _core.permute_cols(Q, invperm)
+            W_int = _core.permute_cols(W_int, invperm)
+            Scale = _core.permute_cols(Scale, invperm)
+        _core.write_back(self.layers, Q, flags)
+        _core.finish(flags)
+
+    def free(self):
+        """gptaq_utils.py:393-399."""
+        self.H = None
+        self.Losses = None
+        self.dXXT = None
+        self.nsamples = None
+        self.fp_inp = None
+        _lib.release_workspaces()

@@ -1,0 +1,98 @@
+"""GuidedQuant per-layer quantizer on MI355X.
+
+Drop-in for ``GPTQGuided`` of gptq_utils/gptq_guided_utils.py (:25-219 of the
+reference): saliency-weighted per-row-group Hessians (shared MFMA kernel with
+G2PTQ) and GPTQ's compensation, inherited unchanged.
+"""
+import torch
+
+from . import _core, _lib
+from .gptq_utils import GPTQ, _compensate
+
+
+class GPTQGuided(GPTQ):
+    """gptq_utils/gptq_guided_utils.py:25-219."""
+
+    def __init__(self, layers, saliencies, num_groups: int, offload_hessians: bool = False):
+        self.layers = layers
+        self.num_layers = len(layers)
+        self.offload_hessians = offload_hessians
+        weight = layers[0].weight
+        self.dev = weight.device
+        self.rows, self.columns = weight.shape
+        self.num_groups = num_groups
+        # saliencies: per layer a (N, seq_len, G) tensor
+        self.saliencies = [s.float() for s in saliencies]
+        H_device = "cpu" if offload_hessians else self.dev
+        self.H = _core.alloc((self.num_layers, self.num_groups, self.columns, self.columns),
+                             H_device)
+        self.act_square = torch.zeros((self.num_layers, self.columns), device=self.dev)
+        self.index = torch.tensor([0] * self.num_layers, device=self.dev)
+        self._k = [0] * self.num_layers
+        assert self.rows % self.num_groups == 0, (
+            f"Number of rows ({self.rows}) must be divisible by num_groups ({self.num_groups})")
+
+    def _maybe_onload_hessian(self):
+        """gptq_guided_utils.py:53-57."""
+        return _core.onload_attrs(self, ("H",), enabled=self.offload_hessians, device=self.dev)
+
+    @torch.no_grad()
+    def add_batch(self, idx, inp, out):
+        """gptq_guided_utils.py:59-81: H[g] += Σ_t s_tg x xᵀ; act += Σ x² / T."""
+        if inp.dim() == 2:
+            inp = inp.unsqueeze(0)
+        else:
+            assert inp.dim() == 3, "Input must be 2D or 3D. Got %dD." % inp.dim()
+        bsz = inp.shape[0]
+        k = self._k[idx]
+        sal = self.saliencies[idx][k:k + bsz].to(self.dev)
+        self._k[idx] = k + bsz
+        self.index[idx] += bsz
+        X = _core.as_bf16_tokens(inp)
+        sal = sal.reshape(-1, sal.shape[-1]).float()
+        n_tokens = X.shape[0]
+        _core.weighted_update(self.H[idx], X, sal, 1.0, 1.0, self.act_square[idx],
+                              _core.f32(1 / n_tokens), 1.0)
+
+    def fasterquant(self, blocksize=128, percdamp=0.01, groupsize=-1, actorder=False,
+                    static_groups=False, export_compressed_tensors=False, backend="hip",
+                    graph=False):
+        """gptq_guided_utils.py:83-211."""
+        _core.check_backend(backend)
+        _core.check_export(export_compressed_tensors)
+        if self.quantizer[0].hclip:
+            raise NotImplementedError("hclip (Hessian-diagonal clip search) is not implemented")
+        W = _core.stack_weights_f32(self.layers)
+        B, R, C = W.shape
+        G = self.num_groups
+        W_flat = W.view(B * R, C)
+        W_sub = W.view(B * G, R // G, C)
+        flags = torch.zeros(1, dtype=torch.int32, device=self.dev)
+        with self._maybe_onload_hessian():
+            H = self.H
+            self.H = None
+            H_sub = H.view(B * G, C, C)
+            _core.fit_static_params(self.quantizer, W_flat, groupsize, static_groups, flags)
+            _core.prepare_hessian(H_sub, W_sub)
+            perm = invperm = None
+            if actorder:
+                perm, invperm = _core.act_order(self.act_square, 1)
+                W_sub = _core.permute_cols(W_sub, perm)
+                H_sub = _core.permute_sym(H_sub, perm)
+            Hinv, _ = _core.factor(H_sub, percdamp)
+        Q, W_int, Scale = _compensate(_lib.VARIANT_GPTQ, self.quantizer, W_sub, Hinv, blocksize,
+                                      groupsize, static_groups,
+                                      perm if static_groups and actorder else None, flags, graph)
+        if actorder:
+            Q = _core.permute_cols(Q, invperm)
+        _core.write_back(self.layers, Q.view(B, R, C), flags)
+        _core.finish(flags)
+
+    def free(self):
+        """gptq_guided_utils.py:213-219."""
+        self.H = None
+        self.Losses = None
+        self.act_square = None
+        self.saliencies = None
+        self.index = None
+        _lib.release_workspaces()

@@ -1,0 +1,144 @@
+"""GPTQ per-layer quantizer on MI355X.
+
+Drop-in for the ``GPTQ`` class and ``run_eager`` of gptq_utils/gptq_utils.py
+(:67-359 of the reference): same constructor, attributes and methods, with a
+``"hip"`` backend.  ``add_batch`` accumulates the Hessian with the bf16 MFMA
+Gram kernel, ``fasterquant`` runs the dampened inverse-Cholesky factor and
+the fused lazy-batch compensation in libg2ptq_hip.so.
+"""
+import torch
+
+from . import _core, _lib
+from .graph_utils import run_graph, validate_tensors
+
+
+def run_eager(weight, hinv, scale, zero, maxq, backend, int_weight=None, error=None):
+    """gptq_utils/gptq_utils.py:67-90 — one prepared block on the transposed
+    layout (B, bs, R); outputs written in place and returned."""
+    validate_tensors(f"{backend} GPTQ", weight, hinv, scale, zero, int_weight, error)
+    _core.check_backend(backend)
+    B, bs, R = weight.shape
+    _lib.call("g2ptq_block_sweep", _core.stream(), _lib.VARIANT_GPTQ, B, bs, R, int(maxq),
+              _lib.ptr(weight), _lib.ptr(hinv), None, _lib.ptr(scale), _lib.ptr(zero), None, None,
+              None, _lib.ptr(int_weight), _lib.ptr(error), None)
+    return weight, int_weight, error
+
+
+class GPTQ:
+    """gptq_utils/gptq_utils.py:93-359."""
+
+    def __init__(self, layers, offload_hessians: bool = False):
+        self.layers = layers
+        self.num_layers = len(layers)
+        self.offload_hessians = offload_hessians
+        weight = layers[0].weight
+        self.dev = weight.device
+        self.rows, self.columns = weight.shape
+        H_device = "cpu" if offload_hessians else self.dev
+        self.H = _core.alloc((self.num_layers, self.columns, self.columns), H_device)
+        self.nsamples = torch.tensor([0] * self.num_layers, device=self.dev)
+        self._n = [0] * self.num_layers  # host mirror of nsamples (no syncs in add_batch)
+
+    def _maybe_onload_hessian(self, idx=None):
+        """gptq_utils.py:109-113."""
+        return _core.onload_attrs(self, ("H",), enabled=self.offload_hessians, device=self.dev)
+
+    def add_batch(self, idx, inp, out):
+        """gptq_utils.py:115-126: H ← H·n/(n+t) + (2/(n+t))·XᵀX, t = #sequences."""
+        if len(inp.shape) == 2:
+            inp = inp.unsqueeze(0)
+        tmp = inp.shape[0]
+        X = _core.as_bf16_tokens(inp)
+        n = self._n[idx]
+        beta = _core.f32(n / (n + tmp))
+        n += tmp
+        self._n[idx] = n
+        self.nsamples[idx] += tmp
+        _core.hessian_update(self.H[idx], X, _core.sqrt_scale_sq(n), beta)
+
+    def _run_compensation_block(self, weight, hinv, scale, zero, backend, graph):
+        """gptq_utils.py:128-163 — one block in (B, R, bs) layout."""
+        quantizer = self.quantizer[0]
+        weight = weight.transpose(1, 2).contiguous()
+        params = {
+            "weight": weight,
+            "hinv": hinv.contiguous(),
+            "scale": scale.transpose(1, 2).contiguous(),
+            "zero": zero.transpose(1, 2).contiguous(),
+            "maxq": quantizer.maxq,
+            "backend": backend,
+            "int_weight": torch.empty_like(weight),
+            "error": torch.empty_like(weight),
+        }
+        if graph:
+            out = run_graph(run_eager, params, input_names=("weight", "hinv", "scale", "zero"),
+                            output_names=("weight", "int_weight", "error"),
+                            name="GPTQ compensation block")
+        else:
+            out = run_eager(**params)
+        return tuple(t.transpose(1, 2).contiguous() for t in out)
+
+    def _run_compensation(self, W, Hinv, blocksize, groupsize, static_groups, qparam_perm,
+                          backend, graph, H_diag=None):
+        """gptq_utils.py:165-232: the whole lazy-batch loop, natively.
+
+        ``graph=True`` replays the loop from a HIP graph captured per shape.
+        """
+        _core.check_backend(backend)
+        if H_diag is not None:
+            raise NotImplementedError("hclip (H_diag) is not implemented by the HIP path")
+        flags = torch.zeros(1, dtype=torch.int32, device=W.device)
+        out = _compensate(_lib.VARIANT_GPTQ, self.quantizer, W, Hinv, blocksize, groupsize,
+                          static_groups, qparam_perm, flags, graph)
+        self._last_flags = flags  # device-side failure flags, read by the caller's sync
+        return out
+
+    def fasterquant(self, blocksize=128, percdamp=0.01, groupsize=-1, actorder=False,
+                    static_groups=False, export_compressed_tensors=False, backend="hip",
+                    graph=False):
+        """gptq_utils.py:234-353."""
+        _core.check_backend(backend)
+        _core.check_export(export_compressed_tensors)
+        W = _core.stack_weights_f32(self.layers)
+        B, R, C = W.shape
+        W_flat = W.view(B * R, C)
+        if self.quantizer[0].hclip:
+            raise NotImplementedError("hclip (Hessian-diagonal clip search) is not implemented")
+        flags = torch.zeros(1, dtype=torch.int32, device=self.dev)
+        with self._maybe_onload_hessian():
+            H = self.H
+            self.H = None
+            _core.fit_static_params(self.quantizer, W_flat, groupsize, static_groups, flags)
+            _core.prepare_hessian(H, W)
+            perm = invperm = None
+            if actorder:
+                perm, invperm = _core.act_order(H, 0)
+                W = _core.permute_cols(W, perm)
+                H = _core.permute_sym(H, perm)
+            Hinv, _ = _core.factor(H, percdamp)
+        Q, W_int, Scale = _compensate(_lib.VARIANT_GPTQ, self.quantizer, W, Hinv, blocksize,
+                                      groupsize, static_groups,
+                                      perm if static_groups and actorder else None, flags, graph)
+        if actorder:
+            Q = _core.permute_cols(Q, invperm)
+            W_int = _core.permute_cols(W_int, invperm)
+            Scale = _core.permute_cols(Scale, invperm)
+        _core.write_back(self.layers, Q, flags)
+        _core.finish(flags)
+
+    def free(self):
+        """gptq_utils.py:355-359."""
+        self.H = None
+        self.Losses = None
+        self.nsamples = None
+        _lib.release_workspaces()
+
+
+def _compensate(variant, quantizers, W, U, blocksize, groupsize, static_groups, qparam_perm,
+                flags, graph, P=None, Z=None, GH=None):
+    if not graph:
+        return _core.compensate(variant, W, U, quantizers, blocksize, groupsize, static_groups,
+                                qparam_perm, flags, P=P, Z=Z, GH=GH)
+    from ._graphs import compensate_graph
+    return compensate_graph(variant, W, U, quantizers, blocksize, groupsize, static_groups,
+                            qparam_perm, flags, P=P, Z=Z, GH=GH)

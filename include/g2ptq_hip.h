@@ -1,0 +1,228 @@
+/*
+ * g2ptq_hip.h — C ABI of libg2ptq_hip.so, the MI355X (gfx950) implementation of
+ * the GPTQ / GPTAQ / G2PTQ per-layer quantization path.
+ *
+ * Conventions
+ *   - Every pointer argument is a device pointer owned by the caller unless the
+ *     comment says "host".  `stream` is a hipStream_t passed as void*.
+ *   - Calls are asynchronous on `stream` and allocate nothing; scratch memory
+ *     comes in through `ws` / `ws_bytes` (size it with the *_workspace query).
+ *   - Return value: 0 on success, < 0 on an argument / runtime error (see
+ *     g2ptq_status_string and g2ptq_last_error), never an exception.
+ *   - Numeric failures are reported through device-side `info` / `flags`
+ *     integers that the caller reads at its own synchronisation point.
+ *   - Matrices are row-major; "ld" is the leading dimension in elements.
+ *     bf16 data is passed as uint16_t bit patterns.
+ *
+ * Paths in comments are relative to the reference repository (G2PTQ/G2PTQ).
+ */
+#ifndef G2PTQ_HIP_H
+#define G2PTQ_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define G2PTQ_OK 0
+#define G2PTQ_ERR_ARG (-1)
+#define G2PTQ_ERR_HIP (-2)
+#define G2PTQ_ERR_WORKSPACE (-3)
+#define G2PTQ_ERR_UNSUPPORTED (-4)
+
+/* Device-side flag bits (OR-ed into an int32 the caller owns). */
+#define G2PTQ_FLAG_BAD_SCALE 1   /* a scale was <= 0 or NaN (quant_utils.py:432 assert) */
+#define G2PTQ_FLAG_NAN_OUTPUT 2  /* NaN in quantized weights (gptq_utils.py:346-350) */
+
+/* Compensation variants. */
+#define G2PTQ_VARIANT_GPTQ 0
+#define G2PTQ_VARIANT_GPTAQ 1
+#define G2PTQ_VARIANT_G2PTQ 2
+
+int g2ptq_abi_version(void);
+const char* g2ptq_status_string(int status);
+/* Detail message of the last failing call on the calling host thread. */
+const char* g2ptq_last_error(void);
+
+/* ------------------------------------------------------------------------
+ * Quantizer grid — utils/quant_utils.py
+ * ---------------------------------------------------------------------- */
+
+/* Per-row min/max → (scale, zero) of one quantization group per row.
+ * Replaces WeightQuantizer.find_params (utils/quant_utils.py:377-433, with
+ * _minmax/_params_from_range_* :47-68) for mse=False, hclip=False.
+ * x: rows × cols, ld ldx.  Writes scale[r*ldp], zero[r*ldp]. */
+int g2ptq_find_params(void* stream, const float* x, int64_t rows, int64_t cols, int64_t ldx,
+                      int bits, int sym, float* scale, float* zero, int64_t ldp, int* flags);
+
+/* MSE clip search of WeightQuantizer.find_params with mse=True
+ * (utils/quant_utils.py:406-425): grid × maxshrink² candidate ranges per row,
+ * error sum(|fq − x|^norm), first strict improvement wins. */
+int g2ptq_find_params_mse(void* stream, const float* x, int64_t rows, int64_t cols, int64_t ldx,
+                          int bits, int sym, float norm, int grid, float maxshrink,
+                          float* scale, float* zero, int64_t ldp, int* flags);
+
+/* Round-to-nearest fake quantization with per-row, per-group parameters.
+ * Replaces WeightQuantizer.fake_quantize (utils/quant_utils.py:435-459) and
+ * fake_quantize_grouped (gptq_utils/common_utils.py:33-44).
+ * Column c of row r uses scale[r*ldp + c/groupsize] (groupsize <= 0: column 0).
+ * q_out: dequantized values; int_out (nullable): integer codes as float. */
+int g2ptq_fake_quantize(void* stream, const float* x, int64_t rows, int64_t cols, int64_t ldx,
+                        int64_t groupsize, const float* scale, const float* zero, int64_t ldp,
+                        int bits, float* q_out, int64_t ldq, float* int_out, int64_t ldi,
+                        int* flags);
+
+/* ------------------------------------------------------------------------
+ * Hessian accumulation
+ * ---------------------------------------------------------------------- */
+
+/* Bytes of workspace needed by the *_update calls below for T tokens of C
+ * features (kind: 0 Hessian, 1 GPTAQ, 2 saliency-weighted). */
+int g2ptq_hessian_workspace(int64_t T, int64_t C, int kind, size_t* bytes);
+
+/* H = beta·H + alpha·XᵀX (H symmetric C×C fp32, both triangles written).
+ * X: T × C bf16 (ld ldx).  Replaces GPTQ.add_batch's update
+ * (gptq_utils/gptq_utils.py:123-126; alpha = 2/n_new, beta = n_old/n_new). */
+int g2ptq_hessian_update(void* stream, const uint16_t* X, int64_t T, int64_t C, int64_t ldx,
+                         float alpha, float beta, float* H, int64_t ldh, void* ws, size_t ws_bytes);
+
+/* GPTAQ: H = beta·H + alpha·XᵀX and Dx = beta·Dx + alpha·(X_fp − X)ᵀX, with
+ * Dx[i][j] = Σ_t (x_fp − x)[t,i]·x[t,j].  Replaces GPTAQ.add_batch
+ * (gptq_utils/gptaq_utils.py:130-148). */
+int g2ptq_gptaq_update(void* stream, const uint16_t* X, const uint16_t* Xfp, int64_t T, int64_t C,
+                       int64_t ldx, int64_t ldxf, float alpha, float beta, float* H, float* Dx,
+                       int64_t ld, void* ws, size_t ws_bytes);
+
+/* Saliency-weighted Hessians for G groups:
+ *   H[g] = beta·H[g] + alpha·Σ_t S[t,g]·x_t x_tᵀ   (H: G × C × C, stride sH)
+ *   act  = act_beta·act + act_alpha·Σ_t x_t²       (act: C, nullable)
+ * Replaces G2PTQ.add_batch (gptq_utils/g2ptq_utils.py:182-201) and
+ * GPTQGuided.add_batch (gptq_utils/gptq_guided_utils.py:59-81).
+ * S: T × G fp32 (ld lds). */
+int g2ptq_weighted_hessian_update(void* stream, const uint16_t* X, int64_t T, int64_t C,
+                                  int64_t ldx, const float* S, int64_t G, int64_t lds,
+                                  float alpha, float beta, float* H, int64_t ldh, int64_t sH,
+                                  float* act, float act_alpha, float act_beta,
+                                  void* ws, size_t ws_bytes);
+
+/* ------------------------------------------------------------------------
+ * Hessian preparation and factor
+ * ---------------------------------------------------------------------- */
+
+/* In place on H (B × C × C) and W (B × R × C): an all-zero H[b] becomes the
+ * identity, a zero diagonal entry d becomes 1 and column d of W[b] (and of
+ * Dx[b], nullable) is zeroed; where H[b] was all zero, Grad[b] (B × Rg × C,
+ * nullable) is zeroed.  Replaces gptq_utils/gptq_utils.py:272-277,
+ * gptaq_utils.py:302-308, g2ptq_utils.py:394-401. */
+int g2ptq_prepare_hessian(void* stream, float* H, int64_t B, int64_t C, float* W, int64_t R,
+                          float* Dx, float* Grad, int64_t Rg, void* ws, size_t ws_bytes);
+
+int g2ptq_factor_workspace(int64_t B, int64_t C, size_t* bytes);
+
+/* U[b] = upper Cholesky factor of (H[b] + p·mean(diag H[b])·I)⁻¹, i.e. the
+ * factor the reference computes as
+ *   chol(cholesky_inverse(chol(H + damp·I)), upper=True)
+ * (gptq_utils/gptq_utils.py:295-302), computed here as J·chol(J·A·J)⁻¹·J.
+ * Entries with skip[b] != 0 (nullable, device) are left untouched.
+ * info[b] (device): 0 ok, k > 0 leading minor k not positive definite,
+ * -1 NaN in the factor (the reference's retry triggers). */
+int g2ptq_inv_chol_upper(void* stream, const float* H, int64_t B, int64_t C, float percdamp,
+                         const int* skip, float* U, int* info, void* ws, size_t ws_bytes);
+
+/* ------------------------------------------------------------------------
+ * Compensation
+ * ---------------------------------------------------------------------- */
+
+/* One compensation block on the reference's transposed block layout
+ * (B, bs, R): the run_eager operators of gptq_utils/gptq_utils.py:67-90
+ * (variant 0), gptaq_utils.py:74-100 (variant 1, needs p and column_weight)
+ * and g2ptq_utils.py:97-126 (variant 2, needs z and ghinv; ghinv updated in
+ * place).  weight is overwritten by the dequantized block; int_weight and
+ * error receive codes and scaled errors; scale/zero are per element. */
+int g2ptq_block_sweep(void* stream, int variant, int64_t B, int64_t bs, int64_t R, int maxq,
+                      float* weight, const float* hinv, const float* p, const float* scale,
+                      const float* zero, const float* z, float* ghinv, float* column_weight,
+                      float* int_weight, float* error, int* flags);
+
+int g2ptq_compensate_workspace(int variant, int64_t B, int64_t R, int64_t C, int64_t blocksize,
+                               size_t* bytes);
+
+/* The lazy-batch loop of _run_compensation for one layer batch:
+ * gptq_utils/gptq_utils.py:165-232 (variant 0), gptaq_utils.py:193-261
+ * (variant 1), g2ptq_utils.py:252-347 (variant 2).
+ *   W   (B,R,C) fp32 in/out (block tails are applied in place, like the reference)
+ *   U   (B,C,C) upper factor;  P (B,C,C) GPTAQ only;  Z, GH (B,R,C) G2PTQ only (GH in/out)
+ *   Quantizer groups: groupsize g (-1: one group).  dynamic (static_groups == 0 and
+ *   g > 0): params of the group starting at column i are fitted on W[:, :, i:i+g]
+ *   when the loop reaches i (gptq_utils.py:194-205).  Otherwise scale_tab/zero_tab
+ *   must already hold every group's params and colgroup (C ints, nullable) maps
+ *   column → group (static groups with act-order: perm[c] // g).  mse_grid > 0 fits
+ *   dynamic groups with the MSE clip search (g2ptq_find_params_mse semantics).
+ *   scale_tab/zero_tab: ngroups × (B·R) fp32, group-major (row b·R + r of group g
+ *   at g·B·R + b·R + r), ngroups = 1 if g == -1 else ceil(C / g).
+ *   Q, Wint, Scale: (B,R,C) outputs (Wint and Scale nullable). */
+int g2ptq_compensate(void* stream, int variant, int64_t B, int64_t R, int64_t C,
+                     int64_t blocksize, float* W, const float* U, const float* P, const float* Z,
+                     float* GH, int bits, int sym, int64_t groupsize, int static_groups,
+                     int mse_grid, float mse_norm, float mse_maxshrink, const int* colgroup,
+                     float* scale_tab, float* zero_tab, float* Q, float* Wint, float* Scale,
+                     int* flags, void* ws, size_t ws_bytes);
+
+/* GPTAQ P = alpha·triu(Dx·Uᵀ, 1)·U for B layers (gptq_utils/gptaq_utils.py:349-352). */
+int g2ptq_gptaq_p(void* stream, const float* Dx, const float* U, int64_t B, int64_t C, float alpha,
+                  float* P, void* ws, size_t ws_bytes);
+
+/* G2PTQ trust region (gptq_utils/g2ptq_utils.py:459-476) for BG row groups of
+ * Rg rows: with A⁻¹ = UᵀU, GA = Grad·A⁻¹, E0 = Q0 − W0,
+ *   loss = |(E0⊙GA + E0²/2) / diag(A⁻¹)|,
+ *   c    = max(rowsum(Grad⊙GA) − GA²/diag(A⁻¹), 2α·loss, tiny),
+ *   beta = mean_j(1 − sqrt(max(1 − 2α·loss/c, 0)))  per row,
+ *   Z = beta·(Grad·Uᵀ),  GH = Z·U = beta·GA.
+ * enabled == 0 gives beta = 0 and Z = GH = 0.  beta: BG·Rg floats. */
+int g2ptq_trust_region(void* stream, const float* Grad, const float* U, const float* Q0,
+                       const float* W0, int64_t BG, int64_t Rg, int64_t C, float alpha,
+                       int enabled, float* beta, float* Z, float* GH, void* ws, size_t ws_bytes);
+
+int g2ptq_trust_region_workspace(int64_t BG, int64_t Rg, int64_t C, size_t* bytes);
+
+/* ------------------------------------------------------------------------
+ * Small device helpers used by the host classes
+ * ---------------------------------------------------------------------- */
+
+/* act-order permutation: perm = argsort(mean_b diag(H[b]) or key, descending,
+ * ties by index) (gptq_utils/gptq_utils.py:279-282, g2ptq_utils.py:417-419).
+ * key_mode 0: key[c] = mean_b H[b][c][c] (H: B × C × C);  key_mode 1: key[c] =
+ * mean_b A[b][c] (A: B × C, e.g. act_square).  perm, invperm: C int32 (device). */
+int g2ptq_act_order(void* stream, const float* src, int64_t B, int64_t C, int key_mode, int* perm,
+                    int* invperm, void* ws, size_t ws_bytes);
+
+/* out[b][r][c] = in[b][r][cols[c]] for a (B·R) × C matrix (column gather). */
+int g2ptq_permute_cols(void* stream, const float* in, float* out, int64_t rows, int64_t C,
+                       const int* cols);
+
+/* out[b][i][j] = in[b][perm[i]][perm[j]] (symmetric permutation, B × C × C). */
+int g2ptq_permute_sym(void* stream, const float* in, float* out, int64_t B, int64_t C,
+                      const int* perm);
+
+/* Cast fp32 → bf16/fp16 (dtype 0 bf16, 1 fp16, 2 fp32 copy) with a NaN check
+ * (sets G2PTQ_FLAG_NAN_OUTPUT), the write-back of gptq_utils.py:346-353. */
+int g2ptq_cast_check(void* stream, const float* in, void* out, int64_t n, int dtype, int* flags);
+
+/* out fp32 = in (bf16/fp16/fp32 by dtype code as above), n elements. */
+int g2ptq_to_f32(void* stream, const void* in, float* out, int64_t n, int dtype);
+
+/* Generic batched fp32 GEMM (MFMA): D = alpha·A·op(B) + beta·C for `batch`
+ * matrices; A row-major M×K, B row-major K×N (b_trans = 0) or N×K
+ * (b_trans = 1).  Exported for the host classes' small products. */
+int g2ptq_gemm_f32(void* stream, int64_t M, int64_t N, int64_t K, int64_t batch, const float* A,
+                   int64_t lda, int64_t sA, const float* B, int64_t ldb, int64_t sB, int b_trans,
+                   const float* C, int64_t ldc, int64_t sC, float* D, int64_t ldd, int64_t sD,
+                   float alpha, float beta);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* G2PTQ_HIP_H */
