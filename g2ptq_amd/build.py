@@ -24,13 +24,19 @@ FLAGS = [
 ]
 
 
+# Per-file extra flags.  The quantize / sweep kernels must round every product
+# and sum separately (the reference's torch ops never fuse); the flag also
+# covers the HIP header's __f*_rn helpers, which a source-level pragma cannot.
+EXTRA = {"quant.hip": ["-ffp-contract=off"]}
+
+
 def sources():
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 
 def _compile(src):
     obj = os.path.join(BUILD, os.path.basename(src)[:-4] + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
+    cmd = [HIPCC, *FLAGS, *EXTRA.get(os.path.basename(src), []), "-c", src, "-o", obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     noise = "'-packed-fp32-ops' is not a recognized feature"
     err = "\n".join(l for l in res.stderr.splitlines() if noise not in l)

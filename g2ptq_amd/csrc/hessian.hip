@@ -101,14 +101,16 @@ __device__ __forceinline__ void tri_tile(int64_t idx, int64_t nt, int64_t& I, in
   J = i + idx;
 }
 
-// MODE 0: H (upper tiles, mirrored).  MODE 1: GPTAQ, all tiles: Dx and, for
-// I <= J, H.  MODE 2: saliency weighted, upper tiles, group g = blockIdx.y,
+// MODE 0: H (upper tiles, mirrored).  MODE 1: GPTAQ, all tiles: Dx from the
+// exact fp32 difference x_fp − x split into bf16 hi + lo operands (two MFMAs),
+// and, for I <= J, H.  MODE 2: saliency weighted, upper tiles, group g = blockIdx.y,
 // scaled operand split into bf16 hi + lo parts (two MFMAs per step).
 template <int MODE>
 __global__ __launch_bounds__(256) void gram_kernel(GramArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t As[GT * GP];
   __shared__ __attribute__((aligned(16))) uint16_t Bs[GT * GP];
   __shared__ __attribute__((aligned(16))) uint16_t A2s[(MODE == 0) ? 8 : GT * GP];
+  __shared__ __attribute__((aligned(16))) uint16_t A3s[(MODE == 1) ? GT * GP : 8];
 
   int64_t I, J;
   if (MODE == 1) {
@@ -170,10 +172,24 @@ __global__ __launch_bounds__(256) void gram_kernel(GramArgs a) {
         *pa = *reinterpret_cast<const uint4*>(hi);
         *reinterpret_cast<uint4*>(A2s + row * GP + col8) = *reinterpret_cast<const uint4*>(lo);
         *pb = rb[i];
+      } else if (MODE == 1) {
+        // d = x_fp - x exactly in fp32, split into bf16 hi + lo.
+        const uint16_t* xs = reinterpret_cast<const uint16_t*>(&ra[i]);
+        const uint16_t* fs = reinterpret_cast<const uint16_t*>(&rf[i]);
+        uint16_t hi[8], lo[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float d = bf16_to_f32(fs[e]) - bf16_to_f32(xs[e]);
+          hi[e] = f32_to_bf16_rne(d);
+          lo[e] = f32_to_bf16_rne(d - bf16_to_f32(hi[e]));
+        }
+        *pa = ra[i];
+        *pb = rb[i];
+        *reinterpret_cast<uint4*>(A2s + row * GP + col8) = *reinterpret_cast<const uint4*>(hi);
+        *reinterpret_cast<uint4*>(A3s + row * GP + col8) = *reinterpret_cast<const uint4*>(lo);
       } else {
         *pa = ra[i];
-        if (!diag_tile || MODE == 1) *pb = rb[i];
-        if (MODE == 1) *reinterpret_cast<uint4*>(A2s + row * GP + col8) = rf[i];
+        if (!diag_tile) *pb = rb[i];
       }
     }
   };
@@ -201,13 +217,14 @@ __global__ __launch_bounds__(256) void gram_kernel(GramArgs a) {
     if (kt + 1 < nk) gload((int64_t)(kt + 1) * GK);
 #pragma unroll
     for (int ks = 0; ks < GK / 16; ++ks) {
-      bf16x8 av[2], bv[2], fv[2];
+      bf16x8 av[2], bv[2], fv[2], lv[2];
       const int kof = ks * 16 + (lane >> 5) * 8;
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
         const int row = wm * 64 + mt * 32 + (lane & 31);
         av[mt] = *reinterpret_cast<const bf16x8*>(As + row * GP + kof);
         if (MODE != 0) fv[mt] = *reinterpret_cast<const bf16x8*>(A2s + row * GP + kof);
+        if (MODE == 1) lv[mt] = *reinterpret_cast<const bf16x8*>(A3s + row * GP + kof);
       }
 #pragma unroll
       for (int nt2 = 0; nt2 < 2; ++nt2) {
@@ -223,6 +240,9 @@ __global__ __launch_bounds__(256) void gram_kernel(GramArgs a) {
           if (MODE != 0)
             acc2[mt][nt2] =
                 __builtin_amdgcn_mfma_f32_32x32x16_bf16(fv[mt], bv[nt2], acc2[mt][nt2], 0, 0, 0);
+          if (MODE == 1)
+            acc2[mt][nt2] =
+                __builtin_amdgcn_mfma_f32_32x32x16_bf16(lv[mt], bv[nt2], acc2[mt][nt2], 0, 0, 0);
         }
     }
   }
@@ -240,7 +260,7 @@ __global__ __launch_bounds__(256) void gram_kernel(GramArgs a) {
         const int64_t j = j0 + wn * 64 + nt2 * 32 + (lane & 31);
         if (i >= a.C || j >= a.C) continue;
         if (MODE == 1) {
-          const float d = acc2[mt][nt2][v] - acc[mt][nt2][v];
+          const float d = acc2[mt][nt2][v];
           float* pd = a.D + i * a.ldd + j;
           *pd = (a.beta != 0.f ? a.beta * *pd : 0.f) + a.alpha * d;
           if (I > J) continue;

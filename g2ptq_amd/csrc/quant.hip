@@ -5,8 +5,12 @@
 //   deq = s * (q - z)
 //   err = (x - deq [- gh]) / U_jj                       IEEE div
 //   w_k = w_k - round(U_jk * err)                       no FMA contraction
-// which is what torch's elementwise ops and its K=1 baddbmm compute.
+// which is what torch's elementwise ops and its K=1 baddbmm compute.  hipcc
+// contracts a*b+c into FMA by default, even across the __f*_rn helpers of the
+// HIP headers, so this translation unit is built with -ffp-contract=off.
 #include "sweep.hpp"
+
+#pragma clang fp contract(off)
 
 namespace g2ptq {
 namespace {
