@@ -29,6 +29,10 @@ SIGNATURES = {
     "g2ptq_fake_quantize": [_p, _p, _i64, _i64, _i64, _i64, _p, _p, _i64, _i32, _p, _i64, _p, _i64, _p],
     "g2ptq_hessian_workspace": [_i64, _i64, _i32, _szp],
     "g2ptq_hessian_update": [_p, _p, _i64, _i64, _i64, _f32, _f32, _p, _i64, _p, _sz],
+    "g2ptq_hessian_stage_rows": [_i64, ctypes.POINTER(ctypes.c_int64)],
+    "g2ptq_hessian_stage": [_p, _p, _i64, _i64, _i64, _p, _i64, _i64],
+    "g2ptq_hessian_gram_workspace": [_i64, _i64, _szp],
+    "g2ptq_hessian_gram": [_p, _p, _i64, _i64, _i64, _f32, _f32, _p, _i64, _p, _sz],
     "g2ptq_gptaq_update": [_p, _p, _p, _i64, _i64, _i64, _i64, _f32, _f32, _p, _p, _i64, _p, _sz],
     "g2ptq_weighted_hessian_update": [_p, _p, _i64, _i64, _i64, _p, _i64, _i64, _f32, _f32, _p, _i64,
                                       _i64, _p, _f32, _f32, _p, _sz],
@@ -97,6 +101,12 @@ def call(name, *args):
 
 def query_size(name, *args):
     out = ctypes.c_size_t(0)
+    call(name, *args, ctypes.byref(out))
+    return out.value
+
+
+def query_size_i64(name, *args):
+    out = ctypes.c_int64(0)
     call(name, *args, ctypes.byref(out))
     return out.value
 

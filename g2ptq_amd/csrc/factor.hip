@@ -68,38 +68,101 @@ __global__ void reverse_damp_kernel(const float* __restrict__ H, int64_t C, floa
 }
 
 // Cholesky + in-place inverse of the nbk×nbk diagonal block at (k, k).
+//
+// Right-looking, register resident: the 128×128 block is split over a 16×16
+// thread grid, each thread holding an 8×8 tile of L and of X = L⁻¹.  At step j
+// the owners of column j of L and of row j of X publish them through LDS
+// (double-buffered, one barrier per step); every thread then finishes the
+// pivot (sqrt, scale by its reciprocal), and applies the rank-1 updates of
+// the Cholesky trailing block and of the forward elimination of L·X = I to its
+// own tile.
 __global__ __launch_bounds__(256) void potrf_diag_kernel(float* WA, int64_t C, int64_t k, int nbk,
                                                          int* st, int* info) {
   const int64_t b = blockIdx.x;
   if (st[b]) return;
-  __shared__ float L[NB][NB + 1];
-  __shared__ float X[NB][NB + 1];
-  __shared__ int fail;
+  __shared__ float colL[2][NB];
+  __shared__ float rowX[2][NB];
   float* Wb = WA + b * C * C + k * C + k;
   const int tid = threadIdx.x;
-  for (int idx = tid; idx < nbk * nbk; idx += 256) {
-    const int i = idx / nbk, j = idx % nbk;
-    L[i][j] = (j <= i) ? Wb[(int64_t)i * C + j] : 0.f;
-  }
-  if (tid == 0) fail = 0;
-  __syncthreads();
+  const int tx = tid & 15, ty = tid >> 4;
+  const int i0 = ty * 8, c0 = tx * 8;
+  float l[8][8], x[8][8];
+#pragma unroll
+  for (int r = 0; r < 8; ++r)
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const int i = i0 + r, kk = c0 + c;
+      l[r][c] = (kk <= i && i < nbk) ? Wb[(int64_t)i * C + kk] : 0.f;
+      x[r][c] = (i == kk) ? 1.f : 0.f;
+    }
+  int fail = 0;
   for (int j = 0; j < nbk; ++j) {
-    if (tid == 0) {
-      const float d = L[j][j];
-      if (!(d > 0.f)) fail = j + 1;  // also catches NaN
-      else L[j][j] = __fsqrt_rn(d);
+    const int buf = j & 1;
+    const int cj = j & 7, tj = j >> 3;
+    // Register tiles are indexed with compile-time indices only (selects), so
+    // they stay in VGPRs.
+    if (tx == tj) {
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        float v = 0.f;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) v = (c == cj) ? l[r][c] : v;
+        colL[buf][i0 + r] = v;
+      }
+    }
+    if (ty == tj) {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        float v = 0.f;
+#pragma unroll
+        for (int r = 0; r < 8; ++r) v = (r == cj) ? x[r][c] : v;
+        rowX[buf][c0 + c] = v;
+      }
     }
     __syncthreads();
-    if (fail) break;
-    const float dj = L[j][j];
-    for (int i = j + 1 + tid; i < nbk; i += 256) L[i][j] = __fdiv_rn(L[i][j], dj);
-    __syncthreads();
-    const int m = nbk - j - 1;
-    for (int idx = tid; idx < m * m; idx += 256) {
-      const int ii = idx / m, kk = idx % m;
-      if (kk <= ii) L[j + 1 + ii][j + 1 + kk] -= L[j + 1 + ii][j] * L[j + 1 + kk][j];
+    const float djj = colL[buf][j];
+    if (!(djj > 0.f)) {  // also catches NaN; every thread sees the same value
+      fail = j + 1;
+      break;
     }
-    __syncthreads();
+    const float d = __fsqrt_rn(djj);
+    const float rd = 1.f / d;
+    // Unconditional LDS reads (rows above the pivot hold stale values that the
+    // selects discard), so no divergent branch separates the loads.
+    float li[8], lk[8], xr[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const float v = colL[buf][i0 + r];
+      li[r] = (i0 + r > j) ? v * rd : 0.f;
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const float v = colL[buf][c0 + c];
+      const float xv = rowX[buf][c0 + c];
+      lk[c] = (c0 + c > j) ? v * rd : 0.f;
+      xr[c] = (c0 + c <= j) ? xv * rd : 0.f;
+    }
+    // li[r] = 0 for rows i <= j and lk[c] = 0 for columns <= j, so the rank-1
+    // updates need no masks; only the strict upper triangle of the L tile is
+    // written with values nobody reads.
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const bool diag_row = (i0 + r == j);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        l[r][c] -= li[r] * lk[c];
+        x[r][c] = diag_row ? xr[c] : x[r][c] - li[r] * xr[c];
+      }
+    }
+    if (tx == tj) {
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        const float v = (i0 + r == j) ? d : li[r];
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+          if (c == cj) l[r][c] = v;
+      }
+    }
   }
   if (fail) {
     if (tid == 0) {
@@ -108,21 +171,13 @@ __global__ __launch_bounds__(256) void potrf_diag_kernel(float* WA, int64_t C, i
     }
     return;
   }
-  // Column c of X = L⁻¹ by forward substitution (one thread per column).
-  if (tid < nbk) {
-    const int c = tid;
-    for (int i = 0; i < c; ++i) X[i][c] = 0.f;
-    for (int i = c; i < nbk; ++i) {
-      float s = (i == c) ? 1.f : 0.f;
-      for (int kk = c; kk < i; ++kk) s -= L[i][kk] * X[kk][c];
-      X[i][c] = __fdiv_rn(s, L[i][i]);
+#pragma unroll
+  for (int r = 0; r < 8; ++r)
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const int i = i0 + r, kk = c0 + c;
+      if (i < nbk && kk < nbk) Wb[(int64_t)i * C + kk] = (kk <= i) ? x[r][c] : 0.f;
     }
-  }
-  __syncthreads();
-  for (int idx = tid; idx < nbk * nbk; idx += 256) {
-    const int i = idx / nbk, j = idx % nbk;
-    Wb[(int64_t)i * C + j] = (j <= i) ? X[i][j] : 0.f;
-  }
 }
 
 // U[i][j] = X[C-1-i][C-1-j] for i <= j, 0 below; NaN → info = -1.

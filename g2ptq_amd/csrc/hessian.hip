@@ -310,28 +310,12 @@ using namespace g2ptq;
 
 extern "C" int g2ptq_hessian_workspace(int64_t T, int64_t C, int kind, size_t* bytes) {
   G2PTQ_CHECK(bytes != nullptr, "hessian_workspace: null out");
+  if (kind == 0) {
+    *bytes = gram_update_ws_bytes(T, C);
+    return G2PTQ_OK;
+  }
   const HessWs w = hess_ws(T, C, kind, 8);
   *bytes = w.xt_bytes + w.ft_bytes + w.st_bytes;
-  return G2PTQ_OK;
-}
-
-extern "C" int g2ptq_hessian_update(void* stream, const uint16_t* X, int64_t T, int64_t C,
-                                    int64_t ldx, float alpha, float beta, float* H, int64_t ldh,
-                                    void* ws, size_t ws_bytes) {
-  G2PTQ_TRY(check_sizes(T, C));
-  G2PTQ_CHECK(H != nullptr && (X != nullptr || T == 0), "hessian_update: null pointer");
-  const HessWs w = hess_ws(T, C, 0, 0);
-  G2PTQ_CHECK(ws_bytes >= w.xt_bytes && ws != nullptr, "hessian_update: workspace %zu < %zu",
-              ws_bytes, w.xt_bytes);
-  hipStream_t st = as_stream(stream);
-  uint16_t* XT = static_cast<uint16_t*>(ws);
-  if (w.Tp > 0) G2PTQ_TRY(transpose_into(st, X, T, C, ldx, XT, w));
-  GramArgs a{};
-  a.XT = XT; a.Tp = w.Tp; a.C = C; a.nt = w.Cp / GT;
-  a.alpha = alpha; a.beta = beta; a.H = H; a.ldh = ldh;
-  const int64_t tiles = a.nt * (a.nt + 1) / 2;
-  hipLaunchKernelGGL(gram_kernel<0>, dim3((unsigned)tiles), dim3(256), 0, st, a);
-  G2PTQ_LAUNCHED();
   return G2PTQ_OK;
 }
 

@@ -170,16 +170,27 @@ __global__ __launch_bounds__(256) void fake_quantize_kernel(
 // Fused block sweep.
 //
 // One wave64 owns 64 rows of one layer (lane = row) for a block of n <= 128
-// columns.  The block is walked in panels of PW columns whose values live in
-// VGPRs; updates from earlier panels are replayed from the per-lane error
-// history kept in LDS, in increasing column order, so every element sees the
-// reference's exact sequence of updates.  U (and P) rows are wave-uniform and
-// read through the scalar path.
+// columns.  The block's upper-triangular U (and P) is staged once into LDS in
+// packed row order and read with wave-uniform (broadcast) LDS loads.  The
+// block is walked in panels of PW columns whose values live in VGPRs; updates
+// from earlier panels are replayed from the per-lane error history kept in
+// LDS, in increasing column order, so every element sees the reference's
+// exact sequence of updates.  VEC: every per-row operand is contiguous along
+// columns and 16-byte aligned (the native (B, R, C) layout), so panel loads
+// and result stores move 4 columns per instruction.
 // ---------------------------------------------------------------------------
-template <int V, int PW>
+constexpr int kTri = kMaxBlock * (kMaxBlock + 1) / 2;
+
+// Packed upper triangle: element (j, k >= j) lives at tri_base(j, n) + k.
+__device__ __forceinline__ int tri_base(int j, int n) { return j * n - (j * (j - 1)) / 2 - j; }
+
+template <int V, int PW, bool VEC, bool FULL>
 __global__ __launch_bounds__(64) void sweep_kernel(SweepArgs a) {
+  __shared__ float Us[kTri];
+  __shared__ float Ps[(V == 1) ? kTri : 1];
   __shared__ float e_s[kMaxBlock * 64];
   __shared__ float t_s[(V == 1) ? kMaxBlock * 64 : 1];
+  __shared__ float z_s[(V == 2) ? kMaxBlock * 64 : 1];
 
   const int lane = threadIdx.x;
   const int64_t b = blockIdx.y;
@@ -189,8 +200,34 @@ __global__ __launch_bounds__(64) void sweep_kernel(SweepArgs a) {
   const int n = a.n;
   const float minq = (float)(-(a.maxq + 1)), fmaxq = (float)a.maxq;
 
-  const float* __restrict__ U = a.U + b * a.ub;
-  const float* __restrict__ P = (V == 1) ? a.P + b * a.ub : nullptr;
+  {
+    // Stage the upper triangle: 8 independent loads in flight per lane per batch.
+    const float* U = a.U + b * a.ub;
+    const float* P = (V == 1) ? a.P + b * a.ub : nullptr;
+    const int nn = n * n;
+    for (int base = 0; base < nn; base += 64 * 8) {
+      float uv[8], pv[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int idx = base + q * 64 + lane;
+        const int j = idx / n, k = idx - j * n;
+        const bool need = idx < nn && k >= j;
+        uv[q] = need ? U[(int64_t)j * a.uj + k] : 0.f;
+        if (V == 1) pv[q] = need ? P[(int64_t)j * a.uj + k] : 0.f;
+      }
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int idx = base + q * 64 + lane;
+        const int j = idx / n, k = idx - j * n;
+        if (idx < nn && k >= j) {
+          Us[tri_base(j, n) + k] = uv[q];
+          if (V == 1) Ps[tri_base(j, n) + k] = pv[q];
+        }
+      }
+    }
+  }
+  __syncthreads();
+
   const float* Win = a.W + b * a.wb + r * a.wr;
   const float* Sp = a.S + b * a.sb + r * a.sr;
   const float* Zp = a.Z0 + b * a.sb + r * a.sr;
@@ -207,24 +244,51 @@ __global__ __launch_bounds__(64) void sweep_kernel(SweepArgs a) {
   float last_x = 0.f;
 
   for (int p0 = 0; p0 < n; p0 += PW) {
-    const int np = min(PW, n - p0);
-    float w[PW], gh[PW];
+    const int np = FULL ? PW : min(PW, n - p0);
+    // ---- panel inputs, all issued before any store of this panel -------------
+    float w[PW], gh[PW], sv[PW], zv[PW], zg[PW];
 #pragma unroll
-    for (int kk = 0; kk < PW; ++kk) {
-      w[kk] = (kk < np) ? Win[(int64_t)(p0 + kk) * a.wc] : 0.f;
-      if (V == 2) gh[kk] = (kk < np) ? GH[(int64_t)(p0 + kk) * a.gc] : 0.f;
+    for (int jj = 0; jj < PW; ++jj) {
+      const bool in = FULL || jj < np;
+      const int j = p0 + jj;
+      int gidx = 0;
+      if (a.colgroup) gidx = a.colgroup[in ? j : 0];
+      else if (a.gsize > 0) gidx = (int)((int)a.col0 + j) / (int)a.gsize;
+      if (!in) gidx = 0;
+      sv[jj] = Sp[(int64_t)gidx * a.sg];
+      zv[jj] = Zp[(int64_t)gidx * a.sg];
+      if (V == 2) zg[jj] = Zg[(int64_t)(in ? j : 0) * a.zc];
     }
-    // Replay updates of the columns already swept in earlier panels.
+    if (VEC) {
+#pragma unroll
+      for (int kk = 0; kk < PW; kk += 4) {
+        const int off = (FULL || kk < np) ? p0 + kk : 0;
+        const float4 v = *reinterpret_cast<const float4*>(Win + off);
+        w[kk] = v.x; w[kk + 1] = v.y; w[kk + 2] = v.z; w[kk + 3] = v.w;
+        if (V == 2) {
+          const float4 g4 = *reinterpret_cast<const float4*>(GH + off);
+          gh[kk] = g4.x; gh[kk + 1] = g4.y; gh[kk + 2] = g4.z; gh[kk + 3] = g4.w;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int kk = 0; kk < PW; ++kk) {
+        const int c = (FULL || kk < np) ? p0 + kk : 0;
+        w[kk] = Win[(int64_t)c * a.wc];
+        if (V == 2) gh[kk] = GH[(int64_t)c * a.gc];
+      }
+    }
+    // ---- replay updates of the columns swept in earlier panels (LDS only) ---
     for (int j = 0; j < p0; ++j) {
       const float e = e_s[j * 64 + lane];
       float t = 0.f, zj = 0.f;
       if (V == 1) t = t_s[j * 64 + lane];
-      if (V == 2) zj = Zg[(int64_t)j * a.zc];
-      const float* Uj = U + (int64_t)j * a.uj + p0;
-      const float* Pj = (V == 1) ? P + (int64_t)j * a.uj + p0 : nullptr;
+      if (V == 2) zj = z_s[j * 64 + lane];
+      const float* Uj = Us + tri_base(j, n) + p0;
+      const float* Pj = (V == 1) ? Ps + tri_base(j, n) + p0 : nullptr;
 #pragma unroll
       for (int kk = 0; kk < PW; ++kk) {
-        if (kk < np) {
+        if (FULL || kk < np) {
           const float u = Uj[kk];
           if (V == 0) {
             w[kk] = __fsub_rn(w[kk], __fmul_rn(u, e));
@@ -237,46 +301,39 @@ __global__ __launch_bounds__(64) void sweep_kernel(SweepArgs a) {
         }
       }
     }
-    // Sweep this panel column by column.
+    // ---- sweep this panel column by column (registers + LDS only) -----------
+    float qb[PW], ib[PW], gb[PW];
 #pragma unroll
     for (int jj = 0; jj < PW; ++jj) {
-      if (jj < np) {
+      if (FULL || jj < np) {
         const int j = p0 + jj;
         const float x = w[jj];
-        const int64_t gidx = a.colgroup ? a.colgroup[j]
-                                        : (a.gsize > 0 ? (int64_t)(a.col0 + j) / a.gsize : 0);
-        const float s = Sp[gidx * a.sg];
-        const float z0 = Zp[gidx * a.sg];
+        const float s = sv[jj];
+        const float z0 = zv[jj];
         const float q = clamp_nan(__fadd_rn(rintf(__fdiv_rn(x, s)), z0), minq, fmaxq);
         const float deq = __fmul_rn(s, __fsub_rn(q, z0));
-        const float d = U[(int64_t)j * a.uj + j];
+        const float d = Us[tri_base(j, n) + j];
         float err;
         float zj = 0.f;
         if (V == 2) {
           err = __fdiv_rn(__fsub_rn(__fsub_rn(x, deq), gh[jj]), d);
-          zj = Zg[(int64_t)j * a.zc];
+          zj = zg[jj];
+          z_s[j * 64 + lane] = zj;
+          gb[jj] = gh[jj];
         } else {
           err = __fdiv_rn(__fsub_rn(x, deq), d);
         }
         bad |= !(s > 0.f);
-        if (act) {
-          Qo[(int64_t)j * a.qc] = deq;
-          if (Io) Io[(int64_t)j * a.ic] = q;
-          if (Eo) Eo[(int64_t)j * a.ec] = err;
-          if (So) So[(int64_t)j * a.cc] = s;
-          if (V == 2) {
-            if (GHo) GHo[(int64_t)j * a.gc] = gh[jj];
-            if (E2) E2[(int64_t)j * a.e2c] = __fsub_rn(err, __fmul_rn(zj, (float)(a.dist0 - j)));
-          }
-        }
+        qb[jj] = deq;
+        ib[jj] = q;
         e_s[j * 64 + lane] = err;
         if (V == 1) t_s[j * 64 + lane] = x;
         last_x = x;
-        const float* Uj = U + (int64_t)j * a.uj + p0;
-        const float* Pj = (V == 1) ? P + (int64_t)j * a.uj + p0 : nullptr;
+        const float* Uj = Us + tri_base(j, n) + p0;
+        const float* Pj = (V == 1) ? Ps + tri_base(j, n) + p0 : nullptr;
 #pragma unroll
         for (int kk = jj + 1; kk < PW; ++kk) {
-          if (kk < np) {
+          if (FULL || kk < np) {
             const float u = Uj[kk];
             if (V == 0) {
               w[kk] = __fsub_rn(w[kk], __fmul_rn(u, err));
@@ -290,9 +347,73 @@ __global__ __launch_bounds__(64) void sweep_kernel(SweepArgs a) {
         }
       }
     }
+    // ---- panel outputs ------------------------------------------------------
+    if (act) {
+      if (VEC) {
+#pragma unroll
+        for (int kk = 0; kk < PW; kk += 4) {
+          if (FULL || kk < np) {
+            const int c = p0 + kk;
+            *reinterpret_cast<float4*>(Qo + c) = make_float4(qb[kk], qb[kk + 1], qb[kk + 2], qb[kk + 3]);
+            if (Io) *reinterpret_cast<float4*>(Io + c) = make_float4(ib[kk], ib[kk + 1], ib[kk + 2], ib[kk + 3]);
+            if (So) *reinterpret_cast<float4*>(So + c) = make_float4(sv[kk], sv[kk + 1], sv[kk + 2], sv[kk + 3]);
+            float ev[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) ev[q] = e_s[(c + q) * 64 + lane];
+            if (Eo) *reinterpret_cast<float4*>(Eo + c) = make_float4(ev[0], ev[1], ev[2], ev[3]);
+            if (V == 2 && E2) {
+              float e2[4];
+#pragma unroll
+              for (int q = 0; q < 4; ++q)
+                e2[q] = __fsub_rn(ev[q], __fmul_rn(zg[kk + q], (float)(a.dist0 - (c + q))));
+              *reinterpret_cast<float4*>(E2 + c) = make_float4(e2[0], e2[1], e2[2], e2[3]);
+            }
+          }
+        }
+      } else {
+#pragma unroll
+        for (int jj = 0; jj < PW; ++jj) {
+          if (FULL || jj < np) {
+            const int j = p0 + jj;
+            const float ev = e_s[j * 64 + lane];
+            Qo[(int64_t)j * a.qc] = qb[jj];
+            if (Io) Io[(int64_t)j * a.ic] = ib[jj];
+            if (Eo) Eo[(int64_t)j * a.ec] = ev;
+            if (So) So[(int64_t)j * a.cc] = sv[jj];
+            if (V == 2 && E2)
+              E2[(int64_t)j * a.e2c] = __fsub_rn(ev, __fmul_rn(zg[jj], (float)(a.dist0 - j)));
+            if (V == 2 && GHo) GHo[(int64_t)j * a.gc] = gb[jj];
+          }
+        }
+      }
+    }
   }
   if (V == 1 && a.CW && act) a.CW[b * a.cwb + r * a.cwr] = last_x;
   if (bad && act && a.flags) atomicOr(a.flags, FLAG_BAD_SCALE);
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// Whether every per-row operand is column-contiguous with 16-byte aligned rows.
+bool sweep_vec_ok(const SweepArgs& a) {
+  if (a.n % 32 != 0) return false;
+  auto ok = [](const void* p, int64_t sb, int64_t sr, int64_t sc) {
+    return p == nullptr || (sc == 1 && sr % 4 == 0 && sb % 4 == 0 && aligned16(p));
+  };
+  return ok(a.W, a.wb, a.wr, a.wc) && ok(a.Q, a.qb, a.qr, a.qc) && ok(a.I, a.ib, a.ir, a.ic) &&
+         ok(a.E, a.eb, a.er, a.ec) && ok(a.Sc, a.cb, a.cr, a.cc) &&
+         ok(a.E2, a.e2b, a.e2r, a.e2c) && ok(a.GH, a.gb, a.gr, a.gc) && a.GHout == nullptr;
+}
+
+template <int V>
+void launch_variant(hipStream_t stream, const SweepArgs& a, dim3 grid, bool vec) {
+  const bool full = (a.n % 32) == 0;
+  if (vec && full)
+    hipLaunchKernelGGL((sweep_kernel<V, 32, true, true>), grid, dim3(64), 0, stream, a);
+  else if (full)
+    hipLaunchKernelGGL((sweep_kernel<V, 32, false, true>), grid, dim3(64), 0, stream, a);
+  else
+    hipLaunchKernelGGL((sweep_kernel<V, 32, false, false>), grid, dim3(64), 0, stream, a);
 }
 
 }  // namespace
@@ -303,17 +424,18 @@ int launch_sweep(hipStream_t stream, int variant, const SweepArgs& a, int64_t B)
   if (a.R <= 0 || B <= 0) return G2PTQ_OK;
   G2PTQ_CHECK(B < 65536, "block sweep: batch too large");
   dim3 grid((unsigned)cdiv(a.R, 64), (unsigned)B);
+  const bool vec = sweep_vec_ok(a);
   switch (variant) {
     case G2PTQ_VARIANT_GPTQ:
-      hipLaunchKernelGGL((sweep_kernel<0, 32>), grid, dim3(64), 0, stream, a);
+      launch_variant<0>(stream, a, grid, vec);
       break;
     case G2PTQ_VARIANT_GPTAQ:
       G2PTQ_CHECK(a.P != nullptr, "GPTAQ sweep needs P");
-      hipLaunchKernelGGL((sweep_kernel<1, 32>), grid, dim3(64), 0, stream, a);
+      launch_variant<1>(stream, a, grid, vec);
       break;
     case G2PTQ_VARIANT_G2PTQ:
       G2PTQ_CHECK(a.Zg != nullptr && a.GH != nullptr, "G2PTQ sweep needs z and ghinv");
-      hipLaunchKernelGGL((sweep_kernel<2, 32>), grid, dim3(64), 0, stream, a);
+      launch_variant<2>(stream, a, grid, vec);
       break;
     default:
       G2PTQ_CHECK(false, "unknown compensation variant %d", variant);

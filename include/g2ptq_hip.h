@@ -88,6 +88,22 @@ int g2ptq_hessian_workspace(int64_t T, int64_t C, int kind, size_t* bytes);
 int g2ptq_hessian_update(void* stream, const uint16_t* X, int64_t T, int64_t C, int64_t ldx,
                          float alpha, float beta, float* H, int64_t ldh, void* ws, size_t ws_bytes);
 
+/* Staged accumulation: the two halves of g2ptq_hessian_update, so a caller
+ * can gather several calibration batches (add_batch payloads) into one Gram
+ * launch.  g2ptq_hessian_stage writes Xᵀ of a T × C batch into XT (rows =
+ * g2ptq_hessian_stage_rows(C) ≥ C, zero padded; ld ldt) at token column
+ * t_off (a multiple of 64), zero padding the batch to a multiple of 64
+ * tokens.  g2ptq_hessian_gram then applies H = beta·H + alpha·XTᵀ·XT over
+ * the first K staged columns; it may zero-pad columns up to K rounded to
+ * 64·16, so ldt must leave that room.  Together they replace the per-batch
+ * update of GPTQ.add_batch (gptq_utils/gptq_utils.py:123-126). */
+int g2ptq_hessian_stage_rows(int64_t C, int64_t* rows);
+int g2ptq_hessian_stage(void* stream, const uint16_t* X, int64_t T, int64_t C, int64_t ldx,
+                        uint16_t* XT, int64_t ldt, int64_t t_off);
+int g2ptq_hessian_gram_workspace(int64_t K, int64_t C, size_t* bytes);
+int g2ptq_hessian_gram(void* stream, uint16_t* XT, int64_t ldt, int64_t K, int64_t C, float alpha,
+                       float beta, float* H, int64_t ldh, void* ws, size_t ws_bytes);
+
 /* GPTAQ: H = beta·H + alpha·XᵀX and Dx = beta·Dx + alpha·(X_fp − X)ᵀX, with
  * Dx[i][j] = Σ_t (x_fp − x)[t,i]·x[t,j].  Replaces GPTAQ.add_batch
  * (gptq_utils/gptaq_utils.py:130-148). */

@@ -194,7 +194,8 @@ def test_g2ptq_block_bitexact(dev, case):
     assert_bitexact(dgh, egh, "ghinv")
 
 
-@pytest.mark.parametrize("T,C,calls", [(300, 200, 3), (1000, 129, 1), (64, 384, 2), (2048, 512, 4)])
+@pytest.mark.parametrize("T,C,calls", [(300, 200, 3), (1000, 129, 1), (64, 384, 2), (2048, 512, 4),
+                                        (4096, 1024, 2), (8192, 600, 1), (1536, 2304, 1)])
 def test_hessian_update_matches_oracle(dev, T, C, calls):
     from g2ptq_amd import _core
     g = gen(T + C)
@@ -213,6 +214,37 @@ def test_hessian_update_matches_oracle(dev, T, C, calls):
     ref = st["H"]
     scale = ref.abs().max()
     assert (Hd - ref).abs().max() <= 2e-6 * scale * (T * calls) ** 0.5
+
+
+def test_hessian_staged_matches_one_shot(dev):
+    """Stage three batches and accumulate once == three per-batch updates (to rounding)."""
+    from g2ptq_amd import _core, _lib
+    C = 700
+    g = gen(31)
+    xs = [(torch.randn(T, C, generator=g)).bfloat16() for T in (512, 300, 1000)]
+    H1 = torch.zeros(C, C, device=dev)
+    n = 0
+    for x in xs:
+        beta = _core.f32(n / (n + 1))
+        n += 1
+        _core.hessian_update(H1, x.to(dev), _core.sqrt_scale_sq(n), beta)
+    rows = _lib.query_size_i64("g2ptq_hessian_stage_rows", C)
+    K = sum((x.shape[0] + 63) // 64 * 64 for x in xs)
+    ldt = (K + 1023) // 1024 * 1024 + 1024
+    XT = torch.empty(rows, ldt, dtype=torch.bfloat16, device=dev)
+    off = 0
+    for x in xs:
+        xd = x.to(dev)
+        _lib.call("g2ptq_hessian_stage", _lib.stream_ptr(), _lib.ptr(xd), x.shape[0], C, C,
+                  _lib.ptr(XT), ldt, off)
+        off += (x.shape[0] + 63) // 64 * 64
+    H2 = torch.zeros(C, C, device=dev)
+    ws = _lib.workspace(_lib.query_size("g2ptq_hessian_gram_workspace", off, C), dev)
+    _lib.call("g2ptq_hessian_gram", _lib.stream_ptr(), _lib.ptr(XT), ldt, off, C,
+              _core.sqrt_scale_sq(n), 0.0, _lib.ptr(H2), C, _lib.ptr(ws), ws.numel())
+    torch.cuda.synchronize()
+    assert torch.equal(H2.cpu(), H2.cpu().T)
+    assert (H1 - H2).abs().max().item() <= 1e-5 * H1.abs().max().item()
 
 
 def test_gptaq_update_matches_oracle(dev):
