@@ -14,11 +14,12 @@ from .gptq_guided_utils import GPTQGuided
 from .gptq_utils import GPTQ
 from .graph_utils import clear_graph_cache, run_graph, validate_tensors
 from .quant_utils import WeightQuantizer
+from .shared import SharedInputHessian
 
 __all__ = [
     "GPTQ", "GPTAQ", "G2PTQ", "GPTQGuided", "WeightQuantizer", "ChunkSpec", "build_chunk_specs",
     "make_group_quantizers", "merge_group_quantizers", "fake_quantize_grouped", "run_graph",
-    "validate_tensors", "clear_graph_cache",
+    "validate_tensors", "clear_graph_cache", "SharedInputHessian",
 ]
 
 

@@ -157,14 +157,26 @@ def permute_sym(H, perm):
     return out
 
 
-def factor(H, percdamp):
+def factor(H, percdamp, shared=None, key=None):
     """U[b] = chol((H[b] + p·mean(diag)·I)⁻¹, upper) with the reference's retry loop.
 
     gptq_utils.py:291-311: on a failed factorization (non-PD pivot or NaN) the
     damp is raised by 0.0015 and the layer is factored again; a damp leaving
     (0, 1) raises ``ValueError``.  Layers that succeed keep their damp.
+    ``shared`` (a SharedInputHessian whose members are all of H's slots, so all
+    slots hold the same matrix) factors one slot once and reuses the result.
     """
     B, C, _ = H.shape
+    if shared is not None:
+        ck = (percdamp, key)
+        hit = shared.cached_factor(ck)
+        if hit is None:
+            U1, d1 = factor(H[:1], percdamp)
+            hit = (U1[0], d1[0])
+            shared.store_factor(ck, *hit)
+        U = torch.empty_like(H)
+        U.copy_(hit[0].unsqueeze(0).expand(B, C, C))
+        return U, [hit[1]] * B
     dev = H.device
     U = torch.empty_like(H)
     info = torch.zeros(B, dtype=torch.int32, device=dev)

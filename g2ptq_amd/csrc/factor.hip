@@ -7,7 +7,7 @@
 // index order: one Cholesky plus one triangular inverse (2C³/3).
 //
 //   1. reverse-copy Â = J(H + damp·I)J (lower triangle) into the workspace
-//   2. blocked right-looking Cholesky of Â, NB = 128 columns per step:
+//   2. blocked right-looking Cholesky of Â, NB = 64 columns per step:
 //        potrf of the diagonal block in one workgroup (LDS), which also
 //        inverts it in place;  TRSM as a GEMM with that inverse;  SYRK
 //        trailing update as a lower-triangular fp32 MFMA GEMM
@@ -20,7 +20,8 @@
 namespace g2ptq {
 namespace {
 
-constexpr int NB = 128;
+constexpr int NB = 64;   // diagonal block / panel width
+constexpr int TPT = NB / 16;  // rows (and columns) of the per-thread register tile
 
 __global__ void diag_sum_kernel(const float* __restrict__ H, int64_t C, const int* skip,
                                 float* sums, int* st, int* info) {
@@ -67,15 +68,15 @@ __global__ void reverse_damp_kernel(const float* __restrict__ H, int64_t C, floa
   }
 }
 
-// Cholesky + in-place inverse of the nbk×nbk diagonal block at (k, k).
+// Cholesky + in-place inverse of the nbk×nbk (nbk <= 64) diagonal block at (k, k).
 //
-// Right-looking, register resident: the 128×128 block is split over a 16×16
-// thread grid, each thread holding an 8×8 tile of L and of X = L⁻¹.  At step j
-// the owners of column j of L and of row j of X publish them through LDS
+// Right-looking, register resident: the block is split over a 16×16 thread
+// grid, each thread holding a 4×4 tile of L and of X = L⁻¹.  At step j the
+// owners of column j of L and of row j of X publish them through LDS
 // (double-buffered, one barrier per step); every thread then finishes the
-// pivot (sqrt, scale by its reciprocal), and applies the rank-1 updates of
-// the Cholesky trailing block and of the forward elimination of L·X = I to its
-// own tile.
+// pivot (sqrt, scale by its reciprocal) and applies the rank-1 updates of the
+// Cholesky trailing block and of the forward elimination of L·X = I to its
+// own tile.  Register tiles are indexed with compile-time indices only.
 __global__ __launch_bounds__(256) void potrf_diag_kernel(float* WA, int64_t C, int64_t k, int nbk,
                                                          int* st, int* info) {
   const int64_t b = blockIdx.x;
@@ -85,12 +86,12 @@ __global__ __launch_bounds__(256) void potrf_diag_kernel(float* WA, int64_t C, i
   float* Wb = WA + b * C * C + k * C + k;
   const int tid = threadIdx.x;
   const int tx = tid & 15, ty = tid >> 4;
-  const int i0 = ty * 8, c0 = tx * 8;
-  float l[8][8], x[8][8];
+  const int i0 = ty * TPT, c0 = tx * TPT;
+  float l[TPT][TPT], x[TPT][TPT];
 #pragma unroll
-  for (int r = 0; r < 8; ++r)
+  for (int r = 0; r < TPT; ++r)
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
+    for (int c = 0; c < TPT; ++c) {
       const int i = i0 + r, kk = c0 + c;
       l[r][c] = (kk <= i && i < nbk) ? Wb[(int64_t)i * C + kk] : 0.f;
       x[r][c] = (i == kk) ? 1.f : 0.f;
@@ -98,24 +99,22 @@ __global__ __launch_bounds__(256) void potrf_diag_kernel(float* WA, int64_t C, i
   int fail = 0;
   for (int j = 0; j < nbk; ++j) {
     const int buf = j & 1;
-    const int cj = j & 7, tj = j >> 3;
-    // Register tiles are indexed with compile-time indices only (selects), so
-    // they stay in VGPRs.
+    const int cj = j % TPT, tj = j / TPT;
     if (tx == tj) {
 #pragma unroll
-      for (int r = 0; r < 8; ++r) {
+      for (int r = 0; r < TPT; ++r) {
         float v = 0.f;
 #pragma unroll
-        for (int c = 0; c < 8; ++c) v = (c == cj) ? l[r][c] : v;
+        for (int c = 0; c < TPT; ++c) v = (c == cj) ? l[r][c] : v;
         colL[buf][i0 + r] = v;
       }
     }
     if (ty == tj) {
 #pragma unroll
-      for (int c = 0; c < 8; ++c) {
+      for (int c = 0; c < TPT; ++c) {
         float v = 0.f;
 #pragma unroll
-        for (int r = 0; r < 8; ++r) v = (r == cj) ? x[r][c] : v;
+        for (int r = 0; r < TPT; ++r) v = (r == cj) ? x[r][c] : v;
         rowX[buf][c0 + c] = v;
       }
     }
@@ -129,14 +128,14 @@ __global__ __launch_bounds__(256) void potrf_diag_kernel(float* WA, int64_t C, i
     const float rd = 1.f / d;
     // Unconditional LDS reads (rows above the pivot hold stale values that the
     // selects discard), so no divergent branch separates the loads.
-    float li[8], lk[8], xr[8];
+    float li[TPT], lk[TPT], xr[TPT];
 #pragma unroll
-    for (int r = 0; r < 8; ++r) {
+    for (int r = 0; r < TPT; ++r) {
       const float v = colL[buf][i0 + r];
       li[r] = (i0 + r > j) ? v * rd : 0.f;
     }
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
+    for (int c = 0; c < TPT; ++c) {
       const float v = colL[buf][c0 + c];
       const float xv = rowX[buf][c0 + c];
       lk[c] = (c0 + c > j) ? v * rd : 0.f;
@@ -146,20 +145,20 @@ __global__ __launch_bounds__(256) void potrf_diag_kernel(float* WA, int64_t C, i
     // updates need no masks; only the strict upper triangle of the L tile is
     // written with values nobody reads.
 #pragma unroll
-    for (int r = 0; r < 8; ++r) {
+    for (int r = 0; r < TPT; ++r) {
       const bool diag_row = (i0 + r == j);
 #pragma unroll
-      for (int c = 0; c < 8; ++c) {
+      for (int c = 0; c < TPT; ++c) {
         l[r][c] -= li[r] * lk[c];
         x[r][c] = diag_row ? xr[c] : x[r][c] - li[r] * xr[c];
       }
     }
     if (tx == tj) {
 #pragma unroll
-      for (int r = 0; r < 8; ++r) {
+      for (int r = 0; r < TPT; ++r) {
         const float v = (i0 + r == j) ? d : li[r];
 #pragma unroll
-        for (int c = 0; c < 8; ++c)
+        for (int c = 0; c < TPT; ++c)
           if (c == cj) l[r][c] = v;
       }
     }
@@ -172,9 +171,9 @@ __global__ __launch_bounds__(256) void potrf_diag_kernel(float* WA, int64_t C, i
     return;
   }
 #pragma unroll
-  for (int r = 0; r < 8; ++r)
+  for (int r = 0; r < TPT; ++r)
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
+    for (int c = 0; c < TPT; ++c) {
       const int i = i0 + r, kk = c0 + c;
       if (i < nbk && kk < nbk) Wb[(int64_t)i * C + kk] = (kk <= i) ? x[r][c] : 0.f;
     }

@@ -115,7 +115,8 @@ class GPTQ:
                 perm, invperm = _core.act_order(H, 0)
                 W = _core.permute_cols(W, perm)
                 H = _core.permute_sym(H, perm)
-            Hinv, _ = _core.factor(H, percdamp)
+            Hinv, _ = _core.factor(H, percdamp, getattr(self, "_shared_factor", None),
+                                   key=bool(actorder))
         Q, W_int, Scale = _compensate(_lib.VARIANT_GPTQ, self.quantizer, W, Hinv, blocksize,
                                       groupsize, static_groups,
                                       perm if static_groups and actorder else None, flags, graph)

@@ -16,6 +16,17 @@ class SharedInputHessian:
         if not members:
             raise ValueError("SharedInputHessian needs at least one member")
         self.members = list(members)
+        self._factors = {}
+
+    # The members' Hessians are bit-identical, and so are their dampened
+    # inverse-Cholesky factors: the first member to factor stores it here and
+    # the others reuse it (an instance uses the cache only when all of its
+    # slots are members).
+    def cached_factor(self, percdamp):
+        return self._factors.get(percdamp)
+
+    def store_factor(self, percdamp, U, damp):
+        self._factors[percdamp] = (U, damp)
 
     def add_batch(self, inp, out=None):
         owner, idx = self.members[0]
@@ -29,3 +40,9 @@ class SharedInputHessian:
             inst.H[j].copy_(owner.H[idx])
             inst._n[j] = owner._n[idx]
             inst.nsamples[j] = owner.nsamples[idx]
+        slots = {}
+        for inst, j in self.members:
+            slots.setdefault(id(inst), (inst, set()))[1].add(j)
+        for inst, js in slots.values():
+            if js == set(range(inst.num_layers)):
+                inst._shared_factor = self

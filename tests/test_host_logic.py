@@ -1,0 +1,100 @@
+"""CPU: host-side logic of the drop-in classes (no kernels run)."""
+import pytest
+import torch
+
+from g2ptq_amd import (SharedInputHessian, build_chunk_specs, make_group_quantizers,
+                       merge_group_quantizers, validate_tensors)
+from g2ptq_amd import _core
+from g2ptq_amd.quant_utils import WeightQuantizer
+
+
+def _linear(r, c):
+    return torch.nn.Linear(c, r, bias=False)
+
+
+def test_build_chunk_specs_groups_by_shape_and_chunks():
+    """gptq_utils/common_utils.py:60-85: same-shaped modules batched, ``layer_bsz`` per chunk,
+    first-seen order kept."""
+    subset = {"q": _linear(64, 32), "k": _linear(16, 32), "v": _linear(16, 32),
+              "o": _linear(64, 32), "gate": _linear(128, 32), "up": _linear(128, 32)}
+    specs = build_chunk_specs(subset, layer_bsz=2)
+    assert [s.chunk_names for s in specs] == [("q", "o"), ("k", "v"), ("gate", "up")]
+    assert [(s.rows, s.columns) for s in specs] == [(64, 32), (16, 32), (128, 32)]
+    specs = build_chunk_specs(subset, layer_bsz=1)
+    assert len(specs) == 6 and all(s.num_layers == 1 for s in specs)
+
+
+def test_build_chunk_specs_group_key():
+    subset = {"a.q": _linear(8, 8), "a.o": _linear(8, 8), "b.q": _linear(8, 8)}
+    specs = build_chunk_specs(subset, layer_bsz=4, group_key_fn=lambda n: n.split(".")[1])
+    assert sorted(s.chunk_names for s in specs) == [("a.o",), ("a.q", "b.q")]
+
+
+def test_make_and_merge_group_quantizers():
+    """gptq_utils/common_utils.py:13-30: per-group copies; merging slices rows start:end
+    and concatenates the groups' (rows, 1) parameters column-wise."""
+    q = WeightQuantizer()
+    q.configure(4, perchannel=True, sym=True)
+    qs = make_group_quantizers(q, 300, 128)
+    assert len(qs) == 3 and qs[0] is not qs[1]
+    assert len(make_group_quantizers(q, 300, -1)) == 1
+    for g, qq in enumerate(qs):
+        qq.scale = torch.arange(6, dtype=torch.float32).reshape(6, 1) + 10 * g
+        qq.zero = torch.zeros(6, 1)
+        qq._ready = True
+    m = merge_group_quantizers(qs, 2, 4, 128)
+    assert m.scale.shape == (2, 3)
+    assert m.scale.tolist() == [[2, 12, 22], [3, 13, 23]]
+    assert m.weight_groupsize == 128 and m.ready()
+
+
+def test_validate_tensors_messages():
+    """gptq_utils/graph_utils.py:12-20 — CPU tensors are rejected with RuntimeError."""
+    with pytest.raises(RuntimeError, match="requires every tensor to be on CUDA"):
+        validate_tensors("x", torch.zeros(2))
+
+
+def test_backends_other_than_hip_are_rejected():
+    with pytest.raises(NotImplementedError):
+        _core.check_backend("triton")
+    with pytest.raises(NotImplementedError):
+        _core.check_backend("torch")
+    _core.check_backend("hip")
+    with pytest.raises(NotImplementedError):
+        _core.check_export(True)
+
+
+def test_f32_rounding():
+    assert _core.f32(0.1) == float(torch.tensor(0.1, dtype=torch.float32))
+    n = 7
+    assert _core.f32(n / (n + 3)) == float(torch.tensor(n / (n + 3), dtype=torch.float32))
+
+
+def test_shared_input_hessian_membership():
+    class Fake:
+        def __init__(self, n):
+            self.num_layers = n
+            self.H = torch.zeros(n, 2, 2)
+            self._n = [0] * n
+            self.nsamples = torch.zeros(n, dtype=torch.long)
+            self.calls = []
+
+        def add_batch(self, idx, inp, out):
+            self.calls.append(idx)
+            self.H[idx] += 1
+            self._n[idx] += 1
+            self.nsamples[idx] += 1
+
+    a, b = Fake(1), Fake(2)
+    sh = SharedInputHessian([(a, 0), (b, 0), (b, 1)])
+    sh.add_batch(None)
+    sh.add_batch(None)
+    sh.finalize()
+    assert a.calls == [0, 0] and b.calls == []          # accumulated once, on the owner
+    assert torch.equal(b.H[0], a.H[0]) and torch.equal(b.H[1], a.H[0])
+    assert b._n == [2, 2] and b.nsamples.tolist() == [2, 2]
+    assert a._shared_factor is sh and b._shared_factor is sh
+    c = Fake(2)
+    sh2 = SharedInputHessian([(c, 0)])
+    sh2.finalize()
+    assert not hasattr(c, "_shared_factor")             # not every slot is a member

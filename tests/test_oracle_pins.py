@@ -1,0 +1,472 @@
+"""Pins of the CPU oracle (no GPU): every oracle function is checked against
+something other than its own formula — closed forms, known answers, fp64
+brute force, invariants, and the reference test's independent pre-refactor
+loops (restated in oracle.original_loops)."""
+import copy
+import math
+
+import pytest
+import torch
+
+from oracle import compensate as ocomp
+from oracle import factor as ofactor
+from oracle import flows as oflows
+from oracle import hessian as ohess
+from oracle import original_loops as oloops
+from oracle import quant as oquant
+from tests._util import g2_inputs, gen, gptaq_p, ref_inputs
+
+
+# ---------------------------------------------------------------------------
+# Quantizer (utils/quant_utils.py)
+# ---------------------------------------------------------------------------
+
+def test_quant_known_answer_asym_4bit():
+    """b=4 asym over [-1.5, 2.25] (all values exact in fp32): s = 3.75/15 = 0.25,
+    z = round(-8 + 1.5/0.25) = -2; codes clamp(round(x/s) + z, -8, 7)."""
+    x = torch.tensor([[-1.5, 2.25, 0.625, 0.875, 0.1]])
+    s, z = oquant.find_params(x, 4, sym=False)
+    assert s.item() == 0.25 and z.item() == -2.0
+    q, _, _ = oquant.asym_quant(x, s, z, 7)
+    # 0.625/s = 2.5 → 2 (half-even); 0.875/s = 3.5 → 4; 0.1/s = 0.4 → 0
+    assert q.tolist() == [[-8.0, 7.0, 0.0, 2.0, -2.0]]
+    assert oquant.asym_dequant(q, s, z).tolist() == [[-1.5, 2.25, 0.5, 1.0, 0.0]]
+
+
+def test_quant_known_answer_sym():
+    """sym: s = max(|xmin|, xmax)/(bit_range/2); 4-bit bit_range/2 = 7.5."""
+    x = torch.tensor([[-0.3, 0.75, 0.1]])
+    s, z = oquant.find_params(x, 4, sym=True)
+    assert s.item() == torch.tensor(0.75) / torch.tensor(7.5)
+    assert z.item() == 0.0
+
+
+def test_quant_half_to_even_ties():
+    """torch.round is half-to-even: 2.5 → 2, -1.5 → -2, 0.5 → 0, 3.5 → 4."""
+    s = torch.ones(1, 1)
+    x = torch.tensor([[2.5, -1.5, 0.5, 3.5]])
+    q, _, _ = oquant.asym_quant(x, s, torch.zeros(1, 1), 7)
+    assert q.tolist() == [[2.0, -2.0, 0.0, 4.0]]
+
+
+def test_quant_all_zero_group_scale_zero():
+    s, _ = oquant.find_params(torch.zeros(2, 8), 4, sym=True)
+    assert torch.all(s == 0)  # the reference asserts scale > 0 on this input
+
+
+def test_quant_ranges_include_zero():
+    x = torch.tensor([[0.5, 1.0], [-1.0, -0.25]])
+    s, z = oquant.find_params(x, 4, sym=False)
+    # xmin clamps to 0 on the positive row: s = 1/15, z = round(-8 - 0) = -8
+    assert s[0, 0] == torch.tensor(1.0) / 15 and z[0, 0].item() == -8.0
+    # xmax clamps to 0 on the negative row: z = clamp(round(-8 + 15)) = 7
+    assert z[1, 0].item() == 7.0
+
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+@pytest.mark.parametrize("sym", [True, False])
+def test_quant_unified_asym_matches_fake_quantize(bits, sym):
+    """tests/test_triton_compensation.py:537-579: the unified asym path with a
+    zero-filled zero point equals WeightQuantizer.fake_quantize, bit for bit."""
+    w = torch.randn(2, 37, 13, generator=gen(5000 + bits * 10 + int(sym)))
+    q = oquant.WeightQuantizer().configure(bits, sym=sym)
+    q.find_params(w.reshape(74, 13))
+    fq, codes, _ = q.fake_quantize(w[:, :, 0].reshape(74, 1))
+    c2, s2, z2 = oquant.asym_quant(w[:, :, 0], q.scale.reshape(2, 37), q.zero.reshape(2, 37), q.maxq)
+    assert torch.equal(c2, codes.reshape(2, 37))
+    assert torch.equal(oquant.asym_dequant(c2, s2, z2), fq.reshape(2, 37))
+
+
+def test_quant_mse_never_worse_than_minmax():
+    x = torch.randn(16, 64, generator=gen(1)) * 0.02
+    for sym in (True, False):
+        s0, z0 = oquant.find_params(x, 3, sym)
+        s1, z1 = oquant.find_params(x, 3, sym, mse=True)
+
+        def err(s, z):
+            q = torch.clamp(torch.round(x / s) + z, -4, 3)
+            return ((s * (q - z) - x).abs() ** 2.4).sum(-1)
+        assert torch.all(err(s1, z1) <= err(s0, z0) + 1e-12)
+
+
+# ---------------------------------------------------------------------------
+# Hessians
+# ---------------------------------------------------------------------------
+
+def test_hessian_fp64_brute_force_and_streaming():
+    """H = (2/n_seq)·Σ x xᵀ over all batches; streaming == one-shot; symmetric PSD."""
+    g = gen(2)
+    C = 24
+    batches = [torch.randn(3, 16, C, generator=g) for _ in range(4)]
+    st = ohess.gptq_state(1, C)
+    for x in batches:
+        ohess.gptq_add_batch(st, 0, x)
+    X = torch.cat([b.reshape(-1, C) for b in batches]).double()
+    n_seq = sum(b.shape[0] for b in batches)
+    ref = (2.0 / n_seq) * X.T @ X
+    assert torch.allclose(st["H"][0].double(), ref, rtol=1e-5, atol=1e-5)
+    H = st["H"][0].double()
+    assert torch.allclose(H, H.T, atol=1e-6)
+    assert torch.linalg.eigvalsh(H).min() > -1e-6
+
+
+def test_hessian_2d_input_counts_one_sample():
+    """A 2-D (MoE) input counts as one sample (gptq_utils.py:116-118)."""
+    st = ohess.gptq_state(1, 4)
+    x = torch.randn(10, 4, generator=gen(3))
+    ohess.gptq_add_batch(st, 0, x)
+    assert st["nsamples"][0] == 1
+    assert torch.allclose(st["H"][0], 2 * x.T @ x, rtol=1e-5)
+
+
+def test_gptaq_cross_term_brute_force():
+    g = gen(4)
+    C = 12
+    st = ohess.gptaq_state(1, C)
+    xs, fs = [], []
+    for _ in range(3):
+        x = torch.randn(1, 20, C, generator=g)
+        f = x.reshape(-1, C) + 0.1 * torch.randn(20, C, generator=g)
+        ohess.gptaq_add_batch(st, 0, x, f)
+        xs.append(x.reshape(-1, C))
+        fs.append(f)
+    X, F = torch.cat(xs).double(), torch.cat(fs).double()
+    ref = (2.0 / 3) * (F - X).T @ X
+    assert torch.allclose(st["dXXT"][0].double(), ref, rtol=1e-5, atol=1e-5)
+
+
+def test_gptaq_cross_term_zero_when_fp_equals_input():
+    st = ohess.gptaq_state(1, 8)
+    x = torch.randn(1, 30, 8, generator=gen(5))
+    ohess.gptaq_add_batch(st, 0, x, x.reshape(-1, 8).clone())
+    assert torch.all(st["dXXT"] == 0)
+
+
+def test_weighted_hessian_saliency_one_is_half_gptq_hessian():
+    """With saliency ≡ 1 and K equal batches of n tokens (one sample each),
+    H_g2ptq = XᵀX/(K·n) and H_gptq = 2·XᵀX/K, so H_gptq = 2n·H_g2ptq in every group."""
+    g = gen(6)
+    C, G = 16, 4
+    a = ohess.g2ptq_state(1, G, C)
+    b = ohess.gptq_state(1, C)
+    for _ in range(3):
+        x = torch.randn(32, C, generator=g)
+        ohess.g2ptq_add_batch(a, 0, x, torch.ones(32, G))
+        ohess.gptq_add_batch(b, 0, x.unsqueeze(0))
+    for gi in range(G):
+        assert torch.allclose(a["H"][0, gi] * 64, b["H"][0], rtol=1e-5, atol=1e-5)
+
+
+def test_weighted_hessian_fp64_brute_force():
+    g = gen(7)
+    C, G = 10, 3
+    st = ohess.g2ptq_state(1, G, C)
+    xs, ss = [], []
+    for _ in range(2):
+        x = torch.randn(25, C, generator=g)
+        s = torch.rand(25, G, generator=g)
+        ohess.g2ptq_add_batch(st, 0, x, s)
+        xs.append(x.double())
+        ss.append(s.double())
+    ref = sum(torch.einsum("t,ti,tj->ij", s[:, gi], x, x) / (25 * 2) for x, s in zip(xs, ss)
+              for gi in [0])
+    assert torch.allclose(st["H"][0, 0].double(), ref, rtol=1e-5, atol=1e-6)
+    act = sum((x ** 2).sum(0) for x in xs) / 50
+    assert torch.allclose(st["act_square"][0].double(), act, rtol=1e-5)
+
+
+# ---------------------------------------------------------------------------
+# Factor
+# ---------------------------------------------------------------------------
+
+def _spd(C, seed, scale_spread=1.0):
+    g = gen(seed)
+    X = torch.randn(4 * C, C, generator=g) * torch.exp(scale_spread * torch.randn(C, generator=g))
+    return (2 / X.shape[0]) * X.T @ X
+
+
+def test_factor_is_upper_inverse_cholesky():
+    """UᵀU = (H + λI)⁻¹ and U upper with positive diagonal (the unique such factor)."""
+    H = _spd(48, 8, 0.3)
+    U, damp = ofactor.damp_chol_inv_upper(H, 0.01)
+    assert damp == 0.01
+    assert torch.all(torch.tril(U, -1) == 0) and torch.all(torch.diagonal(U) > 0)
+    A = H.double() + 0.01 * torch.mean(torch.diag(H)).double() * torch.eye(48, dtype=torch.float64)
+    assert torch.allclose(U.double().T @ U.double(), torch.linalg.inv(A), rtol=1e-3, atol=1e-5)
+    Ut, _ = ofactor.exact_inv_upper(H, 0.01)
+    assert ((U.double() - Ut).norm() / Ut.norm()).item() < 1e-4
+
+
+def test_factor_reverse_cholesky_identity():
+    """The identity the HIP factor relies on: chol(A⁻¹, upper) = J·chol(J·A·J)⁻¹·J."""
+    A = _spd(40, 9).double() + 0.05 * torch.eye(40, dtype=torch.float64)
+    J = torch.eye(40, dtype=torch.float64).flip(0)
+    U1 = torch.linalg.cholesky(torch.linalg.inv(A), upper=True)
+    U2 = J @ torch.linalg.inv(torch.linalg.cholesky(J @ A @ J)) @ J
+    assert ((U1 - U2).norm() / U1.norm()).item() < 1e-7
+
+
+def test_factor_damp_retry_then_error():
+    """Indefinite H: damp grows by 0.0015 until PD; hopeless H raises ValueError."""
+    H = _spd(32, 10)
+    lam = torch.linalg.eigvalsh(H.double())[0].item()
+    m = torch.mean(torch.diag(H.double())).item()
+    m2 = (m - lam) / 1.0153
+    H2 = (H.double() - (lam + 0.0153 * m2) * torch.eye(32, dtype=torch.float64)).float()
+    _, d = ofactor.damp_chol_inv_upper(H2, 0.01)
+    assert abs(d - 0.016) < 1e-9
+    bad = -torch.eye(8)
+    with pytest.raises(ValueError):
+        ofactor.damp_chol_inv_upper(bad, 0.01)
+
+
+def test_prepare_hessian_zero_and_dead():
+    H = torch.zeros(2, 4, 4)
+    H[1] = torch.diag(torch.tensor([1.0, 0.0, 2.0, 0.0]))
+    W = torch.ones(2, 3, 4)
+    ofactor.prepare_hessian(H, W)
+    assert torch.equal(H[0], torch.eye(4))          # all-zero → identity (RTN)
+    assert torch.equal(torch.diag(H[1]), torch.tensor([1.0, 1.0, 2.0, 1.0]))
+    assert torch.all(W[0] == 1)
+    assert torch.all(W[1][:, [1, 3]] == 0) and torch.all(W[1][:, [0, 2]] == 1)
+
+
+# ---------------------------------------------------------------------------
+# Compensation
+# ---------------------------------------------------------------------------
+
+def _quantizers(W, bits, sym, groupsize, static):
+    B, R, C = W.shape
+    qs = oquant.make_group_quantizers(oquant.WeightQuantizer().configure(bits, sym=sym), C, groupsize)
+    if groupsize == -1:
+        qs[0].find_params(W.reshape(B * R, C))
+    elif static:
+        for i, q in enumerate(qs):
+            q.find_params(W.reshape(B * R, C)[:, i * groupsize:(i + 1) * groupsize])
+    return qs
+
+
+@pytest.mark.parametrize("groupsize", [-1, 8])
+def test_gptq_identity_w_minus_q_equals_err_u(groupsize):
+    """GPTQ: W − Q = E·U (exact arithmetic; fp64 here) for every block."""
+    g = gen(11)
+    B, R, C = 1, 6, 24
+    W = torch.randn(B, R, C, generator=g, dtype=torch.float64)
+    U = torch.triu(torch.randn(B, C, C, generator=g, dtype=torch.float64) * 0.05, 1)
+    U += torch.diag_embed(1 + torch.rand(B, C, generator=g, dtype=torch.float64))
+    # collect errors with an fp64 run of the block loop
+    W0 = W.clone()
+    qs = _quantizers(W.float(), 4, True, groupsize, False)
+    for q in qs:
+        q.scale = q.scale.double() if torch.is_tensor(q.scale) else q.scale
+    Wd = W.clone()
+    E = torch.zeros_like(W)
+    Q = torch.zeros_like(W)
+    bs = 8
+    for i1 in range(0, C, bs):
+        i2 = min(i1 + bs, C)
+        W1 = Wd[:, :, i1:i2].clone()
+        for j in range(i2 - i1):
+            col = i1 + j
+            gi = 0 if groupsize == -1 else col // groupsize
+            if groupsize != -1 and col % groupsize == 0:
+                s, z = oquant.find_params(Wd[0, :, col:col + groupsize].float(), 4, True)
+                qs[gi].scale, qs[gi].zero = s.double(), z.double()
+            s, z = qs[gi].scale.reshape(R).double(), qs[gi].zero.reshape(R).double()
+            x = W1[0, :, j]
+            qv = s * (torch.clamp(torch.round(x / s) + z, -8, 7) - z)
+            e = (x - qv) / U[0, col, col]
+            Q[0, :, col], E[0, :, col] = qv, e
+            W1[0, :, j:] -= e[:, None] * U[0, col, i1 + j:i2][None, :]
+        Wd[:, :, i2:] -= E[:, :, i1:i2] @ U[:, i1:i2, i2:]
+    assert torch.allclose(W0 - Q, E @ U, atol=1e-10)
+
+
+def test_gptq_diagonal_u_is_rtn():
+    """U diagonal ⇒ no compensation ⇒ GPTQ == round-to-nearest, bit for bit."""
+    g = gen(12)
+    B, R, C = 2, 9, 20
+    W = torch.randn(B, R, C, generator=g) * 0.1
+    U = torch.diag_embed(1 + torch.rand(B, C, generator=g))
+    qs = _quantizers(W, 4, False, -1, False)
+    Q, codes, _ = ocomp.gptq_compensation(W.clone(), U, qs, 8)
+    q = oquant.WeightQuantizer().configure(4, sym=False)
+    q.find_params(W.reshape(B * R, C))
+    fq, c2, _ = q.fake_quantize(W.reshape(B * R, C))
+    assert torch.equal(Q.reshape(B * R, C), fq)
+    assert torch.equal(codes.reshape(B * R, C), c2)
+
+
+def test_gptq_blocksize_invariance():
+    """With every group start on a block start, results do not depend on the block size."""
+    g = gen(13)
+    B, R, C = 1, 16, 32
+    W = torch.randn(B, R, C, generator=g, dtype=torch.float64).float()
+    H = _spd(C, 14).unsqueeze(0)
+    U, _ = ofactor.damp_chol_inv_upper(H[0], 0.01)
+    outs = []
+    for bs in (4, 8, 16, 32):
+        qs = _quantizers(W, 4, True, 8, True)
+        outs.append(ocomp.gptq_compensation(W.clone(), U.unsqueeze(0), qs, bs, 8, True)[1])
+    for o in outs[1:]:
+        mismatch = (o != outs[0]).float().mean().item()
+        assert mismatch <= 0.01  # only rounding-tie cascades may differ
+
+
+def test_gptaq_with_zero_p_equals_gptq():
+    g = gen(15)
+    W = torch.randn(2, 11, 20, generator=g)
+    H = torch.stack([_spd(20, 16), _spd(20, 17)])
+    U = torch.stack([ofactor.damp_chol_inv_upper(h, 0.01)[0] for h in H])
+    qa = _quantizers(W, 4, False, -1, False)
+    qb = copy.deepcopy(qa)
+    a = ocomp.gptq_compensation(W.clone(), U, qa, 8)
+    b = ocomp.gptaq_compensation(W.clone(), U, torch.zeros_like(U), qb, 8)
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+
+
+def test_g2ptq_with_zero_gradient_terms_equals_gptq():
+    g = gen(18)
+    W = torch.randn(1, 12, 24, generator=g)
+    U = ofactor.damp_chol_inv_upper(_spd(24, 19), 0.01)[0].unsqueeze(0)
+    qa = _quantizers(W, 3, True, 8, True)
+    qb = copy.deepcopy(qa)
+    a = ocomp.gptq_compensation(W.clone(), U, qa, 8, 8, True)
+    Z = torch.zeros_like(W)
+    b = ocomp.g2ptq_compensation(W.clone(), U, Z, Z.clone(), qb, 8, 8, True)
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+
+
+def test_obs_brute_force_tiny_c():
+    """Tiny C in fp64: GPTQ's lazy-batch loop equals the optimal-brain-surgeon
+    sequence with explicit inverse downdates (the GPTQ paper's equivalence)."""
+    g = gen(20)
+    R, C = 5, 7
+    W = torch.randn(R, C, generator=g, dtype=torch.float64)
+    H = _spd(C, 21).double() + 0.1 * torch.eye(C, dtype=torch.float64)
+    s = torch.full((R, 1), 0.3, dtype=torch.float64)
+
+    def qf(x):
+        return s[:, 0] * torch.clamp(torch.round(x / s[:, 0]), -8, 7)
+    # OBS: quantize column j, update remaining with the current inverse, downdate the inverse
+    Wo = W.clone()
+    Hinv = torch.linalg.inv(H)
+    Qo = torch.zeros_like(W)
+    for j in range(C):
+        q = qf(Wo[:, j])
+        Qo[:, j] = q
+        err = (Wo[:, j] - q) / Hinv[j, j]
+        Wo[:, j:] -= err[:, None] * Hinv[j, j:][None, :]
+        Hinv = Hinv - Hinv[:, j:j + 1] @ Hinv[j:j + 1, :] / Hinv[j, j]
+    # GPTQ with U = chol(H⁻¹, upper)
+    U = torch.linalg.cholesky(torch.linalg.inv(H), upper=True)
+    Wg = W.clone()
+    Qg = torch.zeros_like(W)
+    for j in range(C):
+        q = qf(Wg[:, j])
+        Qg[:, j] = q
+        e = (Wg[:, j] - q) / U[j, j]
+        Wg[:, j:] -= e[:, None] * U[j, j:][None, :]
+    assert torch.allclose(Qo, Qg, atol=1e-9)
+
+
+@pytest.mark.parametrize("cfg", [("ungrouped", -1, False, False), ("dynamic", 4, False, False),
+                                 ("static_actorder", 4, True, True)])
+@pytest.mark.parametrize("sym", [True, False])
+def test_refactored_loops_match_original_loops(cfg, sym):
+    """tests/test_triton_compensation.py:581-772 on CPU: oracle.compensate (refactored
+    torch backend) vs oracle.original_loops (pre-refactor loops)."""
+    name, groupsize, static, actorder = cfg
+    B, R, C, bs, bits = 2, 37, 15, 5, 4
+    g = gen(8000 + len(name) * 100 + int(sym))
+    original = torch.randn(B, R, C, generator=g)
+    perm = None
+    weight = original.clone()
+    if actorder:
+        perm = torch.randperm(C, generator=g)
+        weight = weight[:, :, perm]
+    hinv = torch.triu(torch.randn(B, C, C, generator=g).mul_(0.002), diagonal=1)
+    torch.diagonal(hinv, dim1=1, dim2=2).copy_(torch.rand(B, C, generator=g).mul_(0.5).add_(0.75))
+    z = torch.randn(weight.shape, generator=g).mul_(0.002)
+    gh = torch.randn(weight.shape, generator=g).mul_(0.002)
+    p = torch.triu(torch.randn(B, C, C, generator=g).mul_(0.002), diagonal=1)
+    qperm = perm if static and actorder else None
+
+    def prep():
+        tpl = oquant.WeightQuantizer().configure(bits, sym=sym)
+        orig = copy.deepcopy(tpl)
+        orig.find_params(original.reshape(B * R, C))
+        groups = None
+        if static:
+            groups = []
+            for s in range(0, C, groupsize):
+                q = copy.deepcopy(orig)
+                q.find_params(original[:, :, s:s + groupsize].reshape(B * R, -1))
+                groups.append(q)
+            cur = copy.deepcopy(groups)
+        elif groupsize == -1:
+            cur = [copy.deepcopy(orig)]
+        else:
+            cur = [copy.deepcopy(tpl) for _ in range((C + groupsize - 1) // groupsize)]
+        return orig, groups, cur
+
+    def same(a, e):
+        assert torch.equal(a[1], e[1])
+        for i in (0, 2, 3) + ((4,) if len(e) == 5 else ()):
+            torch.testing.assert_close(a[i], e[i], rtol=2e-5, atol=2e-5)
+
+    o, gr, cur = prep()
+    exp = oloops.gptq_loop(weight.clone(), hinv.clone(), o, gr, bs, groupsize, qperm)
+    w = weight.clone()
+    same((*ocomp.gptq_compensation(w, hinv.clone(), cur, bs, groupsize, static, qperm), w), exp)
+    o, gr, cur = prep()
+    exp = oloops.g2ptq_loop(weight.clone(), hinv.clone(), z.clone(), gh.clone(), o, gr, bs,
+                            groupsize, qperm)
+    w, ghc = weight.clone(), gh.clone()
+    same((*ocomp.g2ptq_compensation(w, hinv.clone(), z.clone(), ghc, cur, bs, groupsize, static,
+                                    qperm), w, ghc), exp)
+    o, gr, cur = prep()
+    exp = oloops.gptaq_loop(weight.clone(), hinv.clone(), p.clone(), o, gr, bs, groupsize, qperm)
+    w = weight.clone()
+    same((*ocomp.gptaq_compensation(w, hinv.clone(), p.clone(), cur, bs, groupsize, static, qperm),
+          w), exp)
+
+
+def test_gptaq_p_definition_brute_force():
+    g = gen(22)
+    D = torch.randn(1, 6, 6, generator=g, dtype=torch.float64)
+    U = torch.triu(torch.rand(1, 6, 6, generator=g, dtype=torch.float64)) + torch.eye(6, dtype=torch.float64)
+    P = ocomp.gptaq_P(D, U, 0.25)
+    T = D[0] @ U[0].T
+    ref = torch.zeros(6, 6, dtype=torch.float64)
+    for i in range(6):
+        for j in range(6):
+            ref[i, j] = 0.25 * sum(T[i, k] * U[0, k, j] for k in range(i + 1, 6))
+    assert torch.allclose(P[0], ref)
+
+
+# ---------------------------------------------------------------------------
+# G2PTQ trust region
+# ---------------------------------------------------------------------------
+
+def test_trust_region_beta_bounds_and_identities():
+    g = gen(23)
+    BG, Rg, C = 2, 8, 16
+    H = torch.stack([_spd(C, 24), _spd(C, 25)])
+    U, Ainv = [], []
+    for h in H:
+        u, _, a = ofactor.damp_chol_inv_upper(h, 0.01, want_inverse=True)
+        U.append(u)
+        Ainv.append(a)
+    U, Ainv = torch.stack(U), torch.stack(Ainv)
+    W = torch.randn(BG, Rg, C, generator=g) * 0.02
+    Q = W + 0.001 * torch.randn(BG, Rg, C, generator=g)
+    grad = 1e-3 * torch.randn(BG, Rg, C, generator=g)
+    beta, Z, GH = oflows.g2ptq_trust_region(grad, Ainv, U, Q, W, 0.1, True)
+    assert torch.all(beta >= 0) and torch.all(beta <= 1)
+    # GHinv = Z·U = β·Grad·UᵀU = β·Grad·A⁻¹
+    assert torch.allclose(GH, beta.unsqueeze(2) * torch.bmm(grad, Ainv), rtol=1e-3, atol=1e-9)
+    b0, Z0, G0 = oflows.g2ptq_trust_region(grad, Ainv, U, Q, W, 0.0, False)
+    assert torch.all(b0 == 0) and torch.all(Z0 == 0) and torch.all(G0 == 0)
