@@ -105,8 +105,8 @@ def run_step(acts, layers, w0, n_tokens, ev):
         step_tok = BSZ * SEQ
         for t0 in range(0, n_tokens, step_tok):
             share.add_batch(X[t0:t0 + step_tok].view(-1, SEQ, C))
+        share.finalize()  # reads H: runs the Gram over the staged tokens
         e1.record(stream)
-        share.finalize()
         e2, e3 = ev()
         e2.record(stream)
         for gq, spec in insts:
@@ -177,6 +177,22 @@ def cpu_baseline():
             "parts_s": {k: round(v, 3) for k, v in parts.items()}}
 
 
+def traffic_per_launch():
+    """HBM bytes per Gram launch from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE and WRITE_SIZE, each scaled by its reading for a plain copy of
+    known size), or None when no such summary is present."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                        "gram256_config2_pmc_traffic.txt")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return json.loads(line.split(":", 1)[1])
+    except (OSError, ValueError):
+        pass
+    return None
+
+
 def _cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
@@ -203,10 +219,12 @@ def main():
     def ev():
         return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
+    from g2ptq_amd import _stage
     for _ in range(args.warmup):
         run_step(acts, layers, w0, args.tokens, ev)
     torch.cuda.synchronize()
     hess, quant = [], []
+    _stage.TIMING = []  # HIP events around every Gram launch of the timed steps
     t0 = time.perf_counter()
     for _ in range(args.steps):
         h, q = run_step(acts, layers, w0, args.tokens, ev)
@@ -214,10 +232,18 @@ def main():
         quant.append(q)
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) / args.steps
+    grams, _stage.TIMING = _stage.TIMING, None
     hflops = hessian_flops(args.tokens)
     h_avg = sum(hess) / len(hess) / 1e3
-    launches = sum(args.tokens // (BSZ * SEQ) for _ in INPUT_DIM)
-    achieved = hflops / h_avg
+    stage_rate = hflops / h_avg
+    g_ms = [e0.elapsed_time(e1) for e0, e1, _, _, _ in grams]
+    g_flops = sum(f for _, _, f, _, _ in grams)
+    achieved = g_flops / (sum(g_ms) / 1e3)
+    shapes = {}
+    for (_, _, f, k, c), ms in zip(grams, g_ms):
+        d = shapes.setdefault(f"C{c}_K{k}", [0, 0.0])
+        d[0] += 1
+        d[1] += ms
     out = {
         "metric": METRIC,
         "value": round(wall, 4),
@@ -234,16 +260,21 @@ def main():
         "config": {"workload": "llama3-8b-block GPTQ W4 sym g128, 262144 tokens, bs128, "
                                "groups {q},{k,v},{o},{gate,up},{down}",
                    "tokens": args.tokens, "calib_batch_tokens": BSZ * SEQ},
-        "hessian_tflops": round(achieved / 1e12, 1),
+        "hessian_tflops": round(stage_rate / 1e12, 1),
         "stages_ms": {"hessian": round(h_avg * 1e3, 2),
                       "factor_and_compensation": round(sum(quant) / len(quant), 2)},
-        "roofline": {"bound": "mfma", "kernel": "hessian_update (transpose + bf16 Gram)",
+        "roofline": {"bound": "mfma",
+                     "kernel": "gram256_kernel via g2ptq_hessian_gram (bf16 MFMA Gram of the "
+                               "staged tokens; one launch per flush)",
                      "achieved": round(achieved / 1e12, 2), "peak": PEAK_BF16 / 1e12,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16, 4),
-                     "launches_per_step": launches,
-                     "flops_per_launch_C4096": 2 * BSZ * SEQ * 4096 ** 2,
-                     "flops_per_launch_C14336": 2 * BSZ * SEQ * 14336 ** 2,
-                     "traffic": None},
+                     "traffic": traffic_per_launch(),
+                     "work_per_launch": "2*K*C^2 flop (K staged tokens, C features)",
+                     "launches_per_step": len(grams) // max(1, args.steps),
+                     "avg_launch_ms": round(sum(g_ms) / max(1, len(g_ms)), 4),
+                     "launches": {k: {"n": v[0] // max(1, args.steps),
+                                      "avg_ms": round(v[1] / v[0], 4)}
+                                  for k, v in sorted(shapes.items())}},
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:

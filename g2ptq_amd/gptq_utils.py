@@ -9,6 +9,7 @@ the fused lazy-batch compensation in libg2ptq_hip.so.
 import torch
 
 from . import _core, _lib
+from ._stage import GramStager
 from .graph_utils import run_graph, validate_tensors
 
 
@@ -38,6 +39,36 @@ class GPTQ:
         self.H = _core.alloc((self.num_layers, self.columns, self.columns), H_device)
         self.nsamples = torch.tensor([0] * self.num_layers, device=self.dev)
         self._n = [0] * self.num_layers  # host mirror of nsamples (no syncs in add_batch)
+        self._n_flushed = [0] * self.num_layers  # samples already folded into H
+        self._stagers = [None] * self.num_layers
+
+    # ``H`` reads flush the staged calibration tokens first, so every reader
+    # (fasterquant, onload/offload, shared-input copies, callers) sees the
+    # Hessian of every batch added so far.
+    @property
+    def H(self):
+        self._flush_staged()
+        return self._H
+
+    @H.setter
+    def H(self, value):
+        self._H = value
+        if value is None:
+            for st in getattr(self, "_stagers", None) or ():
+                if st is not None:
+                    st.release()
+
+    def _flush_staged(self, idx=None):
+        stagers = getattr(self, "_stagers", None)
+        if not stagers:
+            return
+        for i in (range(self.num_layers) if idx is None else (idx,)):
+            st = stagers[i]
+            if st is None or st.k == 0:
+                continue
+            n, n0 = self._n[i], self._n_flushed[i]
+            st.flush(self._H[i], _core.sqrt_scale_sq(n), _core.f32(n0 / n))
+            self._n_flushed[i] = n
 
     def _maybe_onload_hessian(self, idx=None):
         """gptq_utils.py:109-113."""
@@ -49,12 +80,24 @@ class GPTQ:
             inp = inp.unsqueeze(0)
         tmp = inp.shape[0]
         X = _core.as_bf16_tokens(inp)
-        n = self._n[idx]
-        beta = _core.f32(n / (n + tmp))
-        n += tmp
+        T = X.shape[0]
+        st = self._stagers[idx]
+        if st is None:
+            st = self._stagers[idx] = GramStager(self.columns, X.device)
+        if not st.fits(T):
+            self._flush_staged(idx)
+            if st.can_stage(T):
+                st.reserve(T)
+        n = self._n[idx] + tmp
+        if st.fits(T):
+            st.stage(X)
+        else:
+            # a batch larger than the staging budget: update H directly
+            n0 = self._n_flushed[idx]
+            _core.hessian_update(self._H[idx], X, _core.sqrt_scale_sq(n), _core.f32(n0 / n))
+            self._n_flushed[idx] = n
         self._n[idx] = n
         self.nsamples[idx] += tmp
-        _core.hessian_update(self.H[idx], X, _core.sqrt_scale_sq(n), beta)
 
     def _run_compensation_block(self, weight, hinv, scale, zero, backend, graph):
         """gptq_utils.py:128-163 — one block in (B, R, bs) layout."""

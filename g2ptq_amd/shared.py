@@ -34,11 +34,14 @@ class SharedInputHessian:
 
     def finalize(self):
         owner, idx = self.members[0]
+        owner.H  # reading H folds any staged calibration tokens into it
         for inst, j in self.members[1:]:
             if inst is owner and j == idx:
                 continue
             inst.H[j].copy_(owner.H[idx])
             inst._n[j] = owner._n[idx]
+            if hasattr(inst, "_n_flushed"):
+                inst._n_flushed[j] = owner._n[idx]
             inst.nsamples[j] = owner.nsamples[idx]
         slots = {}
         for inst, j in self.members:

@@ -93,9 +93,10 @@ int g2ptq_hessian_update(void* stream, const uint16_t* X, int64_t T, int64_t C, 
  * launch.  g2ptq_hessian_stage writes Xᵀ of a T × C batch into XT (rows =
  * g2ptq_hessian_stage_rows(C) ≥ C, zero padded; ld ldt) at token column
  * t_off (a multiple of 64), zero padding the batch to a multiple of 64
- * tokens.  g2ptq_hessian_gram then applies H = beta·H + alpha·XTᵀ·XT over
- * the first K staged columns; it may zero-pad columns up to K rounded to
- * 64·16, so ldt must leave that room.  Together they replace the per-batch
+ * tokens.  XT must be 16-byte aligned and ldt a multiple of 8.
+ * g2ptq_hessian_gram then applies H = beta·H + alpha·XTᵀ·XT over the first K
+ * staged columns; it may zero-pad columns up to K rounded up to a multiple of
+ * 2048, so ldt must leave that room.  Together they replace the per-batch
  * update of GPTQ.add_batch (gptq_utils/gptq_utils.py:123-126). */
 int g2ptq_hessian_stage_rows(int64_t C, int64_t* rows);
 int g2ptq_hessian_stage(void* stream, const uint16_t* X, int64_t T, int64_t C, int64_t ldx,

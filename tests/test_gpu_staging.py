@@ -1,0 +1,85 @@
+"""GPU: GPTQ.add_batch's staged Hessian (tokens transposed into a staging buffer,
+one Gram launch per flush) equals the reference's per-batch running average
+(gptq_utils/gptq_utils.py:115-126) at every point where H is read."""
+import pytest
+import torch
+
+from oracle import hessian as ohess
+from tests._util import gen
+
+pytestmark = pytest.mark.gpu
+
+
+def _layers(B, R, C, dev):
+    return [torch.nn.Linear(C, R, bias=False).to(device=dev, dtype=torch.bfloat16) for _ in range(B)]
+
+
+def _close(Hd, Hr, what):
+    Hd = Hd.detach().cpu()
+    scale = Hr.abs().max().item()
+    err = (Hd - Hr).abs().max().item()
+    assert err <= 2e-6 * scale * 8, f"{what}: max err {err} (scale {scale})"
+    assert torch.equal(Hd, Hd.T), f"{what}: not symmetric"
+
+
+def test_staged_hessian_across_flushes_growth_and_reads(dev, monkeypatch):
+    from g2ptq_amd import GPTQ, _lib, _stage
+    C, B = 640, 2
+    rows = _lib.query_size_i64("g2ptq_hessian_stage_rows", C)
+    # a budget of 8192 staged tokens: the first buffer holds 8192 columns, so the
+    # batches below overflow it (flush), and the 9000-token batch bypasses staging
+    monkeypatch.setattr(_stage, "DEFAULT_BUDGET", rows * 2 * 8192)
+    gq = GPTQ(_layers(B, 64, C, dev))
+    st = ohess.gptq_state(B, C)
+    g = gen(77)
+    sig = torch.exp(torch.randn(C, generator=g))
+    shapes = [(2, 1000), (1, 2048), (3, 300), (1, 2500), (1, 9000), (4, 512), (1, 64), (1, 1)]
+    for step, (bsz, T) in enumerate(shapes):
+        x = (torch.randn(bsz, T, C, generator=g) * sig).bfloat16()
+        for b in range(B):
+            xin = x if b == 0 else x[:, : max(1, T // 2)].contiguous()
+            gq.add_batch(b, xin.to(dev), None)
+            ohess.gptq_add_batch(st, b, xin)
+        if step == 3:  # read H mid-way: flushes, and accumulation continues after
+            torch.cuda.synchronize()
+            for b in range(B):
+                _close(gq.H[b], st["H"][b], f"mid-way layer {b}")
+    torch.cuda.synchronize()
+    for b in range(B):
+        _close(gq.H[b], st["H"][b], f"final layer {b}")
+    assert gq.nsamples.tolist() == st["nsamples"]
+    # 2-D input counts as one sample (gptq_utils.py:116-118)
+    x2 = torch.randn(100, C, generator=g).bfloat16()
+    gq.add_batch(0, x2.to(dev), None)
+    ohess.gptq_add_batch(st, 0, x2)
+    _close(gq.H[0], st["H"][0], "2-D batch")
+
+
+def test_staged_hessian_feeds_fasterquant_and_free(dev):
+    """fasterquant consumes the staged tokens (H read) and free() drops the buffers."""
+    from g2ptq_amd import GPTQ, WeightQuantizer, make_group_quantizers
+    from oracle import flows as oflows
+    C, R = 256, 96
+    layers = _layers(1, R, C, dev)
+    with torch.no_grad():
+        layers[0].weight.copy_((torch.randn(R, C, generator=gen(5)) * 0.02).bfloat16())
+    W0 = layers[0].weight.detach().float().cpu().unsqueeze(0)
+    gq = GPTQ(layers)
+    q = WeightQuantizer()
+    q.configure(4, perchannel=True, sym=True)
+    gq.quantizer = make_group_quantizers(q, C, 128)
+    st = ohess.gptq_state(1, C)
+    g = gen(6)
+    for _ in range(5):
+        x = torch.randn(1, 700, C, generator=g).bfloat16()
+        gq.add_batch(0, x.to(dev), None)
+        ohess.gptq_add_batch(st, 0, x)
+    gq.fasterquant(blocksize=128, percdamp=0.01, groupsize=128, backend="hip")
+    torch.cuda.synchronize()
+    assert gq.H is None and all(s is None or s.buf is None for s in gq._stagers)
+    Qd = layers[0].weight.detach().float().cpu().unsqueeze(0)
+    ref = oflows.gptq_fasterquant(W0, st["H"], 4, True, groupsize=128)
+    e_hip = oflows.reconstruction_error(W0, Qd, st["H"])
+    e_ref = oflows.reconstruction_error(W0, ref["Q"].bfloat16().float(), st["H"])
+    assert abs(e_hip - e_ref) <= 0.005 * e_ref
+    gq.free()
