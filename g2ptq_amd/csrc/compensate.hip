@@ -4,6 +4,8 @@
 // each block is: fit the parameters of groups that start in the block
 // (dynamic groups) → fused sweep (one launch for every row of every layer in
 // the batch) → block-tail update of the remaining columns as fp32 MFMA GEMMs.
+#include <numeric>
+
 #include "sweep.hpp"
 
 namespace g2ptq {
@@ -99,12 +101,32 @@ __global__ __launch_bounds__(256) void trust_row_kernel(const float* __restrict_
 
 using namespace g2ptq;
 
+// Columns per super-block of the compensation loop.  Inside a super-block the
+// tail of every 128-column block is applied right away to the super-block's
+// remaining columns (K = bs); the columns after it receive the errors of the
+// whole super-block in one product (K = super-block width).  This is the
+// reference's right-looking update regrouped: every column still receives
+// every earlier block's error term before it is quantized, and a dynamic
+// group never straddles a super-block boundary (the width is a multiple of
+// the group size), so find_params sees the same, fully updated columns.
+// G2PTQ's tail subtracts bs·GH with a GH that changes every block, so it
+// keeps one block per super-block.
+static int64_t super_block(int variant, int64_t bs, int64_t groupsize, int static_groups) {
+  if (variant == G2PTQ_VARIANT_G2PTQ) return bs;
+  int64_t unit = bs;
+  if (groupsize > 0 && !static_groups) unit = bs / std::gcd(bs, groupsize) * groupsize;
+  return unit >= 512 ? unit : unit * (512 / unit);
+}
+
 extern "C" int g2ptq_compensate_workspace(int variant, int64_t B, int64_t R, int64_t C,
                                           int64_t blocksize, size_t* bytes) {
-  (void)variant;
   (void)C;
   G2PTQ_CHECK(bytes != nullptr, "compensate_workspace: null out");
-  *bytes = al256((size_t)B * R * std::max<int64_t>(blocksize, 1) * 4);
+  // The super-block width depends on the group layout; size for the widest
+  // (a dynamic group size that is coprime to the block size is bounded by C).
+  const int64_t bs = std::max<int64_t>(blocksize, 1);
+  const int64_t widest = variant == G2PTQ_VARIANT_G2PTQ ? bs : std::max<int64_t>(512, bs);
+  *bytes = al256((size_t)B * R * widest * 4);
   return G2PTQ_OK;
 }
 
@@ -123,83 +145,99 @@ extern "C" int g2ptq_compensate(void* stream, int variant, int64_t B, int64_t R,
   G2PTQ_CHECK(variant != G2PTQ_VARIANT_GPTAQ || P, "compensate: GPTAQ needs P");
   G2PTQ_CHECK(variant != G2PTQ_VARIANT_G2PTQ || (Z && GH), "compensate: G2PTQ needs Z and GH");
   G2PTQ_CHECK(B >= 1 && B < 65536 && R >= 1 && C >= 1, "compensate: bad sizes");
-  size_t need = 0;
-  g2ptq_compensate_workspace(variant, B, R, C, bs, &need);
-  G2PTQ_CHECK(ws && ws_bytes >= need, "compensate: workspace %zu < %zu", ws_bytes, need);
   hipStream_t s = as_stream(stream);
   const int maxq = (1 << (bits - 1)) - 1;
   const bool dynamic = groupsize > 0 && !static_groups;
+  int64_t SB = std::min(super_block(variant, bs, groupsize, static_groups),
+                        cdiv(C, bs) * bs);
+  size_t need = al256((size_t)B * R * SB * 4);
+  if (ws_bytes < need && SB > bs) {  // a smaller workspace: fall back to per-block tails
+    SB = bs;
+    need = al256((size_t)B * R * SB * 4);
+  }
+  G2PTQ_CHECK(ws && ws_bytes >= need, "compensate: workspace %zu < %zu", ws_bytes, need);
   float* E = static_cast<float*>(ws);
   const int64_t RC = R * C, CC = C * C;
 
-  for (int64_t i1 = 0; i1 < C; i1 += bs) {
-    const int64_t i2 = std::min(i1 + bs, C), n = i2 - i1;
-    if (dynamic) {
-      for (int64_t gs = (i1 + groupsize - 1) / groupsize * groupsize; gs < i2; gs += groupsize) {
-        const int64_t gi = gs / groupsize;
-        const int64_t width = std::min(groupsize, C - gs);
-        if (mse_grid > 0)
-          G2PTQ_TRY(launch_find_params_mse(s, W + gs, B * R, width, C, maxq, sym, mse_norm,
-                                           mse_grid, mse_maxshrink, scale_tab + gi * B * R,
-                                           zero_tab + gi * B * R, 1, flags));
-        else
-          G2PTQ_TRY(launch_find_params(s, W + gs, B * R, width, C, maxq, sym,
-                                       scale_tab + gi * B * R, zero_tab + gi * B * R, 1, flags));
-      }
-    }
-    SweepArgs a{};
-    a.R = R; a.n = (int)n; a.maxq = maxq;
-    a.W = W + i1; a.wb = RC; a.wr = C; a.wc = 1;
-    a.U = U + i1 * C + i1; a.ub = CC; a.uj = C;
-    a.P = P ? P + i1 * C + i1 : nullptr;
-    a.Zg = Z ? Z + i1 : nullptr; a.zb = RC; a.zr = C; a.zc = 1;
-    a.GH = GH ? GH + i1 : nullptr; a.GHout = nullptr; a.gb = RC; a.gr = C; a.gc = 1;
-    a.S = scale_tab; a.Z0 = zero_tab; a.sb = R; a.sr = 1; a.sg = B * R;
-    a.colgroup = colgroup ? colgroup + i1 : nullptr;
-    a.col0 = i1;
-    a.gsize = groupsize > 0 ? groupsize : 0;
-    a.Q = Q + i1; a.qb = RC; a.qr = C; a.qc = 1;
-    a.I = Wint ? Wint + i1 : nullptr; a.ib = RC; a.ir = C; a.ic = 1;
-    a.Sc = Scale ? Scale + i1 : nullptr; a.cb = RC; a.cr = C; a.cc = 1;
-    a.CW = nullptr;
-    if (variant == G2PTQ_VARIANT_G2PTQ) {
-      a.E = nullptr;
-      a.E2 = E; a.e2b = R * n; a.e2r = n; a.e2c = 1;
-      a.dist0 = bs - 1;
-    } else {
-      a.E = E; a.eb = R * n; a.er = n; a.ec = 1;
-      a.E2 = nullptr;
-    }
-    a.flags = flags;
-    G2PTQ_TRY(launch_sweep(s, variant, a, B));
-    if (i2 >= C) break;
-
-    // Block tail: W[:, :, i2:] -= E · U[i1:i2, i2:]  (+ variant terms).
+  // W[:, :, c0:c1] -= Ecols · U[k0:k1, c0:c1]  (+ GPTAQ: += Q[:, :, k0:k1] · P[k0:k1, c0:c1]).
+  auto tail = [&](const float* Ecols, int64_t lde, int64_t k0, int64_t k1, int64_t c0,
+                  int64_t c1) -> int {
     GemmF32 t;
-    t.M = R; t.N = C - i2; t.K = n; t.batch = B;
-    t.A = E; t.lda = n; t.sA = R * n;
-    t.B = U + i1 * C + i2; t.ldb = C; t.sB = CC;
-    t.C = W + i2; t.ldc = C; t.sC = RC;
-    t.D = W + i2; t.ldd = C; t.sD = RC;
+    t.M = R; t.N = c1 - c0; t.K = k1 - k0; t.batch = B;
+    t.A = Ecols; t.lda = lde; t.sA = R * lde;
+    t.B = U + k0 * C + c0; t.ldb = C; t.sB = CC;
+    t.C = W + c0; t.ldc = C; t.sC = RC;
+    t.D = W + c0; t.ldd = C; t.sD = RC;
     t.alpha = -1.f; t.beta = 1.f;
     if (variant == G2PTQ_VARIANT_G2PTQ) {
-      // W -= bs·GH[:, i2:] + (E − Z·D)·U_slab, with E2 = E − Z·D from the sweep.
-      t.X = GH + i2; t.ldx = C; t.sX = RC; t.gamma = -(float)bs;
+      // W -= bs·GH[:, c0:] + (E − Z·D)·U_slab, with E2 = E − Z·D from the sweep.
+      t.X = GH + c0; t.ldx = C; t.sX = RC; t.gamma = -(float)bs;
     }
     G2PTQ_TRY(gemm_f32(s, t));
     if (variant == G2PTQ_VARIANT_GPTAQ) {
-      GemmF32 p = t;  // W += Q1 · P[i1:i2, i2:]
-      p.A = Q + i1; p.lda = C; p.sA = RC;
-      p.B = P + i1 * C + i2;
+      GemmF32 p = t;  // W += Q1 · P[k0:k1, c0:c1]
+      p.A = Q + k0; p.lda = C; p.sA = RC;
+      p.B = P + k0 * C + c0;
       p.alpha = 1.f;
       G2PTQ_TRY(gemm_f32(s, p));
     } else if (variant == G2PTQ_VARIANT_G2PTQ) {
-      GemmF32 z = t;  // GH[:, i2:] -= Z1 · U_slab
-      z.A = Z + i1; z.lda = C; z.sA = RC;
-      z.C = GH + i2; z.D = GH + i2;
+      GemmF32 z = t;  // GH[:, c0:c1] -= Z1 · U_slab
+      z.A = Z + k0; z.lda = C; z.sA = RC;
+      z.C = GH + c0; z.D = GH + c0;
       z.X = nullptr; z.gamma = 0.f;
       G2PTQ_TRY(gemm_f32(s, z));
     }
+    return G2PTQ_OK;
+  };
+
+  for (int64_t s0 = 0; s0 < C; s0 += SB) {
+    const int64_t s1 = std::min(s0 + SB, C);
+    for (int64_t i1 = s0; i1 < s1; i1 += bs) {
+      const int64_t i2 = std::min(i1 + bs, C), n = i2 - i1;
+      if (dynamic) {
+        for (int64_t gs = (i1 + groupsize - 1) / groupsize * groupsize; gs < i2; gs += groupsize) {
+          const int64_t gi = gs / groupsize;
+          const int64_t width = std::min(groupsize, C - gs);
+          if (mse_grid > 0)
+            G2PTQ_TRY(launch_find_params_mse(s, W + gs, B * R, width, C, maxq, sym, mse_norm,
+                                             mse_grid, mse_maxshrink, scale_tab + gi * B * R,
+                                             zero_tab + gi * B * R, 1, flags));
+          else
+            G2PTQ_TRY(launch_find_params(s, W + gs, B * R, width, C, maxq, sym,
+                                         scale_tab + gi * B * R, zero_tab + gi * B * R, 1, flags));
+        }
+      }
+      float* Eb = E + (i1 - s0);  // this block's error columns (ld SB)
+      SweepArgs a{};
+      a.R = R; a.n = (int)n; a.maxq = maxq;
+      a.W = W + i1; a.wb = RC; a.wr = C; a.wc = 1;
+      a.U = U + i1 * C + i1; a.ub = CC; a.uj = C;
+      a.P = P ? P + i1 * C + i1 : nullptr;
+      a.Zg = Z ? Z + i1 : nullptr; a.zb = RC; a.zr = C; a.zc = 1;
+      a.GH = GH ? GH + i1 : nullptr; a.GHout = nullptr; a.gb = RC; a.gr = C; a.gc = 1;
+      a.S = scale_tab; a.Z0 = zero_tab; a.sb = R; a.sr = 1; a.sg = B * R;
+      a.colgroup = colgroup ? colgroup + i1 : nullptr;
+      a.col0 = i1;
+      a.gsize = groupsize > 0 ? groupsize : 0;
+      a.Q = Q + i1; a.qb = RC; a.qr = C; a.qc = 1;
+      a.I = Wint ? Wint + i1 : nullptr; a.ib = RC; a.ir = C; a.ic = 1;
+      a.Sc = Scale ? Scale + i1 : nullptr; a.cb = RC; a.cr = C; a.cc = 1;
+      a.CW = nullptr;
+      if (variant == G2PTQ_VARIANT_G2PTQ) {
+        a.E = nullptr;
+        a.E2 = Eb; a.e2b = R * SB; a.e2r = SB; a.e2c = 1;
+        a.dist0 = bs - 1;
+      } else {
+        a.E = Eb; a.eb = R * SB; a.er = SB; a.ec = 1;
+        a.E2 = nullptr;
+      }
+      a.flags = flags;
+      G2PTQ_TRY(launch_sweep(s, variant, a, B));
+      // The block's tail inside the super-block.
+      if (i2 < s1) G2PTQ_TRY(tail(Eb, SB, i1, i2, i2, s1));
+    }
+    // The super-block's errors applied to every later column at once.
+    if (s1 < C) G2PTQ_TRY(tail(E, SB, s0, s1, s1, C));
   }
   return G2PTQ_OK;
 }

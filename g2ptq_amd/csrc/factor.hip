@@ -7,10 +7,12 @@
 // index order: one Cholesky plus one triangular inverse (2C³/3).
 //
 //   1. reverse-copy Â = J(H + damp·I)J (lower triangle) into the workspace
-//   2. blocked right-looking Cholesky of Â, NB = 64 columns per step:
-//        potrf of the diagonal block in one workgroup (LDS), which also
-//        inverts it in place;  TRSM as a GEMM with that inverse;  SYRK
-//        trailing update as a lower-triangular fp32 MFMA GEMM
+//   2. blocked right-looking Cholesky of Â in panels of NBO = 256 columns,
+//      each factored NB = 64 columns at a time: potrf of the diagonal block
+//      in one workgroup (registers), which also inverts it in place;  TRSM
+//      as a GEMM with that inverse;  update of the panel's remaining
+//      columns;  then one SYRK trailing update per panel (K = 256) as a
+//      lower-triangular fp32 MFMA GEMM
 //   3. triangular inverse by recursive doubling: diagonal blocks are already
 //      inverted; level s joins pairs of s-sized inverses with
 //      X21 = −X22·(L21·X11), each level two batched GEMMs
@@ -20,7 +22,8 @@
 namespace g2ptq {
 namespace {
 
-constexpr int NB = 64;   // diagonal block / panel width
+constexpr int NB = 64;   // diagonal block width (potrf in registers)
+constexpr int NBO = 256; // panel width of the trailing (SYRK) updates
 constexpr int TPT = NB / 16;  // rows (and columns) of the per-thread register tile
 
 __global__ void diag_sum_kernel(const float* __restrict__ H, int64_t C, const int* skip,
@@ -254,27 +257,46 @@ extern "C" int g2ptq_inv_chol_upper(void* stream, const float* H, int64_t B, int
   hipLaunchKernelGGL(reverse_damp_kernel, cgrid, dim3(256), 0, s, H, C, percdamp, sums, st, WA);
   G2PTQ_LAUNCHED();
 
-  // Blocked Cholesky of Â (lower) with inverted diagonal blocks.
-  for (int64_t k = 0; k < C; k += NB) {
-    const int nbk = (int)std::min<int64_t>(NB, C - k);
-    hipLaunchKernelGGL(potrf_diag_kernel, dim3((unsigned)B), dim3(256), 0, s, WA, C, k, nbk, st,
-                       info);
-    G2PTQ_LAUNCHED();
-    const int64_t rest = C - k - nbk;
+  // Blocked Cholesky of Â (lower) with inverted diagonal blocks, two levels:
+  // panels of NBO columns are factored NB columns at a time (potrf + TRSM +
+  // update of the panel's own remaining columns), then the trailing matrix
+  // receives the whole panel in one SYRK with K = NBO instead of NBO/NB
+  // passes with K = NB (a quarter of the trailing-matrix traffic).
+  for (int64_t k = 0; k < C; k += NBO) {
+    const int64_t kb = std::min<int64_t>(NBO, C - k);
+    for (int64_t j = k; j < k + kb; j += NB) {
+      const int nbk = (int)std::min<int64_t>(NB, k + kb - j);
+      hipLaunchKernelGGL(potrf_diag_kernel, dim3((unsigned)B), dim3(256), 0, s, WA, C, j, nbk,
+                         st, info);
+      G2PTQ_LAUNCHED();
+      const int64_t rest = C - j - nbk;
+      if (rest <= 0) break;
+      GemmF32 t;  // panel ← panel · inv(L_jj)ᵀ
+      t.M = rest; t.N = nbk; t.K = nbk; t.batch = B;
+      t.A = WA + (j + nbk) * C + j; t.lda = C; t.sA = CC;
+      t.B = WA + j * C + j; t.ldb = C; t.sB = CC; t.b_kcontig = 1;
+      t.D = WA + (j + nbk) * C + j; t.ldd = C; t.sD = CC;
+      t.skip = st;
+      G2PTQ_TRY(gemm_f32(s, t));
+      const int64_t pw = k + kb - (j + nbk);  // panel columns still to factor
+      if (pw <= 0) continue;
+      GemmF32 y;  // panel remainder ← remainder − L[:, j] · L[panel rows, j]ᵀ (lower)
+      y.M = rest; y.N = pw; y.K = nbk; y.batch = B;
+      y.A = WA + (j + nbk) * C + j; y.lda = C; y.sA = CC;
+      y.B = WA + (j + nbk) * C + j; y.ldb = C; y.sB = CC; y.b_kcontig = 1;
+      y.C = WA + (j + nbk) * C + (j + nbk); y.ldc = C; y.sC = CC;
+      y.D = WA + (j + nbk) * C + (j + nbk); y.ldd = C; y.sD = CC;
+      y.alpha = -1.f; y.beta = 1.f; y.uplo = 1; y.skip = st;
+      G2PTQ_TRY(gemm_f32(s, y));
+    }
+    const int64_t rest = C - k - kb;
     if (rest <= 0) break;
-    GemmF32 t;  // panel ← panel · inv(L_kk)ᵀ
-    t.M = rest; t.N = nbk; t.K = nbk; t.batch = B;
-    t.A = WA + (k + nbk) * C + k; t.lda = C; t.sA = CC;
-    t.B = WA + k * C + k; t.ldb = C; t.sB = CC; t.b_kcontig = 1;
-    t.D = WA + (k + nbk) * C + k; t.ldd = C; t.sD = CC;
-    t.skip = st;
-    G2PTQ_TRY(gemm_f32(s, t));
-    GemmF32 y;  // trailing ← trailing − panel · panelᵀ (lower)
-    y.M = rest; y.N = rest; y.K = nbk; y.batch = B;
-    y.A = WA + (k + nbk) * C + k; y.lda = C; y.sA = CC;
-    y.B = WA + (k + nbk) * C + k; y.ldb = C; y.sB = CC; y.b_kcontig = 1;
-    y.C = WA + (k + nbk) * C + (k + nbk); y.ldc = C; y.sC = CC;
-    y.D = WA + (k + nbk) * C + (k + nbk); y.ldd = C; y.sD = CC;
+    GemmF32 y;  // trailing ← trailing − panel · panelᵀ (lower), K = panel width
+    y.M = rest; y.N = rest; y.K = kb; y.batch = B;
+    y.A = WA + (k + kb) * C + k; y.lda = C; y.sA = CC;
+    y.B = WA + (k + kb) * C + k; y.ldb = C; y.sB = CC; y.b_kcontig = 1;
+    y.C = WA + (k + kb) * C + (k + kb); y.ldc = C; y.sC = CC;
+    y.D = WA + (k + kb) * C + (k + kb); y.ldd = C; y.sD = CC;
     y.alpha = -1.f; y.beta = 1.f; y.uplo = 1; y.skip = st;
     G2PTQ_TRY(gemm_f32(s, y));
   }

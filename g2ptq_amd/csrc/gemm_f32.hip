@@ -1,159 +1,269 @@
-// Batched fp32 GEMM on CDNA4 matrix cores (v_mfma_f32_16x16x4_f32).
+// Batched fp32 GEMM on CDNA4 matrix cores (v_mfma_f32_32x32x2_f32).
 //
-// One workgroup = 4 wave64s computing a 128×128 output tile; each wave owns a
-// 64×64 quadrant as a 4×4 grid of 16×16 MFMA accumulators.  K advances in
-// slabs of 16 staged through LDS with register double buffering.  The same
-// kernel serves every fp32 product of the path: block-tail updates of the
+//   D = alpha·A·B + beta·C + gamma·X     (optionally one triangle of D only)
+//
+// A is M×K row-major; B is K×N row-major, or N×K row-major (b_kcontig).  The
+// same kernel serves every fp32 product of the path: block-tail updates of the
 // compensation sweep, the Cholesky TRSM/SYRK steps, the triangular-inverse
 // levels, GPTAQ's P and the G2PTQ trust-region products.
+//
+// Shape: a workgroup (4 wave64s, two per CU) computes a 128×128 tile; each
+// wave a 64×64 quadrant as 2×2 blocks of 32×32 MFMA accumulators.  K advances
+// in slabs of 32 through double-buffered LDS with 16-byte global loads for
+// two slabs in flight, interleaved with the MFMAs of the current slab.
+//
+// Operand layout: a 32x32x2 MFMA takes one k per lane half, so a slab's k
+// order is permuted: for k-octet o, lane half h holds k = 8o + 4h + j in the
+// j-th of four consecutive MFMAs.  Both operands use the same permutation,
+// so one 16-byte LDS read (4 consecutive k of one row) feeds four MFMAs.
+// A (and B given N×K) sit in LDS as [row][k] with a 36-float pitch: the
+// 16-byte reads of 16 consecutive rows hit distinct bank quads.  B given K×N
+// sits as [k][n] with a 136-float pitch and is read 4 bytes per lane (the
+// two lane halves land 32 banks apart).
 #include "common.hpp"
 
 namespace g2ptq {
 namespace {
 
-typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int BM = 128, BN = 128, BK = 16;
-constexpr int LDS_P = 144;  // row pitch (floats) of the [k][m] / [k][n] LDS slabs
+constexpr int BM = 128, BN = 128, BK = 32;
+constexpr int PK = 36;   // [row][k] pitch (floats)
+constexpr int PN = 136;  // [k][n] pitch (floats)
+constexpr int LDS_A = BM * PK;
+constexpr int LDS_B = (BN * PK > BK * PN) ? BN * PK : BK * PN;
+constexpr int GH = 8;    // tile-rows per group of the tile order
 
-template <bool B_KCONTIG>
-__global__ __launch_bounds__(256) void gemm_f32_kernel(GemmF32 g, int tiles_n) {
-  __shared__ float As[2][BK][LDS_P];
-  __shared__ float Bs[2][BK][LDS_P];
+// Tile id → (tm, tn): groups of GH tile-rows walked column by column.
+__device__ __forceinline__ void tile_of(int64_t id, int64_t tm, int64_t tn, int64_t& im,
+                                        int64_t& in) {
+  const int64_t per_group = GH * tn;
+  const int64_t grp = id / per_group, r = id - grp * per_group;
+  const int64_t first = grp * GH;
+  const int64_t h = (tm - first) < GH ? (tm - first) : GH;
+  im = first + r % h;
+  in = r / h;
+}
+
+template <bool B_KCONTIG, bool VEC>
+__global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmF32 g, int64_t tm, int64_t tn) {
+  __shared__ __attribute__((aligned(16))) float As[2][LDS_A];
+  __shared__ __attribute__((aligned(16))) float Bs[2][LDS_B];
 
   const int z = blockIdx.z;
   const int64_t b1 = z / g.batch2, b2 = z % g.batch2;
   if (g.skip && g.skip[b1]) return;
-  const int tm = blockIdx.x / tiles_n, tn = blockIdx.x % tiles_n;
-  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  // XCD-aware renumbering (workgroups go round-robin over 8 XCDs): every XCD
+  // gets a contiguous range of the grouped tile order.
+  const int64_t nwg = gridDim.x, bid = blockIdx.x;
+  const int64_t q8 = nwg >> 3, r8 = nwg & 7, xcd = bid & 7;
+  const int64_t id = xcd * q8 + (xcd < r8 ? xcd : r8) + (bid >> 3);
+  int64_t im, in;
+  tile_of(id, tm, tn, im, in);
+  const int64_t m0 = im * BM, n0 = in * BN;
   if (g.uplo == 1 && n0 > m0 + BM - 1) return;
   if (g.uplo == 2 && m0 > n0 + BN - 1) return;
 
-  const float* A = g.A + b1 * g.sA + b2 * g.sA2;
-  const float* B = g.B + b1 * g.sB + b2 * g.sB2;
+  const float* __restrict__ A = g.A + b1 * g.sA + b2 * g.sA2;
+  const float* __restrict__ B = g.B + b1 * g.sB + b2 * g.sB2;
+  const int64_t M = g.M, N = g.N, K = g.K;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
 
-  // Global staging registers: 8 A values and 8 B values per thread per slab.
-  float ra[8], rb[8];
+  // Global → register mapping (4 float4 per operand per slab per thread).
+  //   [row][k] operands: row = tid/8 + 32 i, k-quad = tid % 8.
+  //   B as K×N:          k = tid/32 + 8 i,   n-quad = tid % 32.
+  const int ra_row = tid >> 3, ra_kq = (tid & 7) * 4;
+  const int rb_k = tid >> 5, rb_nq = (tid & 31) * 4;
 
-  // A slab: 128 (m) × 16 (k).  Thread loads m = tid & 127, k = (tid >> 7) * 8 + i.
-  auto load_a = [&](int64_t k0) {
-    const int m = tid & 127;
-    const int kb = (tid >> 7) * 8;
-    const int64_t gm = m0 + m;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int64_t gk = k0 + kb + i;
-      ra[i] = (gm < g.M && gk < g.K) ? A[gm * g.lda + gk] : 0.f;
-    }
-  };
-  auto store_a = [&](int buf) {
-    const int m = tid & 127;
-    const int kb = (tid >> 7) * 8;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) As[buf][kb + i][m] = ra[i];
-  };
-  // B slab: 16 (k) × 128 (n).
-  auto load_b = [&](int64_t k0) {
-    if (B_KCONTIG) {  // B given as N×K row-major
-      const int n = tid & 127;
-      const int kb = (tid >> 7) * 8;
-      const int64_t gn = n0 + n;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int64_t gk = k0 + kb + i;
-        rb[i] = (gn < g.N && gk < g.K) ? B[gn * g.ldb + gk] : 0.f;
-      }
-    } else {  // B row-major K×N: thread loads k = tid >> 4, n = (tid & 15) * 8 + i
-      const int k = tid >> 4;
-      const int nb = (tid & 15) * 8;
-      const int64_t gk = k0 + k;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int64_t gn = n0 + nb + i;
-        rb[i] = (gk < g.K && gn < g.N) ? B[gk * g.ldb + gn] : 0.f;
+  auto ld4 = [&](const float* base, int64_t ld, int64_t r, int64_t c, int64_t R, int64_t Ccols) {
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (r < R) {
+      const float* p = base + r * ld + c;
+      if (VEC) {
+        if (c + 3 < Ccols) {
+          v = *reinterpret_cast<const float4*>(p);
+        } else {
+          if (c < Ccols) v.x = p[0];
+          if (c + 1 < Ccols) v.y = p[1];
+          if (c + 2 < Ccols) v.z = p[2];
+        }
+      } else {
+        if (c < Ccols) v.x = p[0];
+        if (c + 1 < Ccols) v.y = p[1];
+        if (c + 2 < Ccols) v.z = p[2];
+        if (c + 3 < Ccols) v.w = p[3];
       }
     }
-  };
-  auto store_b = [&](int buf) {
-    if (B_KCONTIG) {
-      const int n = tid & 127;
-      const int kb = (tid >> 7) * 8;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) Bs[buf][kb + i][n] = rb[i];
-    } else {
-      const int k = tid >> 4;
-      const int nb = (tid & 15) * 8;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) Bs[buf][k][nb + i] = rb[i];
-    }
+    return v;
   };
 
-  f32x4 acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // Register sets x / y hold one slab each (macros keep them in registers).
+  float4 xa0, xa1, xa2, xa3, xb0, xb1, xb2, xb3;
+  float4 ya0, ya1, ya2, ya3, yb0, yb1, yb2, yb3;
+#define GF_LOAD(R, slab)                                                                       \
+  do {                                                                                         \
+    const int64_t k0_ = (int64_t)(slab) * BK;                                                  \
+    R##a0 = ld4(A, g.lda, m0 + ra_row, k0_ + ra_kq, M, K);                                      \
+    R##a1 = ld4(A, g.lda, m0 + ra_row + 32, k0_ + ra_kq, M, K);                                 \
+    R##a2 = ld4(A, g.lda, m0 + ra_row + 64, k0_ + ra_kq, M, K);                                 \
+    R##a3 = ld4(A, g.lda, m0 + ra_row + 96, k0_ + ra_kq, M, K);                                 \
+    if (B_KCONTIG) {                                                                           \
+      R##b0 = ld4(B, g.ldb, n0 + ra_row, k0_ + ra_kq, N, K);                                    \
+      R##b1 = ld4(B, g.ldb, n0 + ra_row + 32, k0_ + ra_kq, N, K);                               \
+      R##b2 = ld4(B, g.ldb, n0 + ra_row + 64, k0_ + ra_kq, N, K);                               \
+      R##b3 = ld4(B, g.ldb, n0 + ra_row + 96, k0_ + ra_kq, N, K);                               \
+    } else {                                                                                   \
+      R##b0 = ld4(B, g.ldb, k0_ + rb_k, n0 + rb_nq, K, N);                                      \
+      R##b1 = ld4(B, g.ldb, k0_ + rb_k + 8, n0 + rb_nq, K, N);                                  \
+      R##b2 = ld4(B, g.ldb, k0_ + rb_k + 16, n0 + rb_nq, K, N);                                 \
+      R##b3 = ld4(B, g.ldb, k0_ + rb_k + 24, n0 + rb_nq, K, N);                                 \
+    }                                                                                          \
+  } while (0)
+#define GF_STORE(R, buf)                                                                       \
+  do {                                                                                         \
+    float* la = &As[(buf)][ra_row * PK + ra_kq];                                               \
+    *reinterpret_cast<float4*>(la) = R##a0;                                                    \
+    *reinterpret_cast<float4*>(la + 32 * PK) = R##a1;                                          \
+    *reinterpret_cast<float4*>(la + 64 * PK) = R##a2;                                          \
+    *reinterpret_cast<float4*>(la + 96 * PK) = R##a3;                                          \
+    if (B_KCONTIG) {                                                                           \
+      float* lb = &Bs[(buf)][ra_row * PK + ra_kq];                                             \
+      *reinterpret_cast<float4*>(lb) = R##b0;                                                  \
+      *reinterpret_cast<float4*>(lb + 32 * PK) = R##b1;                                        \
+      *reinterpret_cast<float4*>(lb + 64 * PK) = R##b2;                                        \
+      *reinterpret_cast<float4*>(lb + 96 * PK) = R##b3;                                        \
+    } else {                                                                                   \
+      float* lb = &Bs[(buf)][rb_k * PN + rb_nq];                                               \
+      *reinterpret_cast<float4*>(lb) = R##b0;                                                  \
+      *reinterpret_cast<float4*>(lb + 8 * PN) = R##b1;                                         \
+      *reinterpret_cast<float4*>(lb + 16 * PN) = R##b2;                                        \
+      *reinterpret_cast<float4*>(lb + 24 * PN) = R##b3;                                        \
+    }                                                                                          \
+  } while (0)
 
-  const int nk = (int)cdiv(g.K, BK);
-  if (nk > 0) {
-    load_a(0);
-    load_b(0);
-    store_a(0);
-    store_b(0);
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  const int lr = lane & 31, lh = lane >> 5;
+  // One slab: 4 k-octets × (2×2 blocks × 4 MFMAs).
+#define GF_MMA(buf)                                                                            \
+  do {                                                                                         \
+    const float* as_ = As[(buf)];                                                              \
+    const float* bs_ = Bs[(buf)];                                                              \
+    _Pragma("unroll") for (int o = 0; o < BK / 8; ++o) {                                       \
+      float4 av[2], bv[2];                                                                     \
+      _Pragma("unroll") for (int i = 0; i < 2; ++i)                                            \
+        av[i] = *reinterpret_cast<const float4*>(as_ + (wm * 64 + i * 32 + lr) * PK + o * 8 + lh * 4); \
+      _Pragma("unroll") for (int j = 0; j < 2; ++j) {                                          \
+        if (B_KCONTIG) {                                                                       \
+          bv[j] = *reinterpret_cast<const float4*>(bs_ + (wn * 64 + j * 32 + lr) * PK + o * 8 + lh * 4); \
+        } else {                                                                               \
+          const float* pb_ = bs_ + (o * 8 + lh * 4) * PN + wn * 64 + j * 32 + lr;            \
+          bv[j] = make_float4(pb_[0], pb_[PN], pb_[2 * PN], pb_[3 * PN]);                      \
+        }                                                                                      \
+      }                                                                                        \
+      _Pragma("unroll") for (int i = 0; i < 2; ++i)                                            \
+      _Pragma("unroll") for (int j = 0; j < 2; ++j) {                                          \
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i].x, bv[j].x, acc[i][j], 0, 0, 0); \
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i].y, bv[j].y, acc[i][j], 0, 0, 0); \
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i].z, bv[j].z, acc[i][j], 0, 0, 0); \
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i].w, bv[j].w, acc[i][j], 0, 0, 0); \
+      }                                                                                        \
+    }                                                                                          \
+  } while (0)
+
+  // Slabs are processed in pairs; a trailing odd slab and the prefetches past
+  // the end load zeros (k >= K is masked), which add nothing.
+  const int nk = (int)cdiv(K, (int64_t)BK);
+  const int nk2 = (nk + 1) & ~1;
+  if (nk2 > 0) {
+    GF_LOAD(x, 0);
+    GF_STORE(x, 0);
+    GF_LOAD(x, 1);
+    GF_LOAD(y, 2);
   }
   __syncthreads();
-
-  const int lr = lane & 15, lk = lane >> 4;
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < nk) {
-      load_a((int64_t)(kt + 1) * BK);
-      load_b((int64_t)(kt + 1) * BK);
-    }
-#pragma unroll
-    for (int ks = 0; ks < BK / 4; ++ks) {
-      float av[4], bv[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) av[i] = As[buf][ks * 4 + lk][wm * 64 + i * 16 + lr];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) bv[j] = Bs[buf][ks * 4 + lk][wn * 64 + j * 16 + lr];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[i], bv[j], acc[i][j], 0, 0, 0);
-    }
-    if (kt + 1 < nk) {
-      store_a(buf ^ 1);
-      store_b(buf ^ 1);
-    }
+  for (int kt = 0; kt < nk2; kt += 2) {
+    __builtin_amdgcn_sched_barrier(0);
+    GF_MMA(0);          // slab kt
+    GF_STORE(x, 1);     // slab kt+1
+    GF_LOAD(x, kt + 3);
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+    GF_MMA(1);          // slab kt+1
+    GF_STORE(y, 0);     // slab kt+2
+    GF_LOAD(y, kt + 4);
+    __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
   }
+  __builtin_amdgcn_sched_barrier(0);
+#undef GF_LOAD
+#undef GF_STORE
+#undef GF_MMA
 
-  // Epilogue.  16×16 MFMA output: lane holds rows 4*(lane/16)+v, column lane%16.
+  // Epilogue.  32×32 MFMA output: lane holds rows 8*(v/4) + 4*(lane/32) + v%4,
+  // column lane%32.  C / X may alias D (in-place updates), so the inputs of a
+  // half tile (32 per lane) are loaded before any of its outputs is stored:
+  // two memory round trips per lane instead of one per element.
   const float* C = g.C ? g.C + b1 * g.sC + b2 * g.sC2 : nullptr;
   const float* X = g.X ? g.X + b1 * g.sX + b2 * g.sX2 : nullptr;
   float* D = g.D + b1 * g.sD + b2 * g.sD2;
+  const bool use_c = g.beta != 0.f, use_x = g.gamma != 0.f;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 2; ++i) {
+    float cv[2][16];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < 2; ++j) {
+      const int64_t n = n0 + wn * 64 + j * 32 + lr;
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int64_t m = m0 + wm * 64 + i * 16 + lk * 4 + v;
-        const int64_t n = n0 + wn * 64 + j * 16 + lr;
-        if (m >= g.M || n >= g.N) continue;
+      for (int v = 0; v < 16; ++v) {
+        const int64_t m = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+        const bool in = m < M && n < N;
+        float c = (use_c && in) ? C[m * g.ldc + n] : 0.f;
+        cv[j][v] = c;
+      }
+    }
+    if (use_x) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int64_t n = n0 + wn * 64 + j * 32 + lr;
+        float xv[16];
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int64_t m = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+          xv[v] = (m < M && n < N) ? X[m * g.ldx + n] : 0.f;
+        }
+#pragma unroll
+        for (int v = 0; v < 16; ++v) cv[j][v] = g.beta * cv[j][v] + g.gamma * xv[v];
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) cv[j][v] = g.beta * cv[j][v];
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int64_t n = n0 + wn * 64 + j * 32 + lr;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t m = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+        if (m >= M || n >= N) continue;
         if (g.uplo == 1 && n > m) continue;
         if (g.uplo == 2 && m > n) continue;
-        float val = g.alpha * acc[i][j][v];
-        if (g.beta != 0.f) val += g.beta * C[m * g.ldc + n];
-        if (g.gamma != 0.f) val += g.gamma * X[m * g.ldx + n];
-        D[m * g.ldd + n] = val;
+        D[m * g.ldd + n] = g.alpha * acc[i][j][v] + cv[j][v];
       }
+    }
+  }
 }
 
 }  // namespace
@@ -166,14 +276,27 @@ int gemm_f32(hipStream_t stream, const GemmF32& g) {
   G2PTQ_CHECK(g.D != nullptr, "gemm_f32: null D");
   G2PTQ_CHECK(g.beta == 0.f || g.C != nullptr, "gemm_f32: beta != 0 needs C");
   G2PTQ_CHECK(g.gamma == 0.f || g.X != nullptr, "gemm_f32: gamma != 0 needs X");
-  const int64_t tm = cdiv(g.M, BM), tn = cdiv(g.N, BN);
+  const int64_t tm = cdiv(g.M, (int64_t)BM), tn = cdiv(g.N, (int64_t)BN);
   const int64_t nz = g.batch * g.batch2;
   G2PTQ_CHECK(tm * tn < (1ll << 31) && nz < 65536, "gemm_f32: grid too large");
+  // 16-byte operand loads need 16-byte aligned rows (every batch entry too).
+  auto al = [](const void* p, int64_t ld, int64_t s1, int64_t s2) {
+    return p == nullptr || ((reinterpret_cast<uintptr_t>(p) & 15) == 0 && ld % 4 == 0 &&
+                            s1 % 4 == 0 && s2 % 4 == 0);
+  };
+  const bool vec = al(g.A, g.lda, g.sA, g.sA2) && al(g.B, g.ldb, g.sB, g.sB2);
   dim3 grid((unsigned)(tm * tn), 1, (unsigned)nz);
-  if (g.b_kcontig)
-    hipLaunchKernelGGL(gemm_f32_kernel<true>, grid, dim3(256), 0, stream, g, (int)tn);
-  else
-    hipLaunchKernelGGL(gemm_f32_kernel<false>, grid, dim3(256), 0, stream, g, (int)tn);
+  if (g.b_kcontig) {
+    if (vec)
+      hipLaunchKernelGGL((gemm_f32_kernel<true, true>), grid, dim3(256), 0, stream, g, tm, tn);
+    else
+      hipLaunchKernelGGL((gemm_f32_kernel<true, false>), grid, dim3(256), 0, stream, g, tm, tn);
+  } else {
+    if (vec)
+      hipLaunchKernelGGL((gemm_f32_kernel<false, true>), grid, dim3(256), 0, stream, g, tm, tn);
+    else
+      hipLaunchKernelGGL((gemm_f32_kernel<false, false>), grid, dim3(256), 0, stream, g, tm, tn);
+  }
   G2PTQ_LAUNCHED();
   return G2PTQ_OK;
 }
