@@ -51,6 +51,9 @@ def parse():
     p.add_argument("--warmup", type=int, default=1)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--tokens", type=int, default=N_TOKENS)
+    p.add_argument("--calibrate-copy", action="store_true",
+                   help="run one 1 GiB device copy first (the known-size reference kernel "
+                        "for rocprofv3 FETCH_SIZE / WRITE_SIZE scaling)")
     return p.parse_args()
 
 
@@ -215,6 +218,12 @@ def main():
     _lib.load()
     acts, layers, w0 = make_inputs(dev, args.tokens)
     torch.cuda.synchronize()
+    if args.calibrate_copy:
+        src = torch.ones(1 << 28, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)  # reads 1 GiB, writes 1 GiB
+        torch.cuda.synchronize()
+        del src, dst
 
     def ev():
         return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)

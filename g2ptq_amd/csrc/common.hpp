@@ -79,6 +79,10 @@ struct GemmF32 {
   const float* X = nullptr; int64_t ldx = 0, sX = 0, sX2 = 0;
   float alpha = 1.f, beta = 0.f, gamma = 0.f;
   int uplo = 0;
+  // Structural zeros the kernel may skip (optimisation only; the skipped
+  // products must be zero): bit 1 = A lower triangular (A[m][k] = 0 for
+  // k > m), bit 2 = B lower triangular (B[k][n] = 0 for k < n).
+  int tri = 0;
   const int* skip = nullptr;  // optional per-b1 flag: nonzero => skip that entry
 };
 

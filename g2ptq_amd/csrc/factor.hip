@@ -24,7 +24,6 @@ namespace {
 
 constexpr int NB = 64;   // diagonal block width (potrf in registers)
 constexpr int NBO = 256; // panel width of the trailing (SYRK) updates
-constexpr int TPT = NB / 16;  // rows (and columns) of the per-thread register tile
 
 __global__ void diag_sum_kernel(const float* __restrict__ H, int64_t C, const int* skip,
                                 float* sums, int* st, int* info) {
@@ -73,113 +72,86 @@ __global__ void reverse_damp_kernel(const float* __restrict__ H, int64_t C, floa
 
 // Cholesky + in-place inverse of the nbk×nbk (nbk <= 64) diagonal block at (k, k).
 //
-// Right-looking, register resident: the block is split over a 16×16 thread
-// grid, each thread holding a 4×4 tile of L and of X = L⁻¹.  At step j the
-// owners of column j of L and of row j of X publish them through LDS
-// (double-buffered, one barrier per step); every thread then finishes the
-// pivot (sqrt, scale by its reciprocal) and applies the rank-1 updates of the
-// Cholesky trailing block and of the forward elimination of L·X = I to its
-// own tile.  Register tiles are indexed with compile-time indices only.
-__global__ __launch_bounds__(256) void potrf_diag_kernel(float* WA, int64_t C, int64_t k, int nbk,
-                                                         int* st, int* info) {
+// One wave64 per layer, lane i owning row i of L (a[0..63]) and of
+// X = L⁻¹ (x[0..63]) in registers; rows at or past nbk are identity rows.
+// Step j (fully unrolled, so every register index is a compile-time
+// constant): the pivot L[j][j] is read from lane j; column j of L, scaled by
+// 1/sqrt(pivot), and the (unscaled) row j of X are published through LDS;
+// every lane applies the rank-1 updates of its own rows:
+//   L[i][c] −= L[i][j]·L[c][j]          (the column is zero for c ≤ j)
+//   X[i][c] −= L[i][j]/d_j · X[j][c]    (the row is zero for c > j)
+// the Gauss–Jordan elimination of [L | I] with row j's division by d_j
+// deferred: each lane scales its own X row by its pivot's reciprocal at the
+// end.  Every update runs over all 64 entries (zeros make them exact no-ops)
+// so that the published column and row are read as whole 16-byte vectors,
+// all in flight before the first update.  A single wave needs no barriers:
+// its LDS writes and reads are processed in order.  Entries of a above the
+// diagonal accumulate values that are never read.
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void potrf_diag_kernel(
+    float* WA, int64_t C, int64_t k, int nbk, int* st, int* info) {
   const int64_t b = blockIdx.x;
   if (st[b]) return;
-  __shared__ float colL[2][NB];
-  __shared__ float rowX[2][NB];
+  __shared__ __attribute__((aligned(16))) float colL[NB];
+  __shared__ __attribute__((aligned(16))) float rowX[NB];
   float* Wb = WA + b * C * C + k * C + k;
-  const int tid = threadIdx.x;
-  const int tx = tid & 15, ty = tid >> 4;
-  const int i0 = ty * TPT, c0 = tx * TPT;
-  float l[TPT][TPT], x[TPT][TPT];
+  const int i = threadIdx.x;
+  float a[NB], x[NB];
 #pragma unroll
-  for (int r = 0; r < TPT; ++r)
-#pragma unroll
-    for (int c = 0; c < TPT; ++c) {
-      const int i = i0 + r, kk = c0 + c;
-      l[r][c] = (kk <= i && i < nbk) ? Wb[(int64_t)i * C + kk] : 0.f;
-      x[r][c] = (i == kk) ? 1.f : 0.f;
-    }
+  for (int c = 0; c < NB; ++c) {
+    a[c] = (i < nbk) ? ((c <= i) ? Wb[(int64_t)i * C + c] : 0.f) : (c == i ? 1.f : 0.f);
+    x[c] = (c == i) ? 1.f : 0.f;
+  }
+  rowX[i] = 0.f;
+  float myrd = 1.f;
   int fail = 0;
-  for (int j = 0; j < nbk; ++j) {
-    const int buf = j & 1;
-    const int cj = j % TPT, tj = j / TPT;
-    if (tx == tj) {
-#pragma unroll
-      for (int r = 0; r < TPT; ++r) {
-        float v = 0.f;
-#pragma unroll
-        for (int c = 0; c < TPT; ++c) v = (c == cj) ? l[r][c] : v;
-        colL[buf][i0 + r] = v;
-      }
-    }
-    if (ty == tj) {
-#pragma unroll
-      for (int c = 0; c < TPT; ++c) {
-        float v = 0.f;
-#pragma unroll
-        for (int r = 0; r < TPT; ++r) v = (r == cj) ? x[r][c] : v;
-        rowX[buf][c0 + c] = v;
-      }
-    }
-    __syncthreads();
-    const float djj = colL[buf][j];
-    if (!(djj > 0.f)) {  // also catches NaN; every thread sees the same value
+#pragma clang loop unroll(full)
+  for (int j = 0; j < NB; ++j) {
+    const float djj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a[j]), j));
+    if (!(djj > 0.f)) {  // also catches NaN; wave-uniform
       fail = j + 1;
       break;
     }
     const float d = __fsqrt_rn(djj);
     const float rd = 1.f / d;
-    // Unconditional LDS reads (rows above the pivot hold stale values that the
-    // selects discard), so no divergent branch separates the loads.
-    float li[TPT], lk[TPT], xr[TPT];
+    const float lij = (i > j) ? a[j] * rd : 0.f;
+    a[j] = (i == j) ? d : lij;
+    myrd = (i == j) ? rd : myrd;
+    colL[i] = lij;
+    if (i == j) {
 #pragma unroll
-    for (int r = 0; r < TPT; ++r) {
-      const float v = colL[buf][i0 + r];
-      li[r] = (i0 + r > j) ? v * rd : 0.f;
+      for (int c = 0; c <= j; c += 4)
+        *reinterpret_cast<float4*>(&rowX[c]) = make_float4(
+            x[c], c + 1 <= j ? x[c + 1] : 0.f, c + 2 <= j ? x[c + 2] : 0.f, c + 3 <= j ? x[c + 3] : 0.f);
     }
+    __builtin_amdgcn_wave_barrier();
+    float cl[NB], rx[NB];
 #pragma unroll
-    for (int c = 0; c < TPT; ++c) {
-      const float v = colL[buf][c0 + c];
-      const float xv = rowX[buf][c0 + c];
-      lk[c] = (c0 + c > j) ? v * rd : 0.f;
-      xr[c] = (c0 + c <= j) ? xv * rd : 0.f;
+    for (int q = 0; q < NB / 4; ++q) {
+      const float4 u = *reinterpret_cast<const float4*>(&colL[4 * q]);
+      const float4 v = *reinterpret_cast<const float4*>(&rowX[4 * q]);
+      cl[4 * q] = u.x; cl[4 * q + 1] = u.y; cl[4 * q + 2] = u.z; cl[4 * q + 3] = u.w;
+      rx[4 * q] = v.x; rx[4 * q + 1] = v.y; rx[4 * q + 2] = v.z; rx[4 * q + 3] = v.w;
     }
-    // li[r] = 0 for rows i <= j and lk[c] = 0 for columns <= j, so the rank-1
-    // updates need no masks; only the strict upper triangle of the L tile is
-    // written with values nobody reads.
+    const float m = lij * rd;
 #pragma unroll
-    for (int r = 0; r < TPT; ++r) {
-      const bool diag_row = (i0 + r == j);
-#pragma unroll
-      for (int c = 0; c < TPT; ++c) {
-        l[r][c] -= li[r] * lk[c];
-        x[r][c] = diag_row ? xr[c] : x[r][c] - li[r] * xr[c];
-      }
+    for (int c = 0; c < NB; ++c) {
+      a[c] -= lij * cl[c];
+      x[c] -= m * rx[c];
     }
-    if (tx == tj) {
-#pragma unroll
-      for (int r = 0; r < TPT; ++r) {
-        const float v = (i0 + r == j) ? d : li[r];
-#pragma unroll
-        for (int c = 0; c < TPT; ++c)
-          if (c == cj) l[r][c] = v;
-      }
-    }
+    __builtin_amdgcn_wave_barrier();
   }
   if (fail) {
-    if (tid == 0) {
+    if (i == 0) {
       info[b] = (int)(k + fail);
       st[b] = 1;
     }
     return;
   }
+  if (i < nbk) {
 #pragma unroll
-  for (int r = 0; r < TPT; ++r)
-#pragma unroll
-    for (int c = 0; c < TPT; ++c) {
-      const int i = i0 + r, kk = c0 + c;
-      if (i < nbk && kk < nbk) Wb[(int64_t)i * C + kk] = (kk <= i) ? x[r][c] : 0.f;
-    }
+    for (int c = 0; c < NB; ++c)
+      if (c < nbk) Wb[(int64_t)i * C + c] = (c <= i) ? x[c] * myrd : 0.f;
+  }
 }
 
 // U[i][j] = X[C-1-i][C-1-j] for i <= j, 0 below; NaN → info = -1.
@@ -266,7 +238,7 @@ extern "C" int g2ptq_inv_chol_upper(void* stream, const float* H, int64_t B, int
     const int64_t kb = std::min<int64_t>(NBO, C - k);
     for (int64_t j = k; j < k + kb; j += NB) {
       const int nbk = (int)std::min<int64_t>(NB, k + kb - j);
-      hipLaunchKernelGGL(potrf_diag_kernel, dim3((unsigned)B), dim3(256), 0, s, WA, C, j, nbk,
+      hipLaunchKernelGGL(potrf_diag_kernel, dim3((unsigned)B), dim3(64), 0, s, WA, C, j, nbk,
                          st, info);
       G2PTQ_LAUNCHED();
       const int64_t rest = C - j - nbk;
@@ -320,6 +292,7 @@ extern "C" int g2ptq_inv_chol_upper(void* stream, const float* H, int64_t B, int
       t.A = WA + (i0 + sz) * C + i0; t.lda = C; t.sA = CC; t.sA2 = pstride;
       t.B = WA + i0 * C + i0; t.ldb = C; t.sB = CC; t.sB2 = pstride;
       t.D = WT; t.ldd = sz; t.sD = npairs * n2 * sz; t.sD2 = n2 * sz;
+      t.tri = 2;  // X11 is lower triangular
       t.skip = st;
       G2PTQ_TRY(gemm_f32(s, t));
       GemmF32 x;  // X21 = −X22 · T
@@ -327,7 +300,8 @@ extern "C" int g2ptq_inv_chol_upper(void* stream, const float* H, int64_t B, int
       x.A = WA + (i0 + sz) * C + (i0 + sz); x.lda = C; x.sA = CC; x.sA2 = pstride;
       x.B = WT; x.ldb = sz; x.sB = npairs * n2 * sz; x.sB2 = n2 * sz;
       x.D = WA + (i0 + sz) * C + i0; x.ldd = C; x.sD = CC; x.sD2 = pstride;
-      x.alpha = -1.f; x.skip = st;
+      x.alpha = -1.f; x.tri = 1;  // X22 is lower triangular
+      x.skip = st;
       G2PTQ_TRY(gemm_f32(s, x));
     }
   }

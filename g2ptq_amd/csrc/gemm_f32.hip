@@ -66,7 +66,11 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmF32 g, int64_t tm,
 
   const float* __restrict__ A = g.A + b1 * g.sA + b2 * g.sA2;
   const float* __restrict__ B = g.B + b1 * g.sB + b2 * g.sB2;
-  const int64_t M = g.M, N = g.N, K = g.K;
+  const int64_t M = g.M, N = g.N;
+  // K range of this tile: triangular operands contribute nothing outside it.
+  int64_t klo = 0, K = g.K;
+  if (g.tri & 1) K = K < m0 + BM ? K : m0 + BM;
+  if (g.tri & 2) klo = n0 / BK * BK;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -105,7 +109,7 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmF32 g, int64_t tm,
   float4 ya0, ya1, ya2, ya3, yb0, yb1, yb2, yb3;
 #define GF_LOAD(R, slab)                                                                       \
   do {                                                                                         \
-    const int64_t k0_ = (int64_t)(slab) * BK;                                                  \
+    const int64_t k0_ = klo + (int64_t)(slab) * BK;                                            \
     R##a0 = ld4(A, g.lda, m0 + ra_row, k0_ + ra_kq, M, K);                                      \
     R##a1 = ld4(A, g.lda, m0 + ra_row + 32, k0_ + ra_kq, M, K);                                 \
     R##a2 = ld4(A, g.lda, m0 + ra_row + 64, k0_ + ra_kq, M, K);                                 \
@@ -182,7 +186,7 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmF32 g, int64_t tm,
 
   // Slabs are processed in pairs; a trailing odd slab and the prefetches past
   // the end load zeros (k >= K is masked), which add nothing.
-  const int nk = (int)cdiv(K, (int64_t)BK);
+  const int nk = K > klo ? (int)cdiv(K - klo, (int64_t)BK) : 0;
   const int nk2 = (nk + 1) & ~1;
   if (nk2 > 0) {
     GF_LOAD(x, 0);

@@ -432,29 +432,17 @@ __global__ __launch_bounds__(256) void gram_reduce_kernel(G2Args a) {
   }
 }
 
-// Split count from a small cost model: MFMA time at the tile-wave utilisation
-// of the grid (256 CUs, one 256×256 workgroup each) plus the HBM traffic of the
-// split partials (written, read back) and of H (read for beta, written twice
-// for the mirror); padding every split to an even number of stages is counted.
+// Split count: the smallest power of two that gives at least 4096 workgroups
+// (16 waves of one 256×256 tile per CU), at most 16 splits and at least 16
+// KS-token stages per split.  Powers of two keep every split on whole XCDs
+// (the workgroup order is split-major and XCD-contiguous), so the
+// workgroups of one XCD read one K range; measured on MI355X with random
+// bf16 operands (C=4096: S=16; C=14336: S=4).
 int choose_splits(int64_t tiles, int64_t K) {
-  const double tile_elems = (double)tiles * TT * TT;
-  const int64_t smax = std::max<int64_t>(1, std::min<int64_t>(16, K / (KS * 8)));
-  int best = 1;
-  double best_t = 1e300;
-  for (int s = 1; s <= smax; ++s) {
-    const int64_t step = (int64_t)2 * KS * s;
-    const int64_t Kp = cdiv(K, step) * step;
-    const double waves = (double)(tiles * s) / 256.0;
-    const double util = waves / std::ceil(waves);
-    const double t_mma = 2.0 * tile_elems * (double)Kp / (2.0e15 * util);
-    const double bytes = tile_elems * 4.0 * (s > 1 ? 2.0 * s + 3.0 : 3.0);
-    const double t = t_mma + bytes / 6.0e12;
-    if (t < best_t * 0.98) {
-      best_t = t;
-      best = s;
-    }
-  }
-  return best;
+  const int64_t smax = std::max<int64_t>(1, std::min<int64_t>(16, K / (KS * 16)));
+  int S = 1;
+  while (S * 2 <= smax && tiles * S < 4096) S *= 2;
+  return S;
 }
 
 // Token width a split grid of S splits needs for K tokens: every split gets an
