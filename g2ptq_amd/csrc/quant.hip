@@ -392,6 +392,195 @@ __global__ __launch_bounds__(64) void sweep_kernel(SweepArgs a) {
   if (bad && act && a.flags) atomicOr(a.flags, FLAG_BAD_SCALE);
 }
 
+// Quad sweep: the same computation, with each row split over a quad of four
+// lanes (16 rows per wave).  In every 32-column panel lane `sub` of a quad
+// owns columns 4s + sub (s = 0..7).  Column jj's quantisation runs on all
+// lanes but only its owner (sub == jj % 4) holds the column, and its error
+// (and x, z) reach the other three lanes with a DPP quad broadcast; every
+// lane then applies the rank-1 update to the columns it owns.  Each element
+// still receives exactly the reference's sequence of rounded products and
+// differences, in the same order, so the results equal sweep_kernel's bit for
+// bit; the per-wave dependency chain is a quarter as long, and a block is
+// spread over four times as many waves.
+template <int O>
+__device__ __forceinline__ float quad_bcast_c(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), O * 0x55, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float quad_bcast(float v, int o) {
+  switch (o & 3) {
+    case 0: return quad_bcast_c<0>(v);
+    case 1: return quad_bcast_c<1>(v);
+    case 2: return quad_bcast_c<2>(v);
+    default: return quad_bcast_c<3>(v);
+  }
+}
+
+template <int V>
+__global__ __launch_bounds__(64) void sweep4_kernel(SweepArgs a) {
+  constexpr int PW = 32, RW = 16;  // panel width, rows per wave
+  __shared__ float Us[kTri];
+  __shared__ float Ps[(V == 1) ? kTri : 1];
+  __shared__ float e_s[kMaxBlock * RW];
+  __shared__ float t_s[(V == 1) ? kMaxBlock * RW : 1];
+  __shared__ float z_s[(V == 2) ? kMaxBlock * RW : 1];
+
+  const int lane = threadIdx.x, rr = lane >> 2, sub = lane & 3;
+  const int64_t b = blockIdx.y;
+  const int64_t r0 = (int64_t)blockIdx.x * RW + rr;
+  const bool act = r0 < a.R;
+  const int64_t r = act ? r0 : 0;
+  const int n = a.n;
+  const float minq = (float)(-(a.maxq + 1)), fmaxq = (float)a.maxq;
+
+  {
+    const float* U = a.U + b * a.ub;
+    const float* P = (V == 1) ? a.P + b * a.ub : nullptr;
+    const int nn = n * n;
+    for (int base = 0; base < nn; base += 64 * 8) {
+      float uv[8], pv[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int idx = base + q * 64 + lane;
+        const int j = idx / n, k = idx - j * n;
+        const bool need = idx < nn && k >= j;
+        uv[q] = need ? U[(int64_t)j * a.uj + k] : 0.f;
+        if (V == 1) pv[q] = need ? P[(int64_t)j * a.uj + k] : 0.f;
+      }
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int idx = base + q * 64 + lane;
+        const int j = idx / n, k = idx - j * n;
+        if (idx < nn && k >= j) {
+          Us[tri_base(j, n) + k] = uv[q];
+          if (V == 1) Ps[tri_base(j, n) + k] = pv[q];
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  const float* Win = a.W + b * a.wb + r * a.wr;
+  const float* Sp = a.S + b * a.sb + r * a.sr;
+  const float* Zp = a.Z0 + b * a.sb + r * a.sr;
+  const float* Zg = (V == 2) ? a.Zg + b * a.zb + r * a.zr : nullptr;
+  const float* GH = (V == 2) ? a.GH + b * a.gb + r * a.gr : nullptr;
+  float* GHo = (V == 2 && a.GHout) ? a.GHout + b * a.gb + r * a.gr : nullptr;
+  float* Qo = a.Q + b * a.qb + r * a.qr;
+  float* Io = a.I ? a.I + b * a.ib + r * a.ir : nullptr;
+  float* Eo = a.E ? a.E + b * a.eb + r * a.er : nullptr;
+  float* So = a.Sc ? a.Sc + b * a.cb + r * a.cr : nullptr;
+  float* E2 = (V == 2 && a.E2) ? a.E2 + b * a.e2b + r * a.e2r : nullptr;
+
+  int bad = 0;
+  float last_x = 0.f;
+
+  for (int p0 = 0; p0 < n; p0 += PW) {
+    // ---- panel inputs of the lane's 8 columns, all issued before any store --
+    float w[8], gh[8], sv[8], zv[8], zg[8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const int j = p0 + 4 * s + sub;
+      int gidx = 0;
+      if (a.colgroup) gidx = a.colgroup[j];
+      else if (a.gsize > 0) gidx = (int)((int)a.col0 + j) / (int)a.gsize;
+      sv[s] = Sp[(int64_t)gidx * a.sg];
+      zv[s] = Zp[(int64_t)gidx * a.sg];
+      w[s] = Win[(int64_t)j * a.wc];
+      if (V == 2) {
+        zg[s] = Zg[(int64_t)j * a.zc];
+        gh[s] = GH[(int64_t)j * a.gc];
+      }
+    }
+    // ---- replay updates of the columns swept in earlier panels (LDS only) ---
+    for (int j = 0; j < p0; ++j) {
+      const float e = e_s[j * RW + rr];
+      float t = 0.f, zj = 0.f;
+      if (V == 1) t = t_s[j * RW + rr];
+      if (V == 2) zj = z_s[j * RW + rr];
+      const float* Uj = Us + tri_base(j, n) + p0 + sub;
+      const float* Pj = (V == 1) ? Ps + tri_base(j, n) + p0 + sub : nullptr;
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const float u = Uj[4 * s];
+        if (V == 0) {
+          w[s] = __fsub_rn(w[s], __fmul_rn(u, e));
+        } else if (V == 1) {
+          w[s] = __fadd_rn(__fsub_rn(w[s], __fmul_rn(u, e)), __fmul_rn(Pj[4 * s], t));
+        } else {
+          w[s] = __fsub_rn(__fsub_rn(w[s], gh[s]), __fmul_rn(u, e));
+          gh[s] = __fsub_rn(gh[s], __fmul_rn(u, zj));
+        }
+      }
+    }
+    // ---- sweep the panel column by column -----------------------------------
+    float qb[8], ib[8], eb[8], gb[8];
+#pragma unroll
+    for (int jj = 0; jj < PW; ++jj) {
+      const int sl = jj >> 2, o = jj & 3;
+      const bool own = sub == o;
+      const int j = p0 + jj;
+      const float x = w[sl];  // meaningful on the owner lane
+      const float sc = sv[sl];
+      const float z0 = zv[sl];
+      const float q = clamp_nan(__fadd_rn(rintf(__fdiv_rn(x, sc)), z0), minq, fmaxq);
+      const float deq = __fmul_rn(sc, __fsub_rn(q, z0));
+      const float d = Us[tri_base(j, n) + j];
+      float err0;
+      if (V == 2) err0 = __fdiv_rn(__fsub_rn(__fsub_rn(x, deq), gh[sl]), d);
+      else err0 = __fdiv_rn(__fsub_rn(x, deq), d);
+      const float err = quad_bcast(err0, o);
+      const float xb = (V == 1 || jj == PW - 1) ? quad_bcast(x, o) : 0.f;
+      const float zj = (V == 2) ? quad_bcast(zg[sl], o) : 0.f;
+      bad |= own && !(sc > 0.f);
+      qb[sl] = own ? deq : qb[sl];
+      ib[sl] = own ? q : ib[sl];
+      eb[sl] = own ? err0 : eb[sl];
+      if (V == 2) gb[sl] = own ? gh[sl] : gb[sl];
+      if (sub == 0) {
+        e_s[j * RW + rr] = err;
+        if (V == 1) t_s[j * RW + rr] = xb;
+        if (V == 2) z_s[j * RW + rr] = zj;
+      }
+      if (jj == PW - 1) last_x = xb;
+      const float* Uj = Us + tri_base(j, n) + p0 + sub;
+      const float* Pj = (V == 1) ? Ps + tri_base(j, n) + p0 + sub : nullptr;
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        if (4 * s + 3 <= jj) continue;           // every column of the slot is done
+        const bool upd = 4 * s > jj || sub > jj - 4 * s;
+        const float u = Uj[4 * s];
+        if (V == 0) {
+          const float nw = __fsub_rn(w[s], __fmul_rn(u, err));
+          w[s] = upd ? nw : w[s];
+        } else if (V == 1) {
+          const float nw = __fadd_rn(__fsub_rn(w[s], __fmul_rn(u, err)), __fmul_rn(Pj[4 * s], xb));
+          w[s] = upd ? nw : w[s];
+        } else {
+          const float nw = __fsub_rn(__fsub_rn(w[s], gh[s]), __fmul_rn(u, err));
+          const float ng = __fsub_rn(gh[s], __fmul_rn(u, zj));
+          w[s] = upd ? nw : w[s];
+          gh[s] = upd ? ng : gh[s];
+        }
+      }
+    }
+    // ---- panel outputs ------------------------------------------------------
+    if (act) {
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const int j = p0 + 4 * s + sub;
+        Qo[(int64_t)j * a.qc] = qb[s];
+        if (Io) Io[(int64_t)j * a.ic] = ib[s];
+        if (Eo) Eo[(int64_t)j * a.ec] = eb[s];
+        if (So) So[(int64_t)j * a.cc] = sv[s];
+        if (V == 2 && E2) E2[(int64_t)j * a.e2c] = __fsub_rn(eb[s], __fmul_rn(zg[s], (float)(a.dist0 - j)));
+        if (V == 2 && GHo) GHo[(int64_t)j * a.gc] = gb[s];
+      }
+    }
+  }
+  if (V == 1 && a.CW && act && sub == 0) a.CW[b * a.cwb + r * a.cwr] = last_x;
+  if (bad && act && a.flags) atomicOr(a.flags, FLAG_BAD_SCALE);
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 // Whether every per-row operand is column-contiguous with 16-byte aligned rows.
@@ -408,6 +597,11 @@ bool sweep_vec_ok(const SweepArgs& a) {
 template <int V>
 void launch_variant(hipStream_t stream, const SweepArgs& a, dim3 grid, bool vec) {
   const bool full = (a.n % 32) == 0;
+  if (full) {
+    dim3 g4((unsigned)cdiv(a.R, (int64_t)16), grid.y);
+    hipLaunchKernelGGL((sweep4_kernel<V>), g4, dim3(64), 0, stream, a);
+    return;
+  }
   if (vec && full)
     hipLaunchKernelGGL((sweep_kernel<V, 32, true, true>), grid, dim3(64), 0, stream, a);
   else if (full)

@@ -23,6 +23,10 @@ CASES = (
     # full 128-wide blocks (four register panels) with many rows
     ("asymmetric_4bit_block128", 2, 128, 300, 7, True, 401),
     ("symmetric_3bit_block100", 1, 100, 130, 3, False, 402),
+    # 32-column multiples (the quad-per-row sweep) with ragged row counts
+    ("symmetric_4bit_block32", 3, 32, 17, 7, False, 403),
+    ("asymmetric_2bit_block64", 1, 64, 45, 1, True, 404),
+    ("symmetric_8bit_block96", 2, 96, 70, 127, False, 405),
 )
 
 
