@@ -401,7 +401,8 @@ __global__ __launch_bounds__(64) void sweep_kernel(SweepArgs a) {
 // still receives exactly the reference's sequence of rounded products and
 // differences, in the same order, so the results equal sweep_kernel's bit for
 // bit; the per-wave dependency chain is a quarter as long, and a block is
-// spread over four times as many waves.
+// spread over four times as many waves.  A workgroup of four waves (64 rows)
+// stages the block's U triangle once for all of them.
 template <int O>
 __device__ __forceinline__ float quad_bcast_c(float v) {
   return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), O * 0x55, 0xf, 0xf, false));
@@ -416,15 +417,15 @@ __device__ __forceinline__ float quad_bcast(float v, int o) {
 }
 
 template <int V>
-__global__ __launch_bounds__(64) void sweep4_kernel(SweepArgs a) {
-  constexpr int PW = 32, RW = 16;  // panel width, rows per wave
+__global__ __launch_bounds__(256) void sweep4_kernel(SweepArgs a) {
+  constexpr int PW = 32, RW = 64;  // panel width, rows per workgroup (16 per wave)
   __shared__ float Us[kTri];
   __shared__ float Ps[(V == 1) ? kTri : 1];
   __shared__ float e_s[kMaxBlock * RW];
   __shared__ float t_s[(V == 1) ? kMaxBlock * RW : 1];
   __shared__ float z_s[(V == 2) ? kMaxBlock * RW : 1];
 
-  const int lane = threadIdx.x, rr = lane >> 2, sub = lane & 3;
+  const int tid = threadIdx.x, rr = tid >> 2, sub = tid & 3;
   const int64_t b = blockIdx.y;
   const int64_t r0 = (int64_t)blockIdx.x * RW + rr;
   const bool act = r0 < a.R;
@@ -433,26 +434,54 @@ __global__ __launch_bounds__(64) void sweep4_kernel(SweepArgs a) {
   const float minq = (float)(-(a.maxq + 1)), fmaxq = (float)a.maxq;
 
   {
+    // Stage the block's upper triangle (shared by the four waves): rows of U
+    // as 16-byte chunks, all of a thread's loads in flight before its stores.
     const float* U = a.U + b * a.ub;
     const float* P = (V == 1) ? a.P + b * a.ub : nullptr;
-    const int nn = n * n;
-    for (int base = 0; base < nn; base += 64 * 8) {
-      float uv[8], pv[8];
+    const int nc = (n + 3) >> 2;              // 4-column chunks per row
+    const int total = n * nc;
+    const bool vec = ((a.uj & 3) == 0) && ((reinterpret_cast<uintptr_t>(U) & 15) == 0) &&
+                     (V != 1 || (reinterpret_cast<uintptr_t>(P) & 15) == 0);
+    for (int base = 0; base < total; base += 256 * 16) {
+      float4 uv[16], pv[16];
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const int idx = base + q * 64 + lane;
-        const int j = idx / n, k = idx - j * n;
-        const bool need = idx < nn && k >= j;
-        uv[q] = need ? U[(int64_t)j * a.uj + k] : 0.f;
-        if (V == 1) pv[q] = need ? P[(int64_t)j * a.uj + k] : 0.f;
+      for (int q = 0; q < 16; ++q) {
+        const int idx = base + q * 256 + tid;
+        const int j = idx / nc, k = (idx - j * nc) * 4;
+        float4 u = make_float4(0.f, 0.f, 0.f, 0.f), pp = u;
+        if (idx < total && k + 3 >= j) {
+          const float* pu = U + (int64_t)j * a.uj + k;
+          const float* ppp = (V == 1) ? P + (int64_t)j * a.uj + k : nullptr;
+          if (vec && k + 3 < n) {
+            u = *reinterpret_cast<const float4*>(pu);
+            if (V == 1) pp = *reinterpret_cast<const float4*>(ppp);
+          } else {
+            if (k >= j && k < n) { u.x = pu[0]; if (V == 1) pp.x = ppp[0]; }
+            if (k + 1 >= j && k + 1 < n) { u.y = pu[1]; if (V == 1) pp.y = ppp[1]; }
+            if (k + 2 >= j && k + 2 < n) { u.z = pu[2]; if (V == 1) pp.z = ppp[2]; }
+            if (k + 3 >= j && k + 3 < n) { u.w = pu[3]; if (V == 1) pp.w = ppp[3]; }
+          }
+        }
+        uv[q] = u;
+        if (V == 1) pv[q] = pp;
       }
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const int idx = base + q * 64 + lane;
-        const int j = idx / n, k = idx - j * n;
-        if (idx < nn && k >= j) {
-          Us[tri_base(j, n) + k] = uv[q];
-          if (V == 1) Ps[tri_base(j, n) + k] = pv[q];
+      for (int q = 0; q < 16; ++q) {
+        const int idx = base + q * 256 + tid;
+        const int j = idx / nc, k = (idx - j * nc) * 4;
+        if (idx >= total) continue;
+        const int t0 = tri_base(j, n);
+        const float ue[4] = {uv[q].x, uv[q].y, uv[q].z, uv[q].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (k + e >= j && k + e < n) Us[t0 + k + e] = ue[e];
+        }
+        if (V == 1) {
+          const float pe[4] = {pv[q].x, pv[q].y, pv[q].z, pv[q].w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            if (k + e >= j && k + e < n) Ps[t0 + k + e] = pe[e];
+          }
         }
       }
     }
@@ -598,8 +627,8 @@ template <int V>
 void launch_variant(hipStream_t stream, const SweepArgs& a, dim3 grid, bool vec) {
   const bool full = (a.n % 32) == 0;
   if (full) {
-    dim3 g4((unsigned)cdiv(a.R, (int64_t)16), grid.y);
-    hipLaunchKernelGGL((sweep4_kernel<V>), g4, dim3(64), 0, stream, a);
+    dim3 g4((unsigned)cdiv(a.R, (int64_t)64), grid.y);
+    hipLaunchKernelGGL((sweep4_kernel<V>), g4, dim3(256), 0, stream, a);
     return;
   }
   if (vec && full)
