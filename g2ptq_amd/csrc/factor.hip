@@ -17,13 +17,15 @@
 //      inverted; level s joins pairs of s-sized inverses with
 //      X21 = −X22·(L21·X11), each level two batched GEMMs
 //   4. un-reverse into U (upper, zeros below) with the reference's NaN check.
+#include <mutex>
+
 #include "common.hpp"
 
 namespace g2ptq {
 namespace {
 
 constexpr int NB = 64;   // diagonal block width (potrf in registers)
-constexpr int NBO = 256; // panel width of the trailing (SYRK) updates
+constexpr int NBO = 512; // panel width of the trailing (SYRK) updates
 
 __global__ void diag_sum_kernel(const float* __restrict__ H, int64_t C, const int* skip,
                                 float* sums, int* st, int* info) {
@@ -78,13 +80,12 @@ __global__ void reverse_damp_kernel(const float* __restrict__ H, int64_t C, floa
 // constant): the pivot L[j][j] is read from lane j; column j of L, scaled by
 // 1/sqrt(pivot), and the (unscaled) row j of X are published through LDS;
 // every lane applies the rank-1 updates of its own rows:
-//   L[i][c] −= L[i][j]·L[c][j]          (the column is zero for c ≤ j)
-//   X[i][c] −= L[i][j]/d_j · X[j][c]    (the row is zero for c > j)
+//   L[i][c] −= L[i][j]·L[c][j]          (c > j)
+//   X[i][c] −= L[i][j]/d_j · X[j][c]    (c ≤ j; the row is zero beyond)
 // the Gauss–Jordan elimination of [L | I] with row j's division by d_j
 // deferred: each lane scales its own X row by its pivot's reciprocal at the
-// end.  Every update runs over all 64 entries (zeros make them exact no-ops)
-// so that the published column and row are read as whole 16-byte vectors,
-// all in flight before the first update.  A single wave needs no barriers:
+// end.  The published column and row are read as whole 16-byte vectors, all
+// in flight before the first update.  A single wave needs no barriers:
 // its LDS writes and reads are processed in order.  Entries of a above the
 // diagonal accumulate values that are never read.
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void potrf_diag_kernel(
@@ -111,8 +112,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void
       fail = j + 1;
       break;
     }
-    const float d = __fsqrt_rn(djj);
-    const float rd = 1.f / d;
+    // 1/sqrt and sqrt from the hardware reciprocal square root (about 1 ulp):
+    // the factor is held to fp32 tolerance, not to correctly rounded bits, and
+    // this keeps two long correctly-rounded sequences off the pivot chain.
+    const float rd = __builtin_amdgcn_rsqf(djj);
+    const float d = djj * rd;
     const float lij = (i > j) ? a[j] * rd : 0.f;
     a[j] = (i == j) ? d : lij;
     myrd = (i == j) ? rd : myrd;
@@ -126,18 +130,20 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void
     __builtin_amdgcn_wave_barrier();
     float cl[NB], rx[NB];
 #pragma unroll
-    for (int q = 0; q < NB / 4; ++q) {
+    for (int q = j / 4; q < NB / 4; ++q) {
       const float4 u = *reinterpret_cast<const float4*>(&colL[4 * q]);
-      const float4 v = *reinterpret_cast<const float4*>(&rowX[4 * q]);
       cl[4 * q] = u.x; cl[4 * q + 1] = u.y; cl[4 * q + 2] = u.z; cl[4 * q + 3] = u.w;
+    }
+#pragma unroll
+    for (int q = 0; q <= j / 4; ++q) {
+      const float4 v = *reinterpret_cast<const float4*>(&rowX[4 * q]);
       rx[4 * q] = v.x; rx[4 * q + 1] = v.y; rx[4 * q + 2] = v.z; rx[4 * q + 3] = v.w;
     }
     const float m = lij * rd;
 #pragma unroll
-    for (int c = 0; c < NB; ++c) {
-      a[c] -= lij * cl[c];
-      x[c] -= m * rx[c];
-    }
+    for (int c = j + 1; c < NB; ++c) a[c] -= lij * cl[c];
+#pragma unroll
+    for (int c = 0; c <= j; ++c) x[c] -= m * rx[c];
     __builtin_amdgcn_wave_barrier();
   }
   if (fail) {
@@ -182,6 +188,33 @@ __global__ void unreverse_kernel(const float* __restrict__ WA, int64_t C, const 
 struct FactorWs {
   size_t wa, wt, sums, st, total;
 };
+
+// A second stream (default priority) and events per device, created once, for
+// the factor's lookahead.  Calls that overlap on one device would share them:
+// the library's entry points are not meant to run concurrently on one device.
+struct SideStream {
+  hipStream_t stream = nullptr;
+  hipEvent_t factored = nullptr;
+  hipEvent_t done[2] = {nullptr, nullptr};
+};
+
+int side_stream(SideStream& out) {
+  static std::mutex mu;
+  static SideStream cache[64];
+  int dev = 0;
+  G2PTQ_HIP(hipGetDevice(&dev));
+  G2PTQ_CHECK(dev >= 0 && dev < 64, "factor: device index %d", dev);
+  std::lock_guard<std::mutex> lock(mu);
+  SideStream& c = cache[dev];
+  if (c.stream == nullptr) {
+    G2PTQ_HIP(hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking));
+    G2PTQ_HIP(hipEventCreateWithFlags(&c.factored, hipEventDisableTiming));
+    G2PTQ_HIP(hipEventCreateWithFlags(&c.done[0], hipEventDisableTiming));
+    G2PTQ_HIP(hipEventCreateWithFlags(&c.done[1], hipEventDisableTiming));
+  }
+  out = c;
+  return G2PTQ_OK;
+}
 
 FactorWs factor_ws(int64_t B, int64_t C) {
   FactorWs w;
@@ -231,11 +264,12 @@ extern "C" int g2ptq_inv_chol_upper(void* stream, const float* H, int64_t B, int
 
   // Blocked Cholesky of Â (lower) with inverted diagonal blocks, two levels:
   // panels of NBO columns are factored NB columns at a time (potrf + TRSM +
-  // update of the panel's own remaining columns), then the trailing matrix
-  // receives the whole panel in one SYRK with K = NBO instead of NBO/NB
-  // passes with K = NB (a quarter of the trailing-matrix traffic).
-  for (int64_t k = 0; k < C; k += NBO) {
-    const int64_t kb = std::min<int64_t>(NBO, C - k);
+  // update of the panel's own remaining columns), and the trailing matrix
+  // receives each whole panel in one SYRK with K = NBO.  Lookahead of one
+  // panel: the trailing update beyond the next panel runs on a second stream
+  // while the next panel (updated first, on the caller's stream) is factored,
+  // so the latency-bound panel chain overlaps the bandwidth/MFMA-bound SYRK.
+  auto factor_panel = [&](int64_t k, int64_t kb) -> int {
     for (int64_t j = k; j < k + kb; j += NB) {
       const int nbk = (int)std::min<int64_t>(NB, k + kb - j);
       hipLaunchKernelGGL(potrf_diag_kernel, dim3((unsigned)B), dim3(64), 0, s, WA, C, j, nbk,
@@ -261,17 +295,45 @@ extern "C" int g2ptq_inv_chol_upper(void* stream, const float* H, int64_t B, int
       y.alpha = -1.f; y.beta = 1.f; y.uplo = 1; y.skip = st;
       G2PTQ_TRY(gemm_f32(s, y));
     }
-    const int64_t rest = C - k - kb;
-    if (rest <= 0) break;
-    GemmF32 y;  // trailing ← trailing − panel · panelᵀ (lower), K = panel width
-    y.M = rest; y.N = rest; y.K = kb; y.batch = B;
-    y.A = WA + (k + kb) * C + k; y.lda = C; y.sA = CC;
-    y.B = WA + (k + kb) * C + k; y.ldb = C; y.sB = CC; y.b_kcontig = 1;
-    y.C = WA + (k + kb) * C + (k + kb); y.ldc = C; y.sC = CC;
-    y.D = WA + (k + kb) * C + (k + kb); y.ldd = C; y.sD = CC;
+    return G2PTQ_OK;
+  };
+  // Rows [c0, C) × columns [c0, c1) (lower part) −= panel [k, k + kb) contribution.
+  auto syrk = [&](hipStream_t q, int64_t k, int64_t kb, int64_t c0, int64_t c1) -> int {
+    GemmF32 y;
+    y.M = C - c0; y.N = c1 - c0; y.K = kb; y.batch = B;
+    y.A = WA + c0 * C + k; y.lda = C; y.sA = CC;
+    y.B = WA + c0 * C + k; y.ldb = C; y.sB = CC; y.b_kcontig = 1;
+    y.C = WA + c0 * C + c0; y.ldc = C; y.sC = CC;
+    y.D = WA + c0 * C + c0; y.ldd = C; y.sD = CC;
     y.alpha = -1.f; y.beta = 1.f; y.uplo = 1; y.skip = st;
-    G2PTQ_TRY(gemm_f32(s, y));
+    return gemm_f32(q, y);
+  };
+  SideStream side;
+  G2PTQ_TRY(side_stream(side));
+  G2PTQ_TRY(factor_panel(0, std::min<int64_t>(NBO, C)));
+  int pend = -1;  // ping-pong slot of the latest trailing update on the side stream
+  for (int64_t k = 0, p = 0; k < C; k += NBO, ++p) {
+    const int64_t kb = std::min<int64_t>(NBO, C - k);
+    const int64_t next = k + kb;
+    if (next >= C) break;
+    const int64_t nb2 = std::min<int64_t>(NBO, C - next);
+    if (next + nb2 < C) {  // trailing part beyond the next panel, on the side stream
+      G2PTQ_HIP(hipEventRecord(side.factored, s));
+      G2PTQ_HIP(hipStreamWaitEvent(side.stream, side.factored, 0));
+      G2PTQ_TRY(syrk(side.stream, k, kb, next + nb2, C));
+    }
+    // The next panel's columns also received the previous trailing update.
+    if (pend >= 0) G2PTQ_HIP(hipStreamWaitEvent(s, side.done[pend], 0));
+    if (next + nb2 < C) {
+      pend = (int)(p & 1);
+      G2PTQ_HIP(hipEventRecord(side.done[pend], side.stream));
+    } else {
+      pend = -1;
+    }
+    G2PTQ_TRY(syrk(s, k, kb, next, next + nb2));
+    G2PTQ_TRY(factor_panel(next, nb2));
   }
+  if (pend >= 0) G2PTQ_HIP(hipStreamWaitEvent(s, side.done[pend], 0));
 
   // Triangular inverse by recursive doubling (diagonal NB blocks already inverted).
   for (int64_t sz = NB; sz < C; sz *= 2) {
