@@ -37,54 +37,58 @@ constexpr int NTH = 512;  // threads per workgroup (8 waves)
 __device__ __forceinline__ int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
 // X (T × C, ld ldx) → XT[c][t_off + t] for t < roundup(T, 64), zero padded in
-// both directions up to the 64-token / Cp-feature grid.  One workgroup moves a
-// 128-token × 64-feature block: 16-byte row loads, an LDS transpose, and
-// 16-byte loads/stores of 8 consecutive tokens per feature row.
-constexpr int ST_T = 128, ST_C = 64, ST_PAD = 8;
+// both directions up to the 64-token / Cp-feature grid.  No LDS: each thread
+// loads an 8-token × 8-feature block (eight 16-byte row pieces), transposes
+// it in registers with byte permutes, and stores eight 16-byte pieces of
+// feature rows.  A wave covers 64 tokens × 64 features; the 8 lanes sharing a
+// token row (or a feature row) touch one contiguous 128-byte segment.
+constexpr int ST_T = 64, ST_C = 256;  // tokens × features per workgroup (4 waves)
+
+// Low / high 16-bit halves of two words → one word (v_perm_b32 selectors).
+__device__ __forceinline__ uint32_t lo_lo(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x05040100u);
+}
+__device__ __forceinline__ uint32_t hi_hi(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x07060302u);
+}
+
 __global__ __launch_bounds__(256) void stage_kernel(const uint16_t* __restrict__ X, int64_t T,
                                                     int64_t C, int64_t ldx,
                                                     uint16_t* __restrict__ XT, int64_t ldt,
                                                     int64_t t_off, int64_t t_end, int vec) {
-  __shared__ __attribute__((aligned(16))) uint16_t tile[ST_T][ST_C + ST_PAD];
-  const int64_t t0 = (int64_t)blockIdx.x * ST_T, c0 = (int64_t)blockIdx.y * ST_C;
-  const int tid = threadIdx.x;
-  {
-    const int chunk = tid & 7, r0 = tid >> 3;  // 8 chunks of 8 features per token row
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int tb = lane >> 3, fb = lane & 7;
+  const int64_t t0 = (int64_t)blockIdx.x * ST_T + tb * 8;
+  const int64_t f0 = (int64_t)blockIdx.y * ST_C + wave * 64 + fb * 8;
+  // r[i] = features f0..f0+7 of token t0+i (4 words, 2 bf16 each)
+  uint32_t r[8][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = r0 + 32 * i;
-      const int64_t t = t0 + r, c = c0 + chunk * 8;
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (t < T) {
-        if (vec && c + 8 <= C) {
-          v = *reinterpret_cast<const uint4*>(X + t * ldx + c);
-        } else {
-          uint16_t e[8];
+  for (int i = 0; i < 8; ++i) {
+    const int64_t t = t0 + i;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (t < T) {
+      if (vec && f0 + 8 <= C) {
+        v = *reinterpret_cast<const uint4*>(X + t * ldx + f0);
+      } else {
+        uint16_t e[8];
 #pragma unroll
-          for (int k = 0; k < 8; ++k) e[k] = (c + k < C) ? X[t * ldx + c + k] : (uint16_t)0;
-          v.x = e[0] | ((uint32_t)e[1] << 16); v.y = e[2] | ((uint32_t)e[3] << 16);
-          v.z = e[4] | ((uint32_t)e[5] << 16); v.w = e[6] | ((uint32_t)e[7] << 16);
-        }
+        for (int k = 0; k < 8; ++k) e[k] = (f0 + k < C) ? X[t * ldx + f0 + k] : (uint16_t)0;
+        v.x = e[0] | ((uint32_t)e[1] << 16); v.y = e[2] | ((uint32_t)e[3] << 16);
+        v.z = e[4] | ((uint32_t)e[5] << 16); v.w = e[6] | ((uint32_t)e[7] << 16);
       }
-      *reinterpret_cast<uint4*>(&tile[r][chunk * 8]) = v;
     }
+    r[i][0] = v.x; r[i][1] = v.y; r[i][2] = v.z; r[i][3] = v.w;
   }
-  __syncthreads();
-  {
-    const int tc = tid & 15, f0 = tid >> 4;  // 16 chunks of 8 tokens per feature row
+  if (t0 >= t_end) return;  // t_end is a multiple of 8
+  // Output row f0 + 2w (+1): tokens t0..t0+7 = low (high) halves of r[0..7][w].
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int f = f0 + 16 * i;
-      const int64_t t = t0 + tc * 8;
-      if (t >= t_end) continue;  // t_end is a multiple of 8 (the 64-token grid)
-      uint16_t e[8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) e[k] = tile[tc * 8 + k][f];
-      uint4 v;
-      v.x = e[0] | ((uint32_t)e[1] << 16); v.y = e[2] | ((uint32_t)e[3] << 16);
-      v.z = e[4] | ((uint32_t)e[5] << 16); v.w = e[6] | ((uint32_t)e[7] << 16);
-      *reinterpret_cast<uint4*>(XT + (c0 + f) * ldt + t_off + t) = v;
-    }
+  for (int w = 0; w < 4; ++w) {
+    const uint4 even = make_uint4(lo_lo(r[0][w], r[1][w]), lo_lo(r[2][w], r[3][w]),
+                                  lo_lo(r[4][w], r[5][w]), lo_lo(r[6][w], r[7][w]));
+    const uint4 odd = make_uint4(hi_hi(r[0][w], r[1][w]), hi_hi(r[2][w], r[3][w]),
+                                 hi_hi(r[4][w], r[5][w]), hi_hi(r[6][w], r[7][w]));
+    *reinterpret_cast<uint4*>(XT + (f0 + 2 * w) * ldt + t_off + t0) = even;
+    *reinterpret_cast<uint4*>(XT + (f0 + 2 * w + 1) * ldt + t_off + t0) = odd;
   }
 }
 
@@ -472,7 +476,7 @@ int gram_stage(hipStream_t st, const uint16_t* X, int64_t T, int64_t C, int64_t 
   const int vec = (ldx % 8 == 0) && ((reinterpret_cast<uintptr_t>(X) & 15) == 0);
   G2PTQ_CHECK(ldt % 8 == 0 && t_off % 8 == 0 && (reinterpret_cast<uintptr_t>(XT) & 15) == 0,
               "hessian stage: XT must be 16-byte aligned with ldt and t_off multiples of 8");
-  dim3 grid((unsigned)cdiv(T, ST_T), (unsigned)(Cp / ST_C));
+  dim3 grid((unsigned)cdiv(T, (int64_t)ST_T), (unsigned)(Cp / ST_C));
   hipLaunchKernelGGL(stage_kernel, grid, dim3(256), 0, st, X, T, C, ldx, XT, ldt, t_off, T64, vec);
   G2PTQ_LAUNCHED();
   return G2PTQ_OK;
