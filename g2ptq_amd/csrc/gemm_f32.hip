@@ -7,8 +7,8 @@
 // compensation sweep, the Cholesky TRSM/SYRK steps, the triangular-inverse
 // levels, GPTAQ's P and the G2PTQ trust-region products.
 //
-// Shape: a workgroup (4 wave64s, two per CU) computes a 128×128 tile; each
-// wave a 64×64 quadrant as 2×2 blocks of 32×32 MFMA accumulators.  K advances
+// Shape: a workgroup (4 wave64s, two per CU) computes a 128×128 tile (64×64
+// for small grids); each wave a quadrant made of 32×32 MFMA blocks.  K advances
 // in slabs of 32 through double-buffered LDS with 16-byte global loads for
 // two slabs in flight, interleaved with the MFMAs of the current slab.
 //
@@ -27,11 +27,8 @@ namespace {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int BM = 128, BN = 128, BK = 32;
+constexpr int BK = 32;
 constexpr int PK = 36;   // [row][k] pitch (floats)
-constexpr int PN = 136;  // [k][n] pitch (floats)
-constexpr int LDS_A = BM * PK;
-constexpr int LDS_B = (BN * PK > BK * PN) ? BN * PK : BK * PN;
 constexpr int GH = 8;    // tile-rows per group of the tile order
 
 // Tile id → (tm, tn): groups of GH tile-rows walked column by column.
@@ -45,8 +42,19 @@ __device__ __forceinline__ void tile_of(int64_t id, int64_t tm, int64_t tn, int6
   in = r / h;
 }
 
-template <bool B_KCONTIG, bool VEC>
+// TILE × TILE output per workgroup (4 waves in 2×2, each TILE/2 square made
+// of 32×32 MFMA blocks): 128 for large products, 64 when a 128 grid would
+// leave most CUs idle (the factor's TRSM / panel updates, short tails).
+template <int TILE, bool B_KCONTIG, bool VEC>
 __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmF32 g, int64_t tm, int64_t tn) {
+  constexpr int BM = TILE, BN = TILE;
+  constexpr int PN = BN + 8;                       // [k][n] pitch (floats)
+  constexpr int LDS_A = BM * PK;
+  constexpr int LDS_B = (BN * PK > BK * PN) ? BN * PK : BK * PN;
+  constexpr int WT = TILE / 2, NBLK = WT / 32;     // wave tile, 32×32 blocks per side
+  constexpr int RA = BM / 32;                      // float4 per thread per slab (A)
+  constexpr int KQ = BN / 4, RB_ROWS = 256 / KQ;   // B as K×N: n-quads per k row, k rows per pass
+  constexpr int RB = BN / 32;                      // float4 per thread per slab (B)
   __shared__ __attribute__((aligned(16))) float As[2][LDS_A];
   __shared__ __attribute__((aligned(16))) float Bs[2][LDS_B];
 
@@ -76,11 +84,11 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmF32 g, int64_t tm,
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
 
-  // Global → register mapping (4 float4 per operand per slab per thread).
+  // Global → register mapping.
   //   [row][k] operands: row = tid/8 + 32 i, k-quad = tid % 8.
-  //   B as K×N:          k = tid/32 + 8 i,   n-quad = tid % 32.
+  //   B as K×N:          k = tid/KQ + RB_ROWS i, n-quad = tid % KQ.
   const int ra_row = tid >> 3, ra_kq = (tid & 7) * 4;
-  const int rb_k = tid >> 5, rb_nq = (tid & 31) * 4;
+  const int rb_k = tid / KQ, rb_nq = (tid % KQ) * 4;
 
   auto ld4 = [&](const float* base, int64_t ld, int64_t r, int64_t c, int64_t R, int64_t Ccols) {
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -104,78 +112,58 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmF32 g, int64_t tm,
     return v;
   };
 
-  // Register sets x / y hold one slab each (macros keep them in registers).
-  float4 xa0, xa1, xa2, xa3, xb0, xb1, xb2, xb3;
-  float4 ya0, ya1, ya2, ya3, yb0, yb1, yb2, yb3;
-#define GF_LOAD(R, slab)                                                                       \
+  // Register sets x / y hold one slab each (indices are compile-time constants).
+  float4 xa[RA], xb[RB], ya[RA], yb[RB];
+#define GF_LOAD(RAr, RBr, slab)                                                                \
   do {                                                                                         \
     const int64_t k0_ = klo + (int64_t)(slab) * BK;                                            \
-    R##a0 = ld4(A, g.lda, m0 + ra_row, k0_ + ra_kq, M, K);                                      \
-    R##a1 = ld4(A, g.lda, m0 + ra_row + 32, k0_ + ra_kq, M, K);                                 \
-    R##a2 = ld4(A, g.lda, m0 + ra_row + 64, k0_ + ra_kq, M, K);                                 \
-    R##a3 = ld4(A, g.lda, m0 + ra_row + 96, k0_ + ra_kq, M, K);                                 \
-    if (B_KCONTIG) {                                                                           \
-      R##b0 = ld4(B, g.ldb, n0 + ra_row, k0_ + ra_kq, N, K);                                    \
-      R##b1 = ld4(B, g.ldb, n0 + ra_row + 32, k0_ + ra_kq, N, K);                               \
-      R##b2 = ld4(B, g.ldb, n0 + ra_row + 64, k0_ + ra_kq, N, K);                               \
-      R##b3 = ld4(B, g.ldb, n0 + ra_row + 96, k0_ + ra_kq, N, K);                               \
-    } else {                                                                                   \
-      R##b0 = ld4(B, g.ldb, k0_ + rb_k, n0 + rb_nq, K, N);                                      \
-      R##b1 = ld4(B, g.ldb, k0_ + rb_k + 8, n0 + rb_nq, K, N);                                  \
-      R##b2 = ld4(B, g.ldb, k0_ + rb_k + 16, n0 + rb_nq, K, N);                                 \
-      R##b3 = ld4(B, g.ldb, k0_ + rb_k + 24, n0 + rb_nq, K, N);                                 \
+    _Pragma("unroll") for (int i_ = 0; i_ < RA; ++i_)                                          \
+      RAr[i_] = ld4(A, g.lda, m0 + ra_row + 32 * i_, k0_ + ra_kq, M, K);                       \
+    _Pragma("unroll") for (int i_ = 0; i_ < RB; ++i_) {                                        \
+      if (B_KCONTIG) RBr[i_] = ld4(B, g.ldb, n0 + ra_row + 32 * i_, k0_ + ra_kq, N, K);         \
+      else RBr[i_] = ld4(B, g.ldb, k0_ + rb_k + RB_ROWS * i_, n0 + rb_nq, K, N);                \
     }                                                                                          \
   } while (0)
-#define GF_STORE(R, buf)                                                                       \
+#define GF_STORE(RAr, RBr, buf)                                                                \
   do {                                                                                         \
-    float* la = &As[(buf)][ra_row * PK + ra_kq];                                               \
-    *reinterpret_cast<float4*>(la) = R##a0;                                                    \
-    *reinterpret_cast<float4*>(la + 32 * PK) = R##a1;                                          \
-    *reinterpret_cast<float4*>(la + 64 * PK) = R##a2;                                          \
-    *reinterpret_cast<float4*>(la + 96 * PK) = R##a3;                                          \
-    if (B_KCONTIG) {                                                                           \
-      float* lb = &Bs[(buf)][ra_row * PK + ra_kq];                                             \
-      *reinterpret_cast<float4*>(lb) = R##b0;                                                  \
-      *reinterpret_cast<float4*>(lb + 32 * PK) = R##b1;                                        \
-      *reinterpret_cast<float4*>(lb + 64 * PK) = R##b2;                                        \
-      *reinterpret_cast<float4*>(lb + 96 * PK) = R##b3;                                        \
-    } else {                                                                                   \
-      float* lb = &Bs[(buf)][rb_k * PN + rb_nq];                                               \
-      *reinterpret_cast<float4*>(lb) = R##b0;                                                  \
-      *reinterpret_cast<float4*>(lb + 8 * PN) = R##b1;                                         \
-      *reinterpret_cast<float4*>(lb + 16 * PN) = R##b2;                                        \
-      *reinterpret_cast<float4*>(lb + 24 * PN) = R##b3;                                        \
+    _Pragma("unroll") for (int i_ = 0; i_ < RA; ++i_)                                          \
+      *reinterpret_cast<float4*>(&As[(buf)][(ra_row + 32 * i_) * PK + ra_kq]) = RAr[i_];       \
+    _Pragma("unroll") for (int i_ = 0; i_ < RB; ++i_) {                                        \
+      if (B_KCONTIG)                                                                           \
+        *reinterpret_cast<float4*>(&Bs[(buf)][(ra_row + 32 * i_) * PK + ra_kq]) = RBr[i_];     \
+      else                                                                                     \
+        *reinterpret_cast<float4*>(&Bs[(buf)][(rb_k + RB_ROWS * i_) * PN + rb_nq]) = RBr[i_];  \
     }                                                                                          \
   } while (0)
 
-  f32x16 acc[2][2];
+  f32x16 acc[NBLK][NBLK];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < NBLK; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < NBLK; ++j)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
 
   const int lr = lane & 31, lh = lane >> 5;
-  // One slab: 4 k-octets × (2×2 blocks × 4 MFMAs).
+  // One slab: 4 k-octets × (NBLK×NBLK blocks × 4 MFMAs).
 #define GF_MMA(buf)                                                                            \
   do {                                                                                         \
     const float* as_ = As[(buf)];                                                              \
     const float* bs_ = Bs[(buf)];                                                              \
     _Pragma("unroll") for (int o = 0; o < BK / 8; ++o) {                                       \
-      float4 av[2], bv[2];                                                                     \
-      _Pragma("unroll") for (int i = 0; i < 2; ++i)                                            \
-        av[i] = *reinterpret_cast<const float4*>(as_ + (wm * 64 + i * 32 + lr) * PK + o * 8 + lh * 4); \
-      _Pragma("unroll") for (int j = 0; j < 2; ++j) {                                          \
+      float4 av[NBLK], bv[NBLK];                                                               \
+      _Pragma("unroll") for (int i = 0; i < NBLK; ++i)                                         \
+        av[i] = *reinterpret_cast<const float4*>(as_ + (wm * WT + i * 32 + lr) * PK + o * 8 + lh * 4); \
+      _Pragma("unroll") for (int j = 0; j < NBLK; ++j) {                                       \
         if (B_KCONTIG) {                                                                       \
-          bv[j] = *reinterpret_cast<const float4*>(bs_ + (wn * 64 + j * 32 + lr) * PK + o * 8 + lh * 4); \
+          bv[j] = *reinterpret_cast<const float4*>(bs_ + (wn * WT + j * 32 + lr) * PK + o * 8 + lh * 4); \
         } else {                                                                               \
-          const float* pb_ = bs_ + (o * 8 + lh * 4) * PN + wn * 64 + j * 32 + lr;            \
+          const float* pb_ = bs_ + (o * 8 + lh * 4) * PN + wn * WT + j * 32 + lr;            \
           bv[j] = make_float4(pb_[0], pb_[PN], pb_[2 * PN], pb_[3 * PN]);                      \
         }                                                                                      \
       }                                                                                        \
-      _Pragma("unroll") for (int i = 0; i < 2; ++i)                                            \
-      _Pragma("unroll") for (int j = 0; j < 2; ++j) {                                          \
+      _Pragma("unroll") for (int i = 0; i < NBLK; ++i)                                         \
+      _Pragma("unroll") for (int j = 0; j < NBLK; ++j) {                                       \
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i].x, bv[j].x, acc[i][j], 0, 0, 0); \
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i].y, bv[j].y, acc[i][j], 0, 0, 0); \
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i].z, bv[j].z, acc[i][j], 0, 0, 0); \
@@ -189,23 +177,23 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmF32 g, int64_t tm,
   const int nk = K > klo ? (int)cdiv(K - klo, (int64_t)BK) : 0;
   const int nk2 = (nk + 1) & ~1;
   if (nk2 > 0) {
-    GF_LOAD(x, 0);
-    GF_STORE(x, 0);
-    GF_LOAD(x, 1);
-    GF_LOAD(y, 2);
+    GF_LOAD(xa, xb, 0);
+    GF_STORE(xa, xb, 0);
+    GF_LOAD(xa, xb, 1);
+    GF_LOAD(ya, yb, 2);
   }
   __syncthreads();
   for (int kt = 0; kt < nk2; kt += 2) {
     __builtin_amdgcn_sched_barrier(0);
-    GF_MMA(0);          // slab kt
-    GF_STORE(x, 1);     // slab kt+1
-    GF_LOAD(x, kt + 3);
+    GF_MMA(0);              // slab kt
+    GF_STORE(xa, xb, 1);    // slab kt+1
+    GF_LOAD(xa, xb, kt + 3);
     __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
-    GF_MMA(1);          // slab kt+1
-    GF_STORE(y, 0);     // slab kt+2
-    GF_LOAD(y, kt + 4);
+    GF_MMA(1);              // slab kt+1
+    GF_STORE(ya, yb, 0);    // slab kt+2
+    GF_LOAD(ya, yb, kt + 4);
     __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
   }
@@ -216,34 +204,33 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmF32 g, int64_t tm,
 
   // Epilogue.  32×32 MFMA output: lane holds rows 8*(v/4) + 4*(lane/32) + v%4,
   // column lane%32.  C / X may alias D (in-place updates), so the inputs of a
-  // half tile (32 per lane) are loaded before any of its outputs is stored:
-  // two memory round trips per lane instead of one per element.
+  // row of blocks (16·NBLK per lane) are loaded before any of its outputs is
+  // stored: NBLK memory round trips per lane instead of one per element.
   const float* C = g.C ? g.C + b1 * g.sC + b2 * g.sC2 : nullptr;
   const float* X = g.X ? g.X + b1 * g.sX + b2 * g.sX2 : nullptr;
   float* D = g.D + b1 * g.sD + b2 * g.sD2;
   const bool use_c = g.beta != 0.f, use_x = g.gamma != 0.f;
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    float cv[2][16];
+  for (int i = 0; i < NBLK; ++i) {
+    float cv[NBLK][16];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int64_t n = n0 + wn * 64 + j * 32 + lr;
+    for (int j = 0; j < NBLK; ++j) {
+      const int64_t n = n0 + wn * WT + j * 32 + lr;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const int64_t m = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+        const int64_t m = m0 + wm * WT + i * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
         const bool in = m < M && n < N;
-        float c = (use_c && in) ? C[m * g.ldc + n] : 0.f;
-        cv[j][v] = c;
+        cv[j][v] = (use_c && in) ? C[m * g.ldc + n] : 0.f;
       }
     }
     if (use_x) {
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int64_t n = n0 + wn * 64 + j * 32 + lr;
+      for (int j = 0; j < NBLK; ++j) {
+        const int64_t n = n0 + wn * WT + j * 32 + lr;
         float xv[16];
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
-          const int64_t m = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+          const int64_t m = m0 + wm * WT + i * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
           xv[v] = (m < M && n < N) ? X[m * g.ldx + n] : 0.f;
         }
 #pragma unroll
@@ -251,22 +238,39 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmF32 g, int64_t tm,
       }
     } else {
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < NBLK; ++j)
 #pragma unroll
         for (int v = 0; v < 16; ++v) cv[j][v] = g.beta * cv[j][v];
     }
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int64_t n = n0 + wn * 64 + j * 32 + lr;
+    for (int j = 0; j < NBLK; ++j) {
+      const int64_t n = n0 + wn * WT + j * 32 + lr;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const int64_t m = m0 + wm * 64 + i * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+        const int64_t m = m0 + wm * WT + i * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
         if (m >= M || n >= N) continue;
         if (g.uplo == 1 && n > m) continue;
         if (g.uplo == 2 && m > n) continue;
         D[m * g.ldd + n] = g.alpha * acc[i][j][v] + cv[j][v];
       }
     }
+  }
+}
+
+template <int TILE>
+void launch_gemm(hipStream_t stream, const GemmF32& g, bool vec, int64_t nz) {
+  const int64_t tm = cdiv(g.M, (int64_t)TILE), tn = cdiv(g.N, (int64_t)TILE);
+  dim3 grid((unsigned)(tm * tn), 1, (unsigned)nz);
+  if (g.b_kcontig) {
+    if (vec)
+      hipLaunchKernelGGL((gemm_f32_kernel<TILE, true, true>), grid, dim3(256), 0, stream, g, tm, tn);
+    else
+      hipLaunchKernelGGL((gemm_f32_kernel<TILE, true, false>), grid, dim3(256), 0, stream, g, tm, tn);
+  } else {
+    if (vec)
+      hipLaunchKernelGGL((gemm_f32_kernel<TILE, false, true>), grid, dim3(256), 0, stream, g, tm, tn);
+    else
+      hipLaunchKernelGGL((gemm_f32_kernel<TILE, false, false>), grid, dim3(256), 0, stream, g, tm, tn);
   }
 }
 
@@ -280,27 +284,20 @@ int gemm_f32(hipStream_t stream, const GemmF32& g) {
   G2PTQ_CHECK(g.D != nullptr, "gemm_f32: null D");
   G2PTQ_CHECK(g.beta == 0.f || g.C != nullptr, "gemm_f32: beta != 0 needs C");
   G2PTQ_CHECK(g.gamma == 0.f || g.X != nullptr, "gemm_f32: gamma != 0 needs X");
-  const int64_t tm = cdiv(g.M, (int64_t)BM), tn = cdiv(g.N, (int64_t)BN);
   const int64_t nz = g.batch * g.batch2;
-  G2PTQ_CHECK(tm * tn < (1ll << 31) && nz < 65536, "gemm_f32: grid too large");
+  const int64_t t128 = cdiv(g.M, (int64_t)128) * cdiv(g.N, (int64_t)128);
+  G2PTQ_CHECK(cdiv(g.M, (int64_t)64) * cdiv(g.N, (int64_t)64) < (1ll << 31) && nz < 65536,
+              "gemm_f32: grid too large");
   // 16-byte operand loads need 16-byte aligned rows (every batch entry too).
   auto al = [](const void* p, int64_t ld, int64_t s1, int64_t s2) {
     return p == nullptr || ((reinterpret_cast<uintptr_t>(p) & 15) == 0 && ld % 4 == 0 &&
                             s1 % 4 == 0 && s2 % 4 == 0);
   };
   const bool vec = al(g.A, g.lda, g.sA, g.sA2) && al(g.B, g.ldb, g.sB, g.sB2);
-  dim3 grid((unsigned)(tm * tn), 1, (unsigned)nz);
-  if (g.b_kcontig) {
-    if (vec)
-      hipLaunchKernelGGL((gemm_f32_kernel<true, true>), grid, dim3(256), 0, stream, g, tm, tn);
-    else
-      hipLaunchKernelGGL((gemm_f32_kernel<true, false>), grid, dim3(256), 0, stream, g, tm, tn);
-  } else {
-    if (vec)
-      hipLaunchKernelGGL((gemm_f32_kernel<false, true>), grid, dim3(256), 0, stream, g, tm, tn);
-    else
-      hipLaunchKernelGGL((gemm_f32_kernel<false, false>), grid, dim3(256), 0, stream, g, tm, tn);
-  }
+  // 128×128 tiles unless that grid would leave most of the 256 CUs (two
+  // workgroups each) idle.
+  if (t128 * nz >= 512) launch_gemm<128>(stream, g, vec, nz);
+  else launch_gemm<64>(stream, g, vec, nz);
   G2PTQ_LAUNCHED();
   return G2PTQ_OK;
 }

@@ -51,6 +51,8 @@ def _gemm(dev, M, N, K, batch, b_trans, alpha, beta, seed):
 @pytest.mark.parametrize("M,N,K,batch,b_trans", [
     (16, 16, 4, 1, 0), (128, 128, 16, 1, 0), (129, 77, 33, 2, 0), (300, 260, 128, 1, 1),
     (5, 7, 3, 3, 1), (256, 512, 256, 2, 0),
+    # grids of >= 512 128-wide tiles take the 128×128 kernel, the rest 64×64
+    (3000, 2900, 40, 1, 1), (2200, 2100, 36, 2, 0),
 ])
 def test_gemm_f32_matches_fp64(dev, M, N, K, batch, b_trans):
     D, ref = _gemm(dev, M, N, K, batch, b_trans, -1.0, 1.0, 7 + M + N + K)
