@@ -91,7 +91,7 @@ def as_bf16_tokens(inp):
 def hessian_update(H, X, alpha, beta):
     """H = beta·H + alpha·XᵀX for one layer's (C, C) Hessian."""
     T, C = X.shape
-    nbytes = _lib.query_size("g2ptq_hessian_workspace", T, C, 0)
+    nbytes = _lib.query_size("g2ptq_hessian_workspace", T, C, 0, 0)
     ws = _lib.workspace(nbytes, X.device)
     _lib.call("g2ptq_hessian_update", stream(), _lib.ptr(X), T, C, C, f32(alpha), f32(beta),
               _lib.ptr(H), C, _lib.ptr(ws), ws.numel())
@@ -99,7 +99,7 @@ def hessian_update(H, X, alpha, beta):
 
 def gptaq_update(H, Dx, X, Xfp, alpha, beta):
     T, C = X.shape
-    nbytes = _lib.query_size("g2ptq_hessian_workspace", T, C, 1)
+    nbytes = _lib.query_size("g2ptq_hessian_workspace", T, C, 1, 0)
     ws = _lib.workspace(nbytes, X.device)
     _lib.call("g2ptq_gptaq_update", stream(), _lib.ptr(X), _lib.ptr(Xfp), T, C, C, C, f32(alpha),
               f32(beta), _lib.ptr(H), _lib.ptr(Dx), C, _lib.ptr(ws), ws.numel())
@@ -110,7 +110,7 @@ def weighted_update(Hg, X, S, alpha, beta, act, act_alpha, act_beta):
     T, C = X.shape
     G = S.shape[1]
     S = S.float().contiguous()
-    nbytes = _lib.query_size("g2ptq_hessian_workspace", T, C, 2)
+    nbytes = _lib.query_size("g2ptq_hessian_workspace", T, C, 2, G)
     ws = _lib.workspace(nbytes, X.device)
     _lib.call("g2ptq_weighted_hessian_update", stream(), _lib.ptr(X), T, C, C, _lib.ptr(S), G, G,
               f32(alpha), f32(beta), _lib.ptr(Hg), C, C * C, _lib.ptr(act), f32(act_alpha),

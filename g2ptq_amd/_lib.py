@@ -27,15 +27,22 @@ SIGNATURES = {
     "g2ptq_find_params": [_p, _p, _i64, _i64, _i64, _i32, _i32, _p, _p, _i64, _p],
     "g2ptq_find_params_mse": [_p, _p, _i64, _i64, _i64, _i32, _i32, _f32, _i32, _f32, _p, _p, _i64, _p],
     "g2ptq_fake_quantize": [_p, _p, _i64, _i64, _i64, _i64, _p, _p, _i64, _i32, _p, _i64, _p, _i64, _p],
-    "g2ptq_hessian_workspace": [_i64, _i64, _i32, _szp],
+    "g2ptq_hessian_workspace": [_i64, _i64, _i32, _i64, _szp],
     "g2ptq_hessian_update": [_p, _p, _i64, _i64, _i64, _f32, _f32, _p, _i64, _p, _sz],
     "g2ptq_hessian_stage_rows": [_i64, ctypes.POINTER(ctypes.c_int64)],
     "g2ptq_hessian_stage": [_p, _p, _i64, _i64, _i64, _p, _i64, _i64],
     "g2ptq_hessian_gram_workspace": [_i64, _i64, _szp],
     "g2ptq_hessian_gram": [_p, _p, _i64, _i64, _i64, _f32, _f32, _p, _i64, _p, _sz],
     "g2ptq_gptaq_update": [_p, _p, _p, _i64, _i64, _i64, _i64, _f32, _f32, _p, _p, _i64, _p, _sz],
+    "g2ptq_gptaq_stage": [_p, _p, _p, _i64, _i64, _i64, _i64, _p, _i64, _i64],
+    "g2ptq_gptaq_gram_workspace": [_i64, _i64, _szp],
+    "g2ptq_gptaq_gram": [_p, _p, _i64, _i64, _i64, _f32, _f32, _p, _p, _i64, _p, _sz],
     "g2ptq_weighted_hessian_update": [_p, _p, _i64, _i64, _i64, _p, _i64, _i64, _f32, _f32, _p, _i64,
                                       _i64, _p, _f32, _f32, _p, _sz],
+    "g2ptq_weighted_stage": [_p, _p, _i64, _i64, _i64, _p, _i64, _i64, _f32, _p, _i64, _i64, _p, _f32,
+                             _f32],
+    "g2ptq_weighted_gram_workspace": [_i64, _i64, _szp],
+    "g2ptq_weighted_gram": [_p, _p, _i64, _i64, _i64, _i64, _f32, _f32, _p, _i64, _i64, _p, _sz],
     "g2ptq_prepare_hessian": [_p, _p, _i64, _i64, _p, _i64, _p, _p, _i64, _p, _sz],
     "g2ptq_factor_workspace": [_i64, _i64, _szp],
     "g2ptq_inv_chol_upper": [_p, _p, _i64, _i64, _f32, _p, _p, _p, _p, _sz],

@@ -1,14 +1,21 @@
-"""Token staging for the GPTQ Hessian (one Gram launch per flush, not per batch).
+"""Token staging for the Hessians (one Gram launch per flush, not per batch).
 
 ``GPTQ.add_batch`` (gptq_utils/gptq_utils.py:115-126) updates
 ``H ← H·n/(n+t) + (2/(n+t))·XᵀX`` once per calibration batch.  After any
 number of batches since the state (H₀, n₀) this is, exactly in real
 arithmetic, ``H = (n₀/n)·H₀ + (2/n)·Σ XᵀX``: every batch carries the same
-final weight 2/n.  The stager therefore only transposes each batch into a
-feature-major bf16 buffer and runs the Gram product over everything staged
-when the buffer fills or when ``H`` is read, which amortises the Gram
-kernel's per-launch work (reading β·H, writing both triangles) over many
-batches and gives the kernel long K runs.
+final weight 2/n.  The same holds for GPTAQ's cross term
+(gptaq_utils.py:130-148), for GPTQGuided's plain sums
+(gptq_guided_utils.py:59-81) and, once each batch's 1/T_b is folded into its
+staged tokens, for G2PTQ's per-batch means (g2ptq_utils.py:182-201).  The
+stager therefore only transposes each batch into feature-major bf16 planes
+and runs the Gram products over everything staged when the buffer fills or
+when the Hessian is read, which amortises the Gram kernel's per-launch work
+(reading β·H, writing both triangles) over many batches and gives the kernel
+long K runs.
+
+Planes per kind: 0 (GPTQ) Xᵀ; 1 (GPTAQ) Xᵀ and the bf16 hi/lo parts of
+(X_fp − X)ᵀ; 2 (weighted, G groups) Xᵀ and the hi/lo parts of (x·s[t,g])ᵀ.
 
 The buffer grows ×4 at flush points (it is empty then, so nothing is copied),
 up to ``budget_bytes`` (default 8 GiB, env ``G2PTQ_STAGE_BYTES``): MI355X's
@@ -22,11 +29,17 @@ from . import _lib
 
 DEFAULT_BUDGET = int(os.environ.get("G2PTQ_STAGE_BYTES", str(8 << 30)))
 
-# Optional launch timing: when a list, every Gram launch appends
-# (start event, end event, 2·K·C² flops), events recorded on the launch stream.
+# Optional launch timing: when a list, every Gram flush appends
+# (start event, end event, algorithmic flops, K, C), events recorded on the
+# launch stream.
 TIMING = None
 _GRAM_PAD = 2048      # the Gram call may zero-pad K up to a multiple of this
 _FIRST_TOKENS = 65536
+
+KIND_GPTQ, KIND_GPTAQ, KIND_WEIGHTED = 0, 1, 2
+_GRAM_WS = {KIND_GPTQ: "g2ptq_hessian_gram_workspace",
+            KIND_GPTAQ: "g2ptq_gptaq_gram_workspace",
+            KIND_WEIGHTED: "g2ptq_weighted_gram_workspace"}
 
 
 def _ceil(x, m):
@@ -34,12 +47,16 @@ def _ceil(x, m):
 
 
 class GramStager:
-    def __init__(self, columns, device, budget_bytes=None):
+    def __init__(self, columns, device, kind=KIND_GPTQ, groups=0, budget_bytes=None):
         self.C = columns
         self.device = device
+        self.kind = kind
+        self.G = groups
+        self.planes = {KIND_GPTQ: 1, KIND_GPTAQ: 3, KIND_WEIGHTED: 1 + 2 * groups}[kind]
         self.rows = _lib.query_size_i64("g2ptq_hessian_stage_rows", columns)
         budget = DEFAULT_BUDGET if budget_bytes is None else budget_bytes
-        self.max_tokens = max(_GRAM_PAD * 2, budget // (self.rows * 2) // _GRAM_PAD * _GRAM_PAD)
+        per_token = self.planes * self.rows * 2
+        self.max_tokens = max(_GRAM_PAD * 2, budget // per_token // _GRAM_PAD * _GRAM_PAD)
         self.buf = None
         self.cap = 0        # token columns of buf
         self.k = 0          # staged token columns (multiples of 64)
@@ -62,36 +79,81 @@ class GramStager:
         if self.buf is not None and cap <= self.cap:
             return
         self.buf = None
-        self.buf = torch.empty(self.rows, cap, dtype=torch.bfloat16, device=self.device)
+        self.buf = torch.empty(self.planes, self.rows, cap, dtype=torch.bfloat16,
+                               device=self.device)
         self.cap = cap
 
-    def stage(self, X):
+    def stage(self, X, Xfp=None, S=None, s_scale=1.0, act=None, act_alpha=0.0, act_beta=1.0):
+        """Append one (T, C) bf16 batch: X_fp for GPTAQ; the (T, G) fp32
+        saliencies, their scale and the act-square update for the weighted kind."""
         T, C = X.shape
-        _lib.call("g2ptq_hessian_stage", _lib.stream_ptr(), _lib.ptr(X), T, C, C,
-                  _lib.ptr(self.buf), self.cap, self.k)
+        st, xt = _lib.stream_ptr(), _lib.ptr(self.buf)
+        if self.kind == KIND_GPTQ:
+            _lib.call("g2ptq_hessian_stage", st, _lib.ptr(X), T, C, C, xt, self.cap, self.k)
+        elif self.kind == KIND_GPTAQ:
+            _lib.call("g2ptq_gptaq_stage", st, _lib.ptr(X), _lib.ptr(Xfp), T, C, C, C, xt,
+                      self.cap, self.k)
+        else:
+            _lib.call("g2ptq_weighted_stage", st, _lib.ptr(X), T, C, C, _lib.ptr(S), self.G,
+                      S.stride(0), float(s_scale), xt, self.cap, self.k, _lib.ptr(act),
+                      float(act_alpha), float(act_beta))
         self.k += _ceil(T, 64)
 
-    def flush(self, H, alpha, beta):
-        """H = beta·H + alpha·Σ staged XᵀX; empties the buffer."""
+    def flush(self, H, alpha, beta, Dx=None):
+        """H = beta·H + alpha·(Gram of the staged tokens) (and Dx for GPTAQ;
+        H is (G, C, C) for the weighted kind); empties the buffer."""
         if self.k == 0:
             return
-        if not H.is_cuda:
+        if not H.is_cuda or (Dx is not None and not Dx.is_cuda):
             raise RuntimeError("staged Hessian tokens need the Hessian on the GPU: call "
-                               "add_batch inside _maybe_onload_hessian()")
-        nbytes = _lib.query_size("g2ptq_hessian_gram_workspace", self.k, self.C)
+                               "add_batch inside the onload context of the Hessian")
+        nbytes = _lib.query_size(_GRAM_WS[self.kind], self.k, self.C)
         ws = _lib.workspace(nbytes, self.buf.device)
         if TIMING is not None:
             e0 = torch.cuda.Event(enable_timing=True)
             e1 = torch.cuda.Event(enable_timing=True)
             e0.record()
-        _lib.call("g2ptq_hessian_gram", _lib.stream_ptr(), _lib.ptr(self.buf), self.cap, self.k,
-                  self.C, float(alpha), float(beta), _lib.ptr(H), self.C, _lib.ptr(ws), ws.numel())
+        st, xt, C = _lib.stream_ptr(), _lib.ptr(self.buf), self.C
+        if self.kind == KIND_GPTQ:
+            _lib.call("g2ptq_hessian_gram", st, xt, self.cap, self.k, C, float(alpha),
+                      float(beta), _lib.ptr(H), C, _lib.ptr(ws), ws.numel())
+            flops = 2.0 * self.k * C * C
+        elif self.kind == KIND_GPTAQ:
+            _lib.call("g2ptq_gptaq_gram", st, xt, self.cap, self.k, C, float(alpha), float(beta),
+                      _lib.ptr(H), _lib.ptr(Dx), C, _lib.ptr(ws), ws.numel())
+            flops = 4.0 * self.k * C * C
+        else:
+            _lib.call("g2ptq_weighted_gram", st, xt, self.cap, self.k, C, self.G, float(alpha),
+                      float(beta), _lib.ptr(H), C, C * C, _lib.ptr(ws), ws.numel())
+            flops = 2.0 * self.G * self.k * C * C
         if TIMING is not None:
             e1.record()
-            TIMING.append((e0, e1, 2.0 * self.k * self.C * self.C, self.k, self.C))
+            TIMING.append((e0, e1, flops, self.k, C))
         self.k = 0
 
     def release(self):
         self.buf = None
         self.cap = 0
         self.k = 0
+
+
+def staged_attr(name):
+    """A Hessian attribute whose reads first fold every staged token into it
+    (the owner's ``_flush_staged``), and whose deletion (``= None``) folds them
+    in and then drops the staging buffers."""
+    private = "_" + name
+
+    def get(self):
+        self._flush_staged()
+        return getattr(self, private, None)
+
+    def set(self, value):
+        if value is None and getattr(self, private, None) is not None:
+            self._flush_staged()
+        setattr(self, private, value)
+        if value is None:
+            for st in getattr(self, "_stagers", None) or ():
+                if st is not None:
+                    st.release()
+
+    return property(get, set)

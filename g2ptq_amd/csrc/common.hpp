@@ -88,10 +88,6 @@ struct GemmF32 {
 
 int gemm_f32(hipStream_t stream, const GemmF32& g);
 
-// Hessian Gram (gram.hip): staged-operand helpers shared with hessian.hip.
-int64_t gram_padded_features(int64_t C);
-size_t gram_update_ws_bytes(int64_t T, int64_t C);
-
 // p[0..n) = v with a kernel (graph-capture safe, unlike hipMemsetAsync).
 int fill_f32(hipStream_t stream, float* p, int64_t n, float v);
 

@@ -1,14 +1,27 @@
-// Hessian Gram accumulation H = beta·H + alpha·XᵀX on CDNA4 bf16 matrix cores.
+// Hessian Gram products on CDNA4 bf16 matrix cores:
 //
-// Operands: Xᵀ staged as a (Cp × ldt) bf16 matrix (features × tokens,
-// zero padded: Cp multiple of 256, staged token counts multiple of 64), so
-// both MFMA operands of an output tile H[I, J] read K-contiguous rows of the
-// same buffer.
+//   H  = beta·H  + alpha·XᵀX                     (GPTQ, gptq_utils.py:115-126)
+//   Dx = beta·Dx + alpha·(X_fp − X)ᵀX            (GPTAQ, gptaq_utils.py:130-148)
+//   H[g] = beta·H[g] + alpha·Σ_t s[t,g]·x_t x_tᵀ (G2PTQ / GuidedQuant,
+//                                                  g2ptq_utils.py:182-201,
+//                                                  gptq_guided_utils.py:59-81)
+//
+// Operands are staged feature-major: a stage kernel transposes each token-major
+// batch into planes of (Cp × ldt) bf16 (features × tokens, zero padded: Cp a
+// multiple of 256, staged token counts multiples of 64), so both MFMA operands
+// of an output tile read K-contiguous rows.  Plane 0 is Xᵀ.  Operands that are
+// not bf16-exact are staged as two bf16 planes, hi = bf16(v) and
+// lo = bf16(v − hi), which carry 16 significant bits (the residual is below
+// 2⁻¹⁶·|v|): for GPTAQ v = x_fp − x (exact in fp32), for the weighted
+// Hessians v = x·s[t,g]·s_scale.  A product v·x is then the two exact bf16
+// products hi·x + lo·x, accumulated in fp32.
 //
 // Kernel shape (gram256_kernel):
-//   * one workgroup = 8 wave64s = one 256×256 upper-triangular output tile
-//     (I <= J); wave (wm, wn) in a 2×4 grid owns 128×64 = 4×2 tiles of
-//     v_mfma_f32_32x32x16_bf16 (fp32 accumulators in AGPRs);
+//   * one workgroup = 8 wave64s = one 256×256 output tile; wave (wm, wn) in a
+//     2×4 grid owns 128×64 = 4×2 tiles of v_mfma_f32_32x32x16_bf16 (fp32
+//     accumulators in AGPRs).  Symmetric products compute the upper
+//     triangle of tiles (I <= J) and store every tile to both triangles, so
+//     H stays exactly symmetric; the GPTAQ cross term computes all tiles;
 //   * K advances 64 tokens per stage through two LDS buffers (2 × 64 KiB);
 //     the next stage's 16-byte global loads are issued before the current
 //     stage's MFMAs and written to the other buffer after them, so each stage
@@ -16,12 +29,14 @@
 //   * LDS rows are 128 bytes (64 tokens) with the eight 16-byte chunks of
 //     row r stored at chunk position c ^ f(r), f(r) = (r & 7) ^ ((r >> 3) & 1),
 //     which makes the ds_read_b128 operand fetches of 16 consecutive rows
-//     bank-conflict free on 32- and 64-bank LDS;
-//   * diagonal tiles read A and B from the same buffer (half the loads).
-// When the triangle has too few tiles to fill the GPU, K is split S ways:
-// each split writes its raw fp32 tile to a workspace and gram_reduce_kernel
-// sums the splits in a fixed order (deterministic) into H.  Every tile is
-// stored to both triangles of H, so H stays exactly symmetric.
+//     bank-conflict free on 32- and 64-bank LDS.
+// K is split S ways when the tile grid alone would not fill the GPU: each
+// split writes its raw fp32 tile to a workspace and gram_reduce_kernel sums
+// the splits in a fixed order (deterministic) into the output.  A two-plane
+// (hi, lo) operand runs as a product over twice the tokens: the first half of
+// the splits multiplies hi against Xᵀ, the second half lo against Xᵀ.
+#include <algorithm>
+
 #include "common.hpp"
 
 namespace g2ptq {
@@ -36,12 +51,13 @@ constexpr int NTH = 512;  // threads per workgroup (8 waves)
 
 __device__ __forceinline__ int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
-// X (T × C, ld ldx) → XT[c][t_off + t] for t < roundup(T, 64), zero padded in
-// both directions up to the 64-token / Cp-feature grid.  No LDS: each thread
-// loads an 8-token × 8-feature block (eight 16-byte row pieces), transposes
-// it in registers with byte permutes, and stores eight 16-byte pieces of
-// feature rows.  A wave covers 64 tokens × 64 features; the 8 lanes sharing a
-// token row (or a feature row) touch one contiguous 128-byte segment.
+// Staging: X (T × C, ld ldx) → plane[c][t_off + t] for t < roundup(T, 64),
+// zero padded in both directions up to the 64-token / Cp-feature grid.  No
+// LDS: each thread loads an 8-token × 8-feature block (eight 16-byte row
+// pieces), transposes it in registers with byte permutes, and stores eight
+// 16-byte pieces of feature rows.  A wave covers 64 tokens × 64 features; the
+// 8 lanes sharing a token row (or a feature row) touch one contiguous
+// 128-byte segment.
 constexpr int ST_T = 64, ST_C = 256;  // tokens × features per workgroup (4 waves)
 
 // Low / high 16-bit halves of two words → one word (v_perm_b32 selectors).
@@ -52,16 +68,40 @@ __device__ __forceinline__ uint32_t hi_hi(uint32_t a, uint32_t b) {
   return __builtin_amdgcn_perm(b, a, 0x07060302u);
 }
 
-__global__ __launch_bounds__(256) void stage_kernel(const uint16_t* __restrict__ X, int64_t T,
-                                                    int64_t C, int64_t ldx,
-                                                    uint16_t* __restrict__ XT, int64_t ldt,
-                                                    int64_t t_off, int64_t t_end, int vec) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int tb = lane >> 3, fb = lane & 7;
-  const int64_t t0 = (int64_t)blockIdx.x * ST_T + tb * 8;
-  const int64_t f0 = (int64_t)blockIdx.y * ST_C + wave * 64 + fb * 8;
-  // r[i] = features f0..f0+7 of token t0+i (4 words, 2 bf16 each)
-  uint32_t r[8][4];
+__device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;  // NaN stays NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+__device__ __forceinline__ float lo_f32(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float hi_f32(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// v (two fp32 values) → packed bf16 hi word and lo word, v ≈ hi + lo.
+__device__ __forceinline__ void split2(float v0, float v1, uint32_t& hw, uint32_t& lw) {
+  const uint32_t h0 = f32_to_bf16_rne(v0), h1 = f32_to_bf16_rne(v1);
+  const uint32_t l0 = f32_to_bf16_rne(v0 - __uint_as_float(h0 << 16));
+  const uint32_t l1 = f32_to_bf16_rne(v1 - __uint_as_float(h1 << 16));
+  hw = h0 | (h1 << 16);
+  lw = l0 | (l1 << 16);
+}
+
+struct StageArgs {
+  const uint16_t* X;   // T × C bf16, ld ldx
+  const uint16_t* F;   // GPTAQ: X_fp, ld ldf
+  const float* S;      // weighted: T × G saliencies, ld lds
+  int64_t T, C, ldx, ldf, lds;
+  int G;
+  float s_scale;
+  uint16_t* XT;        // planes of Cp × ldt, plane stride `plane` elements
+  int64_t ldt, plane, t_off, t_end;
+  int vec;             // X (and F) rows 16-byte aligned
+};
+
+// r[i] = features f0..f0+7 of token t0+i (4 words, 2 bf16 each), zeros outside.
+__device__ __forceinline__ void load_block(const uint16_t* __restrict__ X, int64_t ldx, int64_t T,
+                                           int64_t C, int64_t t0, int64_t f0, int vec,
+                                           uint32_t (&r)[8][4]) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int64_t t = t0 + i;
@@ -79,17 +119,93 @@ __global__ __launch_bounds__(256) void stage_kernel(const uint16_t* __restrict__
     }
     r[i][0] = v.x; r[i][1] = v.y; r[i][2] = v.z; r[i][3] = v.w;
   }
-  if (t0 >= t_end) return;  // t_end is a multiple of 8
-  // Output row f0 + 2w (+1): tokens t0..t0+7 = low (high) halves of r[0..7][w].
+}
+
+// Output row f0 + 2w (+1), tokens t0..t0+7 = low (high) halves of r[0..7][w].
+__device__ __forceinline__ void store_block(uint16_t* __restrict__ P, int64_t ldt, int64_t f0,
+                                            int64_t col, const uint32_t (&r)[8][4]) {
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
     const uint4 even = make_uint4(lo_lo(r[0][w], r[1][w]), lo_lo(r[2][w], r[3][w]),
                                   lo_lo(r[4][w], r[5][w]), lo_lo(r[6][w], r[7][w]));
     const uint4 odd = make_uint4(hi_hi(r[0][w], r[1][w]), hi_hi(r[2][w], r[3][w]),
                                  hi_hi(r[4][w], r[5][w]), hi_hi(r[6][w], r[7][w]));
-    *reinterpret_cast<uint4*>(XT + (f0 + 2 * w) * ldt + t_off + t0) = even;
-    *reinterpret_cast<uint4*>(XT + (f0 + 2 * w + 1) * ldt + t_off + t0) = odd;
+    *reinterpret_cast<uint4*>(P + (f0 + 2 * w) * ldt + col) = even;
+    *reinterpret_cast<uint4*>(P + (f0 + 2 * w + 1) * ldt + col) = odd;
   }
+}
+
+// KIND 0: plane 0 = Xᵀ.  KIND 1 (GPTAQ): planes 0..2 = Xᵀ, hi and lo of
+// (X_fp − X)ᵀ.  KIND 2 (weighted): plane 0 = Xᵀ, planes 1 + 2g and 2 + 2g =
+// hi and lo of (x·s[t,g]·s_scale)ᵀ.
+template <int KIND>
+__global__ __launch_bounds__(256) void stage_kernel(StageArgs s) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int tb = lane >> 3, fb = lane & 7;
+  const int64_t t0 = (int64_t)blockIdx.x * ST_T + tb * 8;
+  const int64_t f0 = (int64_t)blockIdx.y * ST_C + wave * 64 + fb * 8;
+  uint32_t r[8][4];
+  load_block(s.X, s.ldx, s.T, s.C, t0, f0, s.vec, r);
+  if (t0 >= s.t_end) return;  // t_end is a multiple of 8
+  const int64_t col = s.t_off + t0;
+  store_block(s.XT, s.ldt, f0, col, r);
+  if (KIND == 1) {
+    uint32_t f[8][4], h[8][4];
+    load_block(s.F, s.ldf, s.T, s.C, t0, f0, s.vec, f);
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        uint32_t hw, lw;
+        split2(lo_f32(f[i][w]) - lo_f32(r[i][w]), hi_f32(f[i][w]) - hi_f32(r[i][w]), hw, lw);
+        h[i][w] = hw;
+        f[i][w] = lw;
+      }
+    store_block(s.XT + s.plane, s.ldt, f0, col, h);
+    store_block(s.XT + 2 * s.plane, s.ldt, f0, col, f);
+  }
+  if (KIND == 2) {
+    for (int g = 0; g < s.G; ++g) {
+      float sv[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        sv[i] = (t0 + i < s.T) ? s.S[(t0 + i) * s.lds + g] * s.s_scale : 0.f;
+      uint32_t h[8][4], l[8][4];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int w = 0; w < 4; ++w)
+          split2(lo_f32(r[i][w]) * sv[i], hi_f32(r[i][w]) * sv[i], h[i][w], l[i][w]);
+      store_block(s.XT + (1 + 2 * g) * s.plane, s.ldt, f0, col, h);
+      store_block(s.XT + (2 + 2 * g) * s.plane, s.ldt, f0, col, l);
+    }
+  }
+}
+
+// act = act_beta·act + act_alpha·Σ_t x[t,c]² over tokens [t0, t0 + len) of
+// the staged Xᵀ (one wave per feature, 16-byte loads; len a multiple of 8).
+__global__ __launch_bounds__(256) void act_square_kernel(const uint16_t* __restrict__ XT,
+                                                         int64_t ldt, int64_t t0, int64_t len,
+                                                         int64_t C, float* act, float act_alpha,
+                                                         float act_beta) {
+  const int64_t c = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (c >= C) return;
+  const uint16_t* row = XT + c * ldt + t0;
+  float s = 0.f;
+  for (int64_t t = (int64_t)lane * 8; t < len; t += 512) {
+    const uint4 v = *reinterpret_cast<const uint4*>(row + t);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float a = lo_f32(w[k]), b = hi_f32(w[k]);
+      s += a * a;
+      s += b * b;
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+  if (lane == 0) act[c] = act_beta * act[c] + act_alpha * s;
 }
 
 // Zero columns [k0, k1) of the staged operand (padding up to the split grid).
@@ -103,13 +219,16 @@ __global__ void zero_cols_bf16_kernel(uint16_t* XT, int64_t ldt, int64_t rows, i
 }
 
 struct G2Args {
-  const uint16_t* XT;
+  const uint16_t* A1;  // row operand planes (Cp × ldt); A2 feeds the second
+  const uint16_t* A2;  // half of the splits when halves == 2
+  const uint16_t* B;   // column operand plane
   int64_t ldt;
   int64_t kc;      // tokens per split (an even number of KS stages)
   int64_t nt;      // tiles per dimension
-  int64_t tiles;   // nt (nt + 1) / 2
+  int64_t tiles;   // upper triangle nt (nt + 1) / 2, or nt² for full products
   int64_t C;
-  int S;           // splits
+  int S;           // splits (halves × splits per half)
+  int halves;
   float alpha, beta;
   float* H; int64_t ldh;
   float* P;        // split partials: (tile * S + s) * TT*TT
@@ -159,7 +278,18 @@ __device__ __forceinline__ void band_tile(int64_t idx, int64_t nt, int64_t& I, i
   }
 }
 
-template <bool HAS_BETA>
+// Full-grid tile number idx → (I, J): bands of GB tile-rows walked column by
+// column.
+__device__ __forceinline__ void grid_tile(int64_t idx, int64_t nt, int64_t& I, int64_t& J) {
+  const int64_t per = GB * nt;
+  const int64_t band = idx / per, r = idx - band * per;
+  const int64_t g0 = band * GB;
+  const int64_t h = nt - g0 < GB ? nt - g0 : GB;
+  I = g0 + r % h;
+  J = r / h;
+}
+
+template <bool HAS_BETA, bool FULL>
 __global__ __launch_bounds__(NTH) void gram256_kernel(G2Args a) {
   __shared__ __attribute__((aligned(16))) uint16_t Ls[2][2][TT * KS];  // [buf][A/B]
 
@@ -173,16 +303,25 @@ __global__ __launch_bounds__(NTH) void gram256_kernel(G2Args a) {
   const int split = (int)(id / a.tiles);
   const int64_t tile_ord = id - (int64_t)split * a.tiles;
   int64_t I, J;
-  band_tile(tile_ord, a.nt, I, J);
   int64_t tile;  // row-major tile number (partials layout)
-  tile = I * a.nt - I * (I - 1) / 2 + (J - I);
-  const bool diag = (I == J);
+  if (FULL) {
+    grid_tile(tile_ord, a.nt, I, J);
+    tile = I * a.nt + J;
+  } else {
+    band_tile(tile_ord, a.nt, I, J);
+    tile = I * a.nt - I * (I - 1) / 2 + (J - I);
+  }
+  const bool diag = !FULL && (I == J);
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 2, wn = wave & 3;
 
-  const uint16_t* Ag = a.XT + (I * TT) * a.ldt + (int64_t)split * a.kc;
-  const uint16_t* Bg = a.XT + (J * TT) * a.ldt + (int64_t)split * a.kc;
+  // Split → operand plane and token range.
+  const int per_half = a.S / a.halves;
+  const int half = split / per_half, sp = split - half * per_half;
+  const uint16_t* Aop = half ? a.A2 : a.A1;
+  const uint16_t* Ag = Aop + (I * TT) * a.ldt + (int64_t)sp * a.kc;
+  const uint16_t* Bg = a.B + (J * TT) * a.ldt + (int64_t)sp * a.kc;
 
   // Chunk q = tid + i*512 of a stage: row q >> 3, 16-byte chunk q & 7.
   // Two register sets carry stages kt+1 and kt+2 while stage kt is multiplied.
@@ -309,7 +448,30 @@ __global__ __launch_bounds__(NTH) void gram256_kernel(G2Args a) {
   // any of them is stored (the compiler cannot prove that stores to H do not
   // alias later loads, so interleaved read-modify-writes would serialise one
   // memory round trip per element).
-  if (a.S == 1) {
+  if (FULL && a.S == 1) {
+    const int64_t i0 = I * TT, j0 = J * TT;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      float hv[2][16];
+#pragma unroll
+      for (int n = 0; n < 2; ++n)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int64_t i = i0 + wm * 128 + m * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+          const int64_t j = j0 + wn * 64 + n * 32 + lr;
+          hv[n][v] = (HAS_BETA && i < a.C && j < a.C) ? a.H[i * a.ldh + j] : 0.f;
+        }
+#pragma unroll
+      for (int n = 0; n < 2; ++n)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int64_t i = i0 + wm * 128 + m * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+          const int64_t j = j0 + wn * 64 + n * 32 + lr;
+          if (i < a.C && j < a.C)
+            a.H[i * a.ldh + j] = (HAS_BETA ? a.beta * hv[n][v] : 0.f) + a.alpha * acc[m][n][v];
+        }
+    }
+  } else if (a.S == 1) {
     const int64_t i0 = I * TT, j0 = J * TT;
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
@@ -364,16 +526,22 @@ __global__ __launch_bounds__(NTH) void gram256_kernel(G2Args a) {
   }
 }
 
-// H[I,J] = beta·H + alpha·Σ_s partial_s (fixed order), mirrored.  One
-// workgroup reduces a 64×64 block of a tile: rows are read and written as
-// 16-byte vectors, and the mirror goes through an LDS transpose so that it is
-// written in rows as well.
+// H[I,J] = beta·H + alpha·Σ_s partial_s (fixed order), mirrored for symmetric
+// products.  One workgroup reduces a 64×64 block of a tile: rows are read and
+// written as 16-byte vectors, and the mirror goes through an LDS transpose so
+// that it is written in rows as well.
+template <bool FULL>
 __global__ __launch_bounds__(256) void gram_reduce_kernel(G2Args a) {
   __shared__ float tr[64][65];
   const int64_t tile = blockIdx.y;
   int64_t I, J;
-  tri_tile(tile, a.nt, I, J);
-  const bool diag = (I == J);
+  if (FULL) {
+    I = tile / a.nt;
+    J = tile - I * a.nt;
+  } else {
+    tri_tile(tile, a.nt, I, J);
+  }
+  const bool diag = !FULL && (I == J);
   const int bi = blockIdx.x >> 2, bj = blockIdx.x & 3;  // 64×64 block within the tile
   if (diag && bi > bj) return;                          // strictly below the diagonal
   const bool full = !diag || bi < bj;                    // no element on or below the diagonal
@@ -412,9 +580,12 @@ __global__ __launch_bounds__(256) void gram_reduce_kernel(G2Args a) {
         }
       }
     }
+    if (!FULL) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u) tr[r][cq * 4 + u] = out[u];
+      for (int u = 0; u < 4; ++u) tr[r][cq * 4 + u] = out[u];
+    }
   }
+  if (FULL) return;
   __syncthreads();
   // Mirror: element (i, j) of the block goes to H[j][i]; thread writes row j.
 #pragma unroll
@@ -436,151 +607,346 @@ __global__ __launch_bounds__(256) void gram_reduce_kernel(G2Args a) {
   }
 }
 
-// Split count: the smallest power of two that gives at least 4096 workgroups
-// (16 waves of one 256×256 tile per CU), at most 16 splits and at least 16
-// KS-token stages per split.  Powers of two keep every split on whole XCDs
-// (the workgroup order is split-major and XCD-contiguous), so the
-// workgroups of one XCD read one K range; measured on MI355X with random
-// bf16 operands (C=4096: S=16; C=14336: S=4).
-int choose_splits(int64_t tiles, int64_t K) {
-  const int64_t smax = std::max<int64_t>(1, std::min<int64_t>(16, K / (KS * 16)));
-  int S = 1;
-  while (S * 2 <= smax && tiles * S < 4096) S *= 2;
-  return S;
+// Split plan.  Splits per operand half: the smallest power of two that gives
+// at least 4096 workgroups (16 waves of one 256×256 tile per CU), at most 16
+// splits in all and at least 16 KS-token stages per split.  Powers of two
+// keep every split on whole XCDs (the workgroup order is split-major and
+// XCD-contiguous), so the workgroups of one XCD read one K range; measured on
+// MI355X with random bf16 operands (C=4096: S=16; C=14336: S=4).  Every split
+// gets an even number of stages, so the staged width is K padded to a
+// multiple of 2·KS·(splits per half), at most 2048.
+struct GramPlan {
+  int S;        // total splits
+  int64_t Kp;   // padded tokens per half
+  int64_t kc;   // tokens per split
+};
+
+GramPlan gram_plan(int64_t tiles, int64_t K, int halves) {
+  const int64_t K1 = std::max<int64_t>(K, 1);
+  const int64_t smax = std::max<int64_t>(1, std::min<int64_t>(16 / halves, K1 / (KS * 16)));
+  int s = 1;
+  while (s * 2 <= smax && tiles * halves * s < 4096) s *= 2;
+  const int64_t step = (int64_t)2 * KS * s;
+  GramPlan p;
+  p.S = s * halves;
+  p.Kp = cdiv(K1, step) * step;
+  p.kc = p.Kp / s;
+  return p;
 }
 
-// Token width a split grid of S splits needs for K tokens: every split gets an
-// even number of KS-token stages.
-int64_t padded_tokens(int64_t K, int S) {
-  const int64_t step = (int64_t)2 * KS * S;
-  return cdiv(std::max<int64_t>(K, 1), step) * step;
-}
-
-}  // namespace
-
-int64_t gram_padded_features(int64_t C) { return cdiv(C, TT) * TT; }
-
-size_t gram_ws_bytes(int64_t K, int64_t C) {
+int64_t n_tiles(int64_t C, bool full) {
   const int64_t nt = cdiv(C, TT);
-  const int64_t tiles = nt * (nt + 1) / 2;
-  const int S = choose_splits(tiles, std::max<int64_t>(K, 1));
-  if (S == 1) return 256;
-  return (size_t)tiles * S * TT * TT * sizeof(float);
+  return full ? nt * nt : nt * (nt + 1) / 2;
 }
 
-int gram_stage(hipStream_t st, const uint16_t* X, int64_t T, int64_t C, int64_t ldx, uint16_t* XT,
-               int64_t ldt, int64_t t_off) {
-  if (T <= 0) return G2PTQ_OK;
-  const int64_t Cp = gram_padded_features(C);
-  const int64_t T64 = cdiv(T, KS) * KS;
-  const int vec = (ldx % 8 == 0) && ((reinterpret_cast<uintptr_t>(X) & 15) == 0);
-  G2PTQ_CHECK(ldt % 8 == 0 && t_off % 8 == 0 && (reinterpret_cast<uintptr_t>(XT) & 15) == 0,
-              "hessian stage: XT must be 16-byte aligned with ldt and t_off multiples of 8");
-  dim3 grid((unsigned)cdiv(T, (int64_t)ST_T), (unsigned)(Cp / ST_C));
-  hipLaunchKernelGGL(stage_kernel, grid, dim3(256), 0, st, X, T, C, ldx, XT, ldt, t_off, T64, vec);
+size_t plan_ws_bytes(int64_t tiles, const GramPlan& p) {
+  return p.S == 1 ? 256 : (size_t)tiles * p.S * TT * TT * sizeof(float);
+}
+
+// The three products, as (full, halves).
+struct Product {
+  bool full;
+  int halves;
+};
+constexpr Product SYM1{false, 1};  // H from Xᵀ
+constexpr Product SYM2{false, 2};  // weighted H[g] from (hi_g, lo_g) against Xᵀ
+constexpr Product FULL2{true, 2};  // GPTAQ Dx from (hi, lo) against Xᵀ
+
+size_t product_ws(int64_t K, int64_t C, Product pr) {
+  const int64_t tiles = n_tiles(C, pr.full);
+  return plan_ws_bytes(tiles, gram_plan(tiles, K, pr.halves));
+}
+
+int64_t product_width(int64_t K, int64_t C, Product pr) {
+  return gram_plan(n_tiles(C, pr.full), K, pr.halves).Kp;
+}
+
+// Planes staged per kind (0 Hessian, 1 GPTAQ, 2 weighted with G groups).
+int64_t kind_planes(int kind, int64_t G) { return kind == 0 ? 1 : kind == 1 ? 3 : 1 + 2 * G; }
+
+// Staged token width and Gram workspace a kind needs for K tokens.
+int64_t kind_width(int kind, int64_t K, int64_t C) {
+  if (kind == 0) return product_width(K, C, SYM1);
+  if (kind == 1) return std::max(product_width(K, C, SYM1), product_width(K, C, FULL2));
+  return product_width(K, C, SYM2);
+}
+size_t kind_gram_ws(int kind, int64_t K, int64_t C) {
+  if (kind == 0) return product_ws(K, C, SYM1);
+  if (kind == 1) return std::max(product_ws(K, C, SYM1), product_ws(K, C, FULL2));
+  return product_ws(K, C, SYM2);
+}
+
+// Zero token columns [roundup(K, 64), width) of `rows` staged rows.
+int zero_pad(hipStream_t st, uint16_t* XT, int64_t ldt, int64_t rows, int64_t K, int64_t width) {
+  const int64_t K64 = cdiv(std::max<int64_t>(K, 0), KS) * KS;
+  if (width <= K64) return G2PTQ_OK;
+  const int64_t n = rows * (width - K64);
+  hipLaunchKernelGGL(zero_cols_bf16_kernel, dim3((unsigned)std::min<int64_t>(cdiv(n, 256), 4096)),
+                     dim3(256), 0, st, XT, ldt, rows, K64, width);
   G2PTQ_LAUNCHED();
   return G2PTQ_OK;
 }
 
-int gram_accumulate(hipStream_t st, uint16_t* XT, int64_t ldt, int64_t K, int64_t C, float alpha,
-                    float beta, float* H, int64_t ldh, void* ws, size_t ws_bytes) {
+// out = beta·out + alpha·(product over K staged tokens).  The staged planes
+// must be zero from token roundup(K, 64) up to product_width(K, C, pr).
+int run_product(hipStream_t st, Product pr, const uint16_t* A1, const uint16_t* A2,
+                const uint16_t* B, int64_t ldt, int64_t K, int64_t C, float alpha, float beta,
+                float* out, int64_t ldo, void* ws, size_t ws_bytes) {
   const int64_t nt = cdiv(C, TT);
-  const int64_t Cp = nt * TT;
-  const int64_t tiles = nt * (nt + 1) / 2;
-  const int S = choose_splits(tiles, std::max<int64_t>(K, 1));
-  const int64_t Kp = padded_tokens(K, S);
-  G2PTQ_CHECK(Kp <= ldt, "hessian gram: staged operand too narrow (%lld < %lld)",
-              (long long)ldt, (long long)Kp);
-  G2PTQ_CHECK((reinterpret_cast<uintptr_t>(XT) & 15) == 0 && ldt % 8 == 0,
-              "hessian gram: XT must be 16-byte aligned with ldt a multiple of 8");
-  const int64_t K64 = cdiv(std::max<int64_t>(K, 0), KS) * KS;
-  if (Kp > K64) {
-    const int64_t n = Cp * (Kp - K64);
-    hipLaunchKernelGGL(zero_cols_bf16_kernel, dim3((unsigned)std::min<int64_t>(cdiv(n, 256), 4096)),
-                       dim3(256), 0, st, XT, ldt, Cp, K64, Kp);
-    G2PTQ_LAUNCHED();
-  }
+  const int64_t tiles = n_tiles(C, pr.full);
+  const GramPlan p = gram_plan(tiles, K, pr.halves);
+  G2PTQ_CHECK(p.Kp <= ldt, "hessian gram: staged operand too narrow (%lld < %lld)",
+              (long long)ldt, (long long)p.Kp);
+  G2PTQ_CHECK(tiles * p.S < (1ll << 31) && tiles < 65536, "hessian gram: grid too large");
   G2Args a{};
-  a.XT = XT; a.ldt = ldt; a.kc = Kp / S; a.nt = nt; a.tiles = tiles; a.C = C; a.S = S;
-  a.alpha = alpha; a.beta = beta; a.H = H; a.ldh = ldh;
-  if (S > 1) {
-    const size_t need = (size_t)tiles * S * TT * TT * sizeof(float);
+  a.A1 = A1; a.A2 = A2; a.B = B; a.ldt = ldt; a.kc = p.kc; a.nt = nt; a.tiles = tiles; a.C = C;
+  a.S = p.S; a.halves = pr.halves; a.alpha = alpha; a.beta = beta; a.H = out; a.ldh = ldo;
+  if (p.S > 1) {
+    const size_t need = plan_ws_bytes(tiles, p);
     G2PTQ_CHECK(ws != nullptr && ws_bytes >= need, "hessian gram: workspace %zu < %zu", ws_bytes,
                 need);
     a.P = static_cast<float*>(ws);
   }
-  G2PTQ_CHECK(tiles * S < (1ll << 31), "hessian gram: grid too large");
-  if (S == 1 && beta != 0.f)
-    hipLaunchKernelGGL(gram256_kernel<true>, dim3((unsigned)(tiles * S)), dim3(NTH), 0, st, a);
-  else
-    hipLaunchKernelGGL(gram256_kernel<false>, dim3((unsigned)(tiles * S)), dim3(NTH), 0, st, a);
+  const dim3 grid((unsigned)(tiles * p.S));
+  const bool direct_beta = p.S == 1 && beta != 0.f;
+  if (pr.full) {
+    if (direct_beta) hipLaunchKernelGGL((gram256_kernel<true, true>), grid, dim3(NTH), 0, st, a);
+    else hipLaunchKernelGGL((gram256_kernel<false, true>), grid, dim3(NTH), 0, st, a);
+  } else {
+    if (direct_beta) hipLaunchKernelGGL((gram256_kernel<true, false>), grid, dim3(NTH), 0, st, a);
+    else hipLaunchKernelGGL((gram256_kernel<false, false>), grid, dim3(NTH), 0, st, a);
+  }
   G2PTQ_LAUNCHED();
-  if (S > 1) {
-    hipLaunchKernelGGL(gram_reduce_kernel, dim3(16, (unsigned)tiles), dim3(256), 0, st, a);
+  if (p.S > 1) {
+    if (pr.full)
+      hipLaunchKernelGGL(gram_reduce_kernel<true>, dim3(16, (unsigned)tiles), dim3(256), 0, st, a);
+    else
+      hipLaunchKernelGGL(gram_reduce_kernel<false>, dim3(16, (unsigned)tiles), dim3(256), 0, st, a);
     G2PTQ_LAUNCHED();
   }
   return G2PTQ_OK;
 }
 
-// One-shot update (stage + accumulate) through a caller workspace laid out as
-// [staged Xᵀ: Cp × ldt bf16][split partials].
-static int64_t update_ldt(int64_t T, int64_t C) {
-  const int64_t nt = cdiv(C, TT);
-  const int64_t tiles = nt * (nt + 1) / 2;
-  return padded_tokens(T, choose_splits(tiles, std::max<int64_t>(T, 1)));
+int64_t padded_features(int64_t C) { return cdiv(C, TT) * TT; }
+
+int stage(hipStream_t st, int kind, const uint16_t* X, const uint16_t* F, const float* S,
+          int64_t T, int64_t C, int64_t ldx, int64_t ldf, int64_t G, int64_t lds, float s_scale,
+          uint16_t* XT, int64_t ldt, int64_t t_off) {
+  if (T <= 0) return G2PTQ_OK;
+  G2PTQ_CHECK(C > 0 && C <= (1ll << 20), "hessian stage: bad feature count %lld", (long long)C);
+  G2PTQ_CHECK(ldt % 8 == 0 && t_off % 64 == 0 && (reinterpret_cast<uintptr_t>(XT) & 15) == 0,
+              "hessian stage: XT must be 16-byte aligned, ldt a multiple of 8 and t_off of 64");
+  G2PTQ_CHECK(t_off + cdiv(T, KS) * KS <= ldt,
+              "hessian stage: token offset %lld (+%lld) outside the staged width %lld",
+              (long long)t_off, (long long)T, (long long)ldt);
+  const int64_t Cp = padded_features(C);
+  auto aligned = [](const void* p, int64_t ld) {
+    return ld % 8 == 0 && (reinterpret_cast<uintptr_t>(p) & 15) == 0;
+  };
+  StageArgs s{};
+  s.X = X; s.F = F; s.S = S; s.T = T; s.C = C; s.ldx = ldx; s.ldf = ldf; s.lds = lds;
+  s.G = (int)G; s.s_scale = s_scale; s.XT = XT; s.ldt = ldt; s.plane = Cp * ldt; s.t_off = t_off;
+  s.t_end = cdiv(T, KS) * KS;
+  s.vec = aligned(X, ldx) && (kind != 1 || aligned(F, ldf));
+  const dim3 grid((unsigned)cdiv(T, (int64_t)ST_T), (unsigned)(Cp / ST_C));
+  if (kind == 0) hipLaunchKernelGGL(stage_kernel<0>, grid, dim3(256), 0, st, s);
+  else if (kind == 1) hipLaunchKernelGGL(stage_kernel<1>, grid, dim3(256), 0, st, s);
+  else hipLaunchKernelGGL(stage_kernel<2>, grid, dim3(256), 0, st, s);
+  G2PTQ_LAUNCHED();
+  return G2PTQ_OK;
 }
 
-size_t gram_update_ws_bytes(int64_t T, int64_t C) {
-  const int64_t ldt = update_ldt(T, C);
-  const size_t xt = ((size_t)gram_padded_features(C) * ldt * 2 + 255) / 256 * 256;
-  return xt + gram_ws_bytes(T, C);
+int act_square(hipStream_t st, const uint16_t* XT, int64_t ldt, int64_t t_off, int64_t T, int64_t C,
+               float* act, float act_alpha, float act_beta) {
+  if (!act) return G2PTQ_OK;
+  const int64_t len = cdiv(std::max<int64_t>(T, 0), KS) * KS;
+  hipLaunchKernelGGL(act_square_kernel, dim3((unsigned)cdiv(C, 4)), dim3(256), 0, st, XT, ldt,
+                     t_off, len, C, act, act_alpha, act_beta);
+  G2PTQ_LAUNCHED();
+  return G2PTQ_OK;
 }
 
+int check_gram_args(const uint16_t* XT, int64_t ldt, int64_t K, int64_t C) {
+  G2PTQ_CHECK(XT && C > 0 && C <= (1ll << 20) && K >= 0, "hessian gram: bad arguments");
+  G2PTQ_CHECK((reinterpret_cast<uintptr_t>(XT) & 15) == 0 && ldt % 8 == 0,
+              "hessian gram: XT must be 16-byte aligned with ldt a multiple of 8");
+  return G2PTQ_OK;
+}
+
+// The Gram products of each kind over K tokens staged in XT (planes of Cp × ldt).
+int gram_kind(hipStream_t st, int kind, uint16_t* XT, int64_t ldt, int64_t K, int64_t C, int64_t G,
+              float alpha, float beta, float* H, int64_t ldh, int64_t sH, float* Dx, int64_t ldd,
+              void* ws, size_t ws_bytes) {
+  G2PTQ_TRY(check_gram_args(XT, ldt, K, C));
+  const int64_t Cp = padded_features(C);
+  const int64_t plane = Cp * ldt;
+  const int64_t width = kind_width(kind, K, C);
+  G2PTQ_CHECK(width <= ldt, "hessian gram: staged operand too narrow (%lld < %lld)",
+              (long long)ldt, (long long)width);
+  G2PTQ_TRY(zero_pad(st, XT, ldt, kind_planes(kind, G) * Cp, K, width));
+  if (kind == 0)
+    return run_product(st, SYM1, XT, nullptr, XT, ldt, K, C, alpha, beta, H, ldh, ws, ws_bytes);
+  if (kind == 1) {
+    G2PTQ_TRY(run_product(st, SYM1, XT, nullptr, XT, ldt, K, C, alpha, beta, H, ldh, ws,
+                          ws_bytes));
+    return run_product(st, FULL2, XT + plane, XT + 2 * plane, XT, ldt, K, C, alpha, beta, Dx, ldd,
+                       ws, ws_bytes);
+  }
+  for (int64_t g = 0; g < G; ++g)
+    G2PTQ_TRY(run_product(st, SYM2, XT + (1 + 2 * g) * plane, XT + (2 + 2 * g) * plane, XT, ldt, K,
+                          C, alpha, beta, H + g * sH, ldh, ws, ws_bytes));
+  return G2PTQ_OK;
+}
+
+// One-shot updates (stage + Gram) through a caller workspace laid out as
+// [staged planes: planes × Cp × width bf16][split partials].
+size_t staged_bytes(int kind, int64_t T, int64_t C, int64_t G) {
+  return ((size_t)kind_planes(kind, G) * padded_features(C) * kind_width(kind, T, C) * 2 + 255) /
+         256 * 256;
+}
+size_t update_ws_bytes(int kind, int64_t T, int64_t C, int64_t G) {
+  return staged_bytes(kind, T, C, G) + kind_gram_ws(kind, T, C);
+}
+
+}  // namespace
 }  // namespace g2ptq
 
 using namespace g2ptq;
+
+extern "C" int g2ptq_hessian_workspace(int64_t T, int64_t C, int kind, int64_t G, size_t* bytes) {
+  G2PTQ_CHECK(bytes != nullptr && C > 0 && T >= 0 && kind >= 0 && kind <= 2,
+              "hessian_workspace: bad arguments");
+  G2PTQ_CHECK(kind != 2 || (G >= 1 && G <= 64), "hessian_workspace: G=%lld unsupported",
+              (long long)G);
+  *bytes = update_ws_bytes(kind, T, C, G);
+  return G2PTQ_OK;
+}
 
 extern "C" int g2ptq_hessian_update(void* stream, const uint16_t* X, int64_t T, int64_t C,
                                     int64_t ldx, float alpha, float beta, float* H, int64_t ldh,
                                     void* ws, size_t ws_bytes) {
   G2PTQ_CHECK(H != nullptr && (X != nullptr || T == 0) && C > 0 && T >= 0,
               "hessian_update: bad arguments");
-  const size_t need = gram_update_ws_bytes(T, C);
+  const size_t need = update_ws_bytes(0, T, C, 0);
   G2PTQ_CHECK(ws != nullptr && ws_bytes >= need, "hessian_update: workspace %zu < %zu", ws_bytes,
               need);
   hipStream_t st = as_stream(stream);
-  const int64_t ldt = update_ldt(T, C);
+  const int64_t ldt = kind_width(0, T, C);
   uint16_t* XT = static_cast<uint16_t*>(ws);
-  const size_t xt = ((size_t)gram_padded_features(C) * ldt * 2 + 255) / 256 * 256;
-  G2PTQ_TRY(gram_stage(st, X, T, C, ldx, XT, ldt, 0));
-  return gram_accumulate(st, XT, ldt, T, C, alpha, beta, H, ldh, static_cast<char*>(ws) + xt,
-                         ws_bytes - xt);
+  const size_t xt = staged_bytes(0, T, C, 0);
+  G2PTQ_TRY(stage(st, 0, X, nullptr, nullptr, T, C, ldx, 0, 0, 0, 1.f, XT, ldt, 0));
+  return gram_kind(st, 0, XT, ldt, T, C, 0, alpha, beta, H, ldh, 0, nullptr, 0,
+                   static_cast<char*>(ws) + xt, ws_bytes - xt);
+}
+
+extern "C" int g2ptq_gptaq_update(void* stream, const uint16_t* X, const uint16_t* Xfp, int64_t T,
+                                  int64_t C, int64_t ldx, int64_t ldxf, float alpha, float beta,
+                                  float* H, float* Dx, int64_t ld, void* ws, size_t ws_bytes) {
+  G2PTQ_CHECK(H && Dx && ((X && Xfp) || T == 0) && C > 0 && T >= 0,
+              "gptaq_update: bad arguments");
+  const size_t need = update_ws_bytes(1, T, C, 0);
+  G2PTQ_CHECK(ws != nullptr && ws_bytes >= need, "gptaq_update: workspace %zu < %zu", ws_bytes,
+              need);
+  hipStream_t st = as_stream(stream);
+  const int64_t ldt = kind_width(1, T, C);
+  uint16_t* XT = static_cast<uint16_t*>(ws);
+  const size_t xt = staged_bytes(1, T, C, 0);
+  G2PTQ_TRY(stage(st, 1, X, Xfp, nullptr, T, C, ldx, ldxf, 0, 0, 1.f, XT, ldt, 0));
+  return gram_kind(st, 1, XT, ldt, T, C, 0, alpha, beta, H, ld, 0, Dx, ld,
+                   static_cast<char*>(ws) + xt, ws_bytes - xt);
+}
+
+extern "C" int g2ptq_weighted_hessian_update(void* stream, const uint16_t* X, int64_t T,
+                                             int64_t C, int64_t ldx, const float* S, int64_t G,
+                                             int64_t lds, float alpha, float beta, float* H,
+                                             int64_t ldh, int64_t sH, float* act,
+                                             float act_alpha, float act_beta, void* ws,
+                                             size_t ws_bytes) {
+  G2PTQ_CHECK(G >= 1 && G <= 64, "weighted_hessian_update: G=%lld unsupported", (long long)G);
+  G2PTQ_CHECK(H && ((X && S) || T == 0) && C > 0 && T >= 0,
+              "weighted_hessian_update: bad arguments");
+  const size_t need = update_ws_bytes(2, T, C, G);
+  G2PTQ_CHECK(ws != nullptr && ws_bytes >= need, "weighted_hessian_update: workspace %zu < %zu",
+              ws_bytes, need);
+  hipStream_t st = as_stream(stream);
+  const int64_t ldt = kind_width(2, T, C);
+  uint16_t* XT = static_cast<uint16_t*>(ws);
+  const size_t xt = staged_bytes(2, T, C, G);
+  G2PTQ_TRY(stage(st, 2, X, nullptr, S, T, C, ldx, 0, G, lds, 1.f, XT, ldt, 0));
+  G2PTQ_TRY(act_square(st, XT, ldt, 0, T, C, act, act_alpha, act_beta));
+  return gram_kind(st, 2, XT, ldt, T, C, G, alpha, beta, H, ldh, sH, nullptr, 0,
+                   static_cast<char*>(ws) + xt, ws_bytes - xt);
 }
 
 extern "C" int g2ptq_hessian_stage_rows(int64_t C, int64_t* rows) {
   G2PTQ_CHECK(rows != nullptr && C > 0, "hessian_stage_rows: bad arguments");
-  *rows = gram_padded_features(C);
+  *rows = padded_features(C);
   return G2PTQ_OK;
 }
 
 extern "C" int g2ptq_hessian_stage(void* stream, const uint16_t* X, int64_t T, int64_t C,
                                    int64_t ldx, uint16_t* XT, int64_t ldt, int64_t t_off) {
   G2PTQ_CHECK(XT && (X || T == 0) && C > 0 && T >= 0, "hessian_stage: bad arguments");
-  G2PTQ_CHECK(t_off % 64 == 0 && t_off + cdiv(T, 64) * 64 <= ldt,
-              "hessian_stage: token offset %lld (+%lld) outside the staged width %lld",
-              (long long)t_off, (long long)T, (long long)ldt);
-  return gram_stage(as_stream(stream), X, T, C, ldx, XT, ldt, t_off);
+  return stage(as_stream(stream), 0, X, nullptr, nullptr, T, C, ldx, 0, 0, 0, 1.f, XT, ldt,
+               t_off);
 }
 
 extern "C" int g2ptq_hessian_gram_workspace(int64_t K, int64_t C, size_t* bytes) {
-  G2PTQ_CHECK(bytes != nullptr && C > 0, "hessian_gram_workspace: bad arguments");
-  *bytes = gram_ws_bytes(K, C);
+  G2PTQ_CHECK(bytes != nullptr && C > 0 && K >= 0, "hessian_gram_workspace: bad arguments");
+  *bytes = kind_gram_ws(0, K, C);
   return G2PTQ_OK;
 }
 
 extern "C" int g2ptq_hessian_gram(void* stream, uint16_t* XT, int64_t ldt, int64_t K, int64_t C,
                                   float alpha, float beta, float* H, int64_t ldh, void* ws,
                                   size_t ws_bytes) {
-  G2PTQ_CHECK(XT && H && C > 0 && K >= 0, "hessian_gram: bad arguments");
-  return gram_accumulate(as_stream(stream), XT, ldt, K, C, alpha, beta, H, ldh, ws, ws_bytes);
+  G2PTQ_CHECK(H != nullptr, "hessian_gram: null H");
+  return gram_kind(as_stream(stream), 0, XT, ldt, K, C, 0, alpha, beta, H, ldh, 0, nullptr, 0, ws,
+                   ws_bytes);
+}
+
+extern "C" int g2ptq_gptaq_stage(void* stream, const uint16_t* X, const uint16_t* Xfp, int64_t T,
+                                 int64_t C, int64_t ldx, int64_t ldxf, uint16_t* XT, int64_t ldt,
+                                 int64_t t_off) {
+  G2PTQ_CHECK(XT && ((X && Xfp) || T == 0) && C > 0 && T >= 0, "gptaq_stage: bad arguments");
+  return stage(as_stream(stream), 1, X, Xfp, nullptr, T, C, ldx, ldxf, 0, 0, 1.f, XT, ldt, t_off);
+}
+
+extern "C" int g2ptq_gptaq_gram_workspace(int64_t K, int64_t C, size_t* bytes) {
+  G2PTQ_CHECK(bytes != nullptr && C > 0 && K >= 0, "gptaq_gram_workspace: bad arguments");
+  *bytes = kind_gram_ws(1, K, C);
+  return G2PTQ_OK;
+}
+
+extern "C" int g2ptq_gptaq_gram(void* stream, uint16_t* XT, int64_t ldt, int64_t K, int64_t C,
+                                float alpha, float beta, float* H, float* Dx, int64_t ld, void* ws,
+                                size_t ws_bytes) {
+  G2PTQ_CHECK(H && Dx, "gptaq_gram: null output");
+  return gram_kind(as_stream(stream), 1, XT, ldt, K, C, 0, alpha, beta, H, ld, 0, Dx, ld, ws,
+                   ws_bytes);
+}
+
+extern "C" int g2ptq_weighted_stage(void* stream, const uint16_t* X, int64_t T, int64_t C,
+                                    int64_t ldx, const float* S, int64_t G, int64_t lds,
+                                    float s_scale, uint16_t* XT, int64_t ldt, int64_t t_off,
+                                    float* act, float act_alpha, float act_beta) {
+  G2PTQ_CHECK(G >= 1 && G <= 64, "weighted_stage: G=%lld unsupported", (long long)G);
+  G2PTQ_CHECK(XT && ((X && S) || T == 0) && C > 0 && T >= 0, "weighted_stage: bad arguments");
+  hipStream_t st = as_stream(stream);
+  G2PTQ_TRY(stage(st, 2, X, nullptr, S, T, C, ldx, 0, G, lds, s_scale, XT, ldt, t_off));
+  return act_square(st, XT, ldt, t_off, T, C, act, act_alpha, act_beta);
+}
+
+extern "C" int g2ptq_weighted_gram_workspace(int64_t K, int64_t C, size_t* bytes) {
+  G2PTQ_CHECK(bytes != nullptr && C > 0 && K >= 0, "weighted_gram_workspace: bad arguments");
+  *bytes = kind_gram_ws(2, K, C);
+  return G2PTQ_OK;
+}
+
+extern "C" int g2ptq_weighted_gram(void* stream, uint16_t* XT, int64_t ldt, int64_t K, int64_t C,
+                                   int64_t G, float alpha, float beta, float* H, int64_t ldh,
+                                   int64_t sH, void* ws, size_t ws_bytes) {
+  G2PTQ_CHECK(G >= 1 && G <= 64 && H, "weighted_gram: bad arguments");
+  return gram_kind(as_stream(stream), 2, XT, ldt, K, C, G, alpha, beta, H, ldh, sH, nullptr, 0, ws,
+                   ws_bytes);
 }

@@ -14,6 +14,7 @@ import torch
 
 from . import _core, _lib
 from .common_utils import fake_quantize_grouped
+from ._stage import KIND_WEIGHTED, GramStager, staged_attr
 from .gptq_utils import _compensate
 from .graph_utils import run_graph, validate_tensors
 
@@ -65,9 +66,29 @@ class G2PTQ:
         self.index = torch.tensor([0] * self.num_layers, device=self.dev)
         self.total_tokens = torch.tensor([0] * self.num_layers, device=self.dev)
         self._k = [0] * self.num_layers
+        self._k_flushed = [0] * self.num_layers  # batches already folded into H
         self._tt = [0] * self.num_layers
+        self._stagers = [None] * self.num_layers
         assert self.rows % self.num_groups == 0, (
             f"Number of rows ({self.rows}) must be divisible by num_groups ({self.num_groups})")
+
+    # ``H`` reads fold the staged calibration tokens into it first.  Each
+    # batch's tokens are staged with their 1/T_b folded in, so a flush after
+    # k batches (k₀ of them already in H) is H = (k₀/k)·H + (1/k)·Σ staged,
+    # the reference's running per-batch mean.
+    H = staged_attr("H")
+
+    def _flush_staged(self, idx=None):
+        stagers = getattr(self, "_stagers", None)
+        if not stagers:
+            return
+        for i in (range(self.num_layers) if idx is None else (idx,)):
+            st = stagers[i]
+            if st is None or st.k == 0:
+                continue
+            k, k0 = self._k[i], self._k_flushed[i]
+            st.flush(self._H[i], _core.f32(1 / k), _core.f32(k0 / k))
+            self._k_flushed[i] = k
 
     def _maybe_onload_hessian_grad(self, hessian=True, gradients=False):
         """g2ptq_utils.py:172-180."""
@@ -85,18 +106,33 @@ class G2PTQ:
         del self.saliencies[idx][0]
         if sal.shape != (n_tokens, self.num_groups):
             sal = sal.reshape(n_tokens, self.num_groups)
-        k = self._k[idx]
-        beta = _core.f32(k / (k + 1))
-        k += 1
-        self._k[idx] = k
-        self.index[idx] += 1
+        sal = sal.contiguous()
         tt = self._tt[idx]
         act_beta = _core.f32(tt / (tt + n_tokens))
         tt += n_tokens
         self._tt[idx] = tt
+        act_alpha = _core.f32(1 / tt)
+        st = self._stagers[idx]
+        if st is None:
+            st = self._stagers[idx] = GramStager(self.columns, X.device, KIND_WEIGHTED,
+                                                 self.num_groups)
+        if not st.fits(n_tokens):
+            self._flush_staged(idx)
+            if st.can_stage(n_tokens):
+                st.reserve(n_tokens)
+        k = self._k[idx] + 1
+        if st.fits(n_tokens):
+            st.stage(X, S=sal, s_scale=_core.f32(1 / n_tokens), act=self.act_square[idx],
+                     act_alpha=act_alpha, act_beta=act_beta)
+        else:
+            # a batch larger than the staging budget: update directly
+            k0 = self._k_flushed[idx]
+            _core.weighted_update(self._H[idx], X, sal, _core.f32(1 / (n_tokens * k)),
+                                  _core.f32(k0 / k), self.act_square[idx], act_alpha, act_beta)
+            self._k_flushed[idx] = k
+        self._k[idx] = k
+        self.index[idx] += 1
         self.total_tokens[idx] += n_tokens
-        _core.weighted_update(self.H[idx], X, sal, _core.f32(1 / (n_tokens * k)), beta,
-                              self.act_square[idx], _core.f32(1 / tt), act_beta)
 
     def _run_compensation_block(self, weight, hinv, scale, zero, z, ghinv, backend, graph,
                                 weight_raw=None):

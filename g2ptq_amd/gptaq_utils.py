@@ -9,6 +9,7 @@ block, ``+Q·P`` in the block tail) run in libg2ptq_hip.so.
 import torch
 
 from . import _core, _lib
+from ._stage import KIND_GPTAQ, GramStager, staged_attr
 from .gptq_utils import _compensate
 from .graph_utils import run_graph, validate_tensors
 
@@ -41,7 +42,25 @@ class GPTAQ:
         self.dXXT = _core.alloc((self.num_layers, self.columns, self.columns), H_device)
         self.nsamples = torch.tensor([0] * self.num_layers, device=self.dev)
         self._n = [0] * self.num_layers
+        self._n_flushed = [0] * self.num_layers  # samples already folded into H / dXXT
+        self._stagers = [None] * self.num_layers
         self.fp_inp = [[] for _ in range(self.num_layers)]
+
+    # Reads of H or dXXT fold the staged calibration tokens into both first.
+    H = staged_attr("H")
+    dXXT = staged_attr("dXXT")
+
+    def _flush_staged(self, idx=None):
+        stagers = getattr(self, "_stagers", None)
+        if not stagers:
+            return
+        for i in (range(self.num_layers) if idx is None else (idx,)):
+            st = stagers[i]
+            if st is None or st.k == 0:
+                continue
+            n, n0 = self._n[i], self._n_flushed[i]
+            st.flush(self._H[i], _core.sqrt_scale_sq(n), _core.f32(n0 / n), Dx=self._dXXT[i])
+            self._n_flushed[i] = n
 
     def _maybe_onload_hessian(self):
         """gptaq_utils.py:123-128."""
@@ -49,7 +68,8 @@ class GPTAQ:
                                   device=self.dev)
 
     def add_batch(self, idx, inp, out):
-        """gptaq_utils.py:130-148 (``fp_inp[idx]`` is a FIFO of (tokens, C) tensors)."""
+        """gptaq_utils.py:130-148 (``fp_inp[idx]`` is a FIFO of (tokens, C) tensors):
+        H and dXXT ← ·n/(n+t) + (2/(n+t))·(XᵀX, (X_fp − X)ᵀX), staged."""
         fp = self.fp_inp[idx][0].to(inp.device, non_blocking=True)
         if len(inp.shape) == 2:
             inp = inp.unsqueeze(0)
@@ -58,12 +78,25 @@ class GPTAQ:
         Xfp = _core.as_bf16_tokens(fp.to(inp.dtype))
         if Xfp.shape != X.shape:
             raise ValueError(f"fp_inp shape {tuple(Xfp.shape)} != input {tuple(X.shape)}")
-        n = self._n[idx]
-        beta = _core.f32(n / (n + tmp))
-        n += tmp
+        T = X.shape[0]
+        st = self._stagers[idx]
+        if st is None:
+            st = self._stagers[idx] = GramStager(self.columns, X.device, KIND_GPTAQ)
+        if not st.fits(T):
+            self._flush_staged(idx)
+            if st.can_stage(T):
+                st.reserve(T)
+        n = self._n[idx] + tmp
+        if st.fits(T):
+            st.stage(X, Xfp)
+        else:
+            # a batch larger than the staging budget: update directly
+            n0 = self._n_flushed[idx]
+            _core.gptaq_update(self._H[idx], self._dXXT[idx], X, Xfp, _core.sqrt_scale_sq(n),
+                               _core.f32(n0 / n))
+            self._n_flushed[idx] = n
         self._n[idx] = n
         self.nsamples[idx] += tmp
-        _core.gptaq_update(self.H[idx], self.dXXT[idx], X, Xfp, _core.sqrt_scale_sq(n), beta)
         del self.fp_inp[idx][0]
 
     def _run_compensation_block(self, weight, hinv, p, scale, zero, backend, graph):

@@ -7,6 +7,7 @@ G2PTQ) and GPTQ's compensation, inherited unchanged.
 import torch
 
 from . import _core, _lib
+from ._stage import KIND_WEIGHTED, GramStager
 from .gptq_utils import GPTQ, _compensate
 
 
@@ -29,12 +30,24 @@ class GPTQGuided(GPTQ):
         self.act_square = torch.zeros((self.num_layers, self.columns), device=self.dev)
         self.index = torch.tensor([0] * self.num_layers, device=self.dev)
         self._k = [0] * self.num_layers
+        self._stagers = [None] * self.num_layers
         assert self.rows % self.num_groups == 0, (
             f"Number of rows ({self.rows}) must be divisible by num_groups ({self.num_groups})")
 
     def _maybe_onload_hessian(self):
         """gptq_guided_utils.py:53-57."""
         return _core.onload_attrs(self, ("H",), enabled=self.offload_hessians, device=self.dev)
+
+    # ``H`` (inherited staged attribute) reads fold the staged tokens in first:
+    # the Hessians are plain sums, so a flush is H += Σ staged.
+    def _flush_staged(self, idx=None):
+        stagers = getattr(self, "_stagers", None)
+        if not stagers:
+            return
+        for i in (range(self.num_layers) if idx is None else (idx,)):
+            st = stagers[i]
+            if st is not None and st.k:
+                st.flush(self._H[i], 1.0, 1.0)
 
     @torch.no_grad()
     def add_batch(self, idx, inp, out):
@@ -49,10 +62,24 @@ class GPTQGuided(GPTQ):
         self._k[idx] = k + bsz
         self.index[idx] += bsz
         X = _core.as_bf16_tokens(inp)
-        sal = sal.reshape(-1, sal.shape[-1]).float()
+        sal = sal.reshape(-1, sal.shape[-1]).float().contiguous()
         n_tokens = X.shape[0]
-        _core.weighted_update(self.H[idx], X, sal, 1.0, 1.0, self.act_square[idx],
-                              _core.f32(1 / n_tokens), 1.0)
+        act_alpha = _core.f32(1 / n_tokens)
+        st = self._stagers[idx]
+        if st is None:
+            st = self._stagers[idx] = GramStager(self.columns, X.device, KIND_WEIGHTED,
+                                                 self.num_groups)
+        if not st.fits(n_tokens):
+            self._flush_staged(idx)
+            if st.can_stage(n_tokens):
+                st.reserve(n_tokens)
+        if st.fits(n_tokens):
+            st.stage(X, S=sal, s_scale=1.0, act=self.act_square[idx], act_alpha=act_alpha,
+                     act_beta=1.0)
+        else:
+            # a batch larger than the staging budget: update directly
+            _core.weighted_update(self._H[idx], X, sal, 1.0, 1.0, self.act_square[idx],
+                                  act_alpha, 1.0)
 
     def fasterquant(self, blocksize=128, percdamp=0.01, groupsize=-1, actorder=False,
                     static_groups=False, export_compressed_tensors=False, backend="hip",

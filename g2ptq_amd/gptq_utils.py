@@ -9,7 +9,7 @@ the fused lazy-batch compensation in libg2ptq_hip.so.
 import torch
 
 from . import _core, _lib
-from ._stage import GramStager
+from ._stage import GramStager, staged_attr
 from .graph_utils import run_graph, validate_tensors
 
 
@@ -45,18 +45,7 @@ class GPTQ:
     # ``H`` reads flush the staged calibration tokens first, so every reader
     # (fasterquant, onload/offload, shared-input copies, callers) sees the
     # Hessian of every batch added so far.
-    @property
-    def H(self):
-        self._flush_staged()
-        return self._H
-
-    @H.setter
-    def H(self, value):
-        self._H = value
-        if value is None:
-            for st in getattr(self, "_stagers", None) or ():
-                if st is not None:
-                    st.release()
+    H = staged_attr("H")
 
     def _flush_staged(self, idx=None):
         stagers = getattr(self, "_stagers", None)

@@ -79,8 +79,9 @@ int g2ptq_fake_quantize(void* stream, const float* x, int64_t rows, int64_t cols
  * ---------------------------------------------------------------------- */
 
 /* Bytes of workspace needed by the *_update calls below for T tokens of C
- * features (kind: 0 Hessian, 1 GPTAQ, 2 saliency-weighted). */
-int g2ptq_hessian_workspace(int64_t T, int64_t C, int kind, size_t* bytes);
+ * features (kind: 0 Hessian, 1 GPTAQ, 2 saliency-weighted with G groups;
+ * G is ignored for kinds 0 and 1). */
+int g2ptq_hessian_workspace(int64_t T, int64_t C, int kind, int64_t G, size_t* bytes);
 
 /* H = beta·H + alpha·XᵀX (H symmetric C×C fp32, both triangles written).
  * X: T × C bf16 (ld ldx).  Replaces GPTQ.add_batch's update
@@ -112,6 +113,18 @@ int g2ptq_gptaq_update(void* stream, const uint16_t* X, const uint16_t* Xfp, int
                        int64_t ldx, int64_t ldxf, float alpha, float beta, float* H, float* Dx,
                        int64_t ld, void* ws, size_t ws_bytes);
 
+/* Staged GPTAQ accumulation (the two halves of g2ptq_gptaq_update, as for
+ * g2ptq_hessian_stage / _gram).  XT holds three contiguous planes of
+ * rows × ldt bf16 (rows = g2ptq_hessian_stage_rows(C)): Xᵀ and the bf16 high
+ * and low parts of (X_fp − X)ᵀ.  Same alignment and padding rules as
+ * g2ptq_hessian_stage / _gram.  Replaces the per-batch update of
+ * GPTAQ.add_batch (gptq_utils/gptaq_utils.py:130-148). */
+int g2ptq_gptaq_stage(void* stream, const uint16_t* X, const uint16_t* Xfp, int64_t T, int64_t C,
+                      int64_t ldx, int64_t ldxf, uint16_t* XT, int64_t ldt, int64_t t_off);
+int g2ptq_gptaq_gram_workspace(int64_t K, int64_t C, size_t* bytes);
+int g2ptq_gptaq_gram(void* stream, uint16_t* XT, int64_t ldt, int64_t K, int64_t C, float alpha,
+                     float beta, float* H, float* Dx, int64_t ld, void* ws, size_t ws_bytes);
+
 /* Saliency-weighted Hessians for G groups:
  *   H[g] = beta·H[g] + alpha·Σ_t S[t,g]·x_t x_tᵀ   (H: G × C × C, stride sH)
  *   act  = act_beta·act + act_alpha·Σ_t x_t²       (act: C, nullable)
@@ -123,6 +136,23 @@ int g2ptq_weighted_hessian_update(void* stream, const uint16_t* X, int64_t T, in
                                   float alpha, float beta, float* H, int64_t ldh, int64_t sH,
                                   float* act, float act_alpha, float act_beta,
                                   void* ws, size_t ws_bytes);
+
+/* Staged weighted accumulation.  XT holds 1 + 2G contiguous planes of
+ * rows × ldt bf16: Xᵀ, then for each group g the bf16 high and low parts of
+ * (x·S[t,g]·s_scale)ᵀ; s_scale folds a per-batch factor (G2PTQ's 1/T_b)
+ * into the staged tokens.  g2ptq_weighted_stage also applies the act update
+ * of g2ptq_weighted_hessian_update for the batch.  g2ptq_weighted_gram
+ * applies H[g] = beta·H[g] + alpha·Σ over the first K staged columns.  Same
+ * alignment and padding rules as g2ptq_hessian_stage / _gram.  Replace the
+ * per-batch updates of G2PTQ.add_batch (gptq_utils/g2ptq_utils.py:182-201)
+ * and GPTQGuided.add_batch (gptq_utils/gptq_guided_utils.py:59-81). */
+int g2ptq_weighted_stage(void* stream, const uint16_t* X, int64_t T, int64_t C, int64_t ldx,
+                         const float* S, int64_t G, int64_t lds, float s_scale, uint16_t* XT,
+                         int64_t ldt, int64_t t_off, float* act, float act_alpha, float act_beta);
+int g2ptq_weighted_gram_workspace(int64_t K, int64_t C, size_t* bytes);
+int g2ptq_weighted_gram(void* stream, uint16_t* XT, int64_t ldt, int64_t K, int64_t C, int64_t G,
+                        float alpha, float beta, float* H, int64_t ldh, int64_t sH, void* ws,
+                        size_t ws_bytes);
 
 /* ------------------------------------------------------------------------
  * Hessian preparation and factor

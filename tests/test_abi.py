@@ -53,8 +53,15 @@ def test_size_queries(lib):
     assert _lib.query_size("g2ptq_factor_workspace", 2, 4096) >= 2 * 4096 * 4096 * 4
     assert _lib.query_size("g2ptq_compensate_workspace", 0, 2, 4096, 4096, 128) >= 2 * 4096 * 128 * 4
     assert _lib.query_size("g2ptq_trust_region_workspace", 4, 256, 4096) > 0
-    assert _lib.query_size("g2ptq_hessian_workspace", 8192, 4096, 0) > 0
+    assert _lib.query_size("g2ptq_hessian_workspace", 8192, 4096, 0, 0) > 0
     assert _lib.query_size("g2ptq_hessian_gram_workspace", 32768, 4096) >= 0
+    # GPTAQ stages 3 planes and the weighted update 1 + 2G; both need split partials
+    h = _lib.query_size("g2ptq_hessian_workspace", 8192, 4096, 0, 0)
+    assert _lib.query_size("g2ptq_hessian_workspace", 8192, 4096, 1, 0) > h
+    assert (_lib.query_size("g2ptq_hessian_workspace", 8192, 4096, 2, 4)
+            > _lib.query_size("g2ptq_hessian_workspace", 8192, 4096, 2, 1))
+    assert _lib.query_size("g2ptq_gptaq_gram_workspace", 32768, 4096) > 0
+    assert _lib.query_size("g2ptq_weighted_gram_workspace", 32768, 4096) > 0
     rows = _lib.query_size_i64("g2ptq_hessian_stage_rows", 4096)
     assert rows >= 4096 and rows % 256 == 0
 
@@ -62,6 +69,8 @@ def test_size_queries(lib):
 @pytest.mark.parametrize("call", [
     ("g2ptq_find_params", (None, None, 4, 4, 4, 4, 1, None, None, 1, None)),
     ("g2ptq_find_params", (None, None, 4, 4, 4, 17, 1, None, None, 1, None)),
+    ("g2ptq_weighted_gram", (None, None, 64, 0, 128, 0, 1.0, 0.0, None, 128, 0, None, 0)),
+    ("g2ptq_gptaq_stage", (None, None, None, 8, 128, 128, 128, None, 64, 0)),
 ])
 def test_argument_errors_return_arg_status(lib, call):
     name, args = call

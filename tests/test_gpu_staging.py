@@ -83,3 +83,103 @@ def test_staged_hessian_feeds_fasterquant_and_free(dev):
     e_ref = oflows.reconstruction_error(W0, ref["Q"].bfloat16().float(), st["H"])
     assert abs(e_hip - e_ref) <= 0.005 * e_ref
     gq.free()
+
+
+def _small_budget(monkeypatch, C, planes, tokens=8192):
+    from g2ptq_amd import _lib, _stage
+    rows = _lib.query_size_i64("g2ptq_hessian_stage_rows", C)
+    monkeypatch.setattr(_stage, "DEFAULT_BUDGET", planes * rows * 2 * tokens)
+
+
+# (bsz, T) batches: overflow the 8192-token staging buffer (flush), grow it, and
+# one batch (9000 tokens) larger than the budget takes the direct update.
+_SHAPES = [(2, 700), (1, 2048), (3, 300), (1, 2500), (1, 9000), (4, 512), (1, 64), (1, 1)]
+
+
+def test_staged_gptaq_across_flushes_growth_and_reads(dev, monkeypatch):
+    """GPTAQ.add_batch staged (Xᵀ and the hi/lo planes of (X_fp − X)ᵀ) equals the
+    reference's per-batch update of H and dXXT (gptaq_utils.py:130-148)."""
+    from g2ptq_amd import GPTAQ
+    C, B = 640, 2
+    _small_budget(monkeypatch, C, 3, tokens=4096)
+    gq = GPTAQ(_layers(B, 64, C, dev))
+    st = ohess.gptaq_state(B, C)
+    g = gen(78)
+    sig = torch.exp(torch.randn(C, generator=g))
+    for step, (bsz, T) in enumerate(_SHAPES):
+        x = (torch.randn(bsz, T, C, generator=g) * sig).bfloat16()
+        xf = (x.float() + 0.05 * sig * torch.randn(bsz, T, C, generator=g)).bfloat16()
+        for b in range(B):
+            gq.fp_inp[b].append(xf.reshape(-1, C).to(dev))
+            gq.add_batch(b, x.to(dev), None)
+            ohess.gptaq_add_batch(st, b, x, xf.reshape(-1, C))
+        if step == 3:
+            torch.cuda.synchronize()
+            for b in range(B):
+                _close(gq.H[b], st["H"][b], f"mid-way H {b}")
+    torch.cuda.synchronize()
+    for b in range(B):
+        _close(gq.H[b], st["H"][b], f"final H {b}")
+        D, Dr = gq.dXXT[b].cpu(), st["dXXT"][b]
+        assert (D - Dr).abs().max() <= 5e-5 * Dr.abs().max(), f"dXXT {b}"
+    assert gq.nsamples.tolist() == st["nsamples"]
+
+
+def _weighted_close(Hd, Hr, what):
+    Hd = Hd.detach().cpu()
+    for gi in range(Hd.shape[0]):
+        assert torch.equal(Hd[gi], Hd[gi].T), f"{what}: group {gi} not symmetric"
+    err = (Hd - Hr).abs().max().item()
+    assert err <= 1e-5 * Hr.abs().max().item(), f"{what}: max err {err}"
+
+
+def test_staged_g2ptq_across_flushes_growth_and_reads(dev, monkeypatch):
+    """G2PTQ.add_batch staged (per-batch 1/T_b folded into the hi/lo planes of
+    x·s) equals the reference's running per-batch mean (g2ptq_utils.py:182-201)."""
+    from g2ptq_amd import G2PTQ
+    C, B, G = 384, 2, 4
+    _small_budget(monkeypatch, C, 1 + 2 * G, tokens=4096)
+    g = gen(79)
+    shapes = [(1, 700), (1, 2048), (1, 300), (1, 2500), (1, 5000), (1, 512), (1, 64), (1, 1)]
+    xs = [(torch.randn(T, C, generator=g) * 2).bfloat16() for _, T in shapes]
+    sals = [torch.rand(T, G, generator=g) * 3 for _, T in shapes]
+    gq = G2PTQ(_layers(B, 64, C, dev), [[s.to(dev) for s in sals] for _ in range(B)],
+               [None] * B, G)
+    st = ohess.g2ptq_state(B, G, C)
+    for step, (x, s) in enumerate(zip(xs, sals)):
+        for b in range(B):
+            gq.add_batch(b, x.to(dev), None)
+            ohess.g2ptq_add_batch(st, b, x, s)
+        if step == 3:
+            torch.cuda.synchronize()
+            for b in range(B):
+                _weighted_close(gq.H[b], st["H"][b], f"mid-way layer {b}")
+    torch.cuda.synchronize()
+    for b in range(B):
+        _weighted_close(gq.H[b], st["H"][b], f"final layer {b}")
+        act = gq.act_square[b].cpu()
+        assert (act - st["act_square"][b]).abs().max() <= 1e-5 * st["act_square"][b].abs().max()
+    assert gq.index.tolist() == st["index"]
+    assert gq.total_tokens.tolist() == st["total_tokens"]
+
+
+def test_staged_guided_across_flushes(dev, monkeypatch):
+    """GPTQGuided.add_batch staged equals the reference's plain sums
+    (gptq_guided_utils.py:59-81)."""
+    from g2ptq_amd import GPTQGuided
+    C, G, seq = 320, 2, 600
+    _small_budget(monkeypatch, C, 1 + 2 * G, tokens=4096)
+    g = gen(80)
+    N = 12
+    x = torch.randn(N, seq, C, generator=g).bfloat16()
+    sal = torch.rand(N, seq, G, generator=g)
+    gq = GPTQGuided(_layers(1, 32, C, dev), [sal], G)
+    st = ohess.guided_state(1, G, C)
+    for bsz in (1, 3, 2, 5, 1):
+        k = st["index"][0]
+        gq.add_batch(0, x[k:k + bsz].to(dev), None)
+        ohess.guided_add_batch(st, 0, x[k:k + bsz], sal)
+    torch.cuda.synchronize()
+    _weighted_close(gq.H[0], st["H"][0], "guided")
+    act = gq.act_square[0].cpu()
+    assert (act - st["act_square"][0]).abs().max() <= 1e-5 * st["act_square"][0].abs().max()
