@@ -74,89 +74,119 @@ __global__ void reverse_damp_kernel(const float* __restrict__ H, int64_t C, floa
 
 // Cholesky + in-place inverse of the nbk×nbk (nbk <= 64) diagonal block at (k, k).
 //
-// One wave64 per layer, lane i owning row i of L (a[0..63]) and of
-// X = L⁻¹ (x[0..63]) in registers; rows at or past nbk are identity rows.
-// Step j (fully unrolled, so every register index is a compile-time
-// constant): the pivot L[j][j] is read from lane j; column j of L, scaled by
-// 1/sqrt(pivot), and the (unscaled) row j of X are published through LDS;
-// every lane applies the rank-1 updates of its own rows:
-//   L[i][c] −= L[i][j]·L[c][j]          (c > j)
-//   X[i][c] −= L[i][j]/d_j · X[j][c]    (c ≤ j; the row is zero beyond)
-// the Gauss–Jordan elimination of [L | I] with row j's division by d_j
-// deferred: each lane scales its own X row by its pivot's reciprocal at the
-// end.  The published column and row are read as whole 16-byte vectors, all
-// in flight before the first update.  A single wave needs no barriers:
-// its LDS writes and reads are processed in order.  Entries of a above the
-// diagonal accumulate values that are never read.
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 1))) void potrf_diag_kernel(
-    float* WA, int64_t C, int64_t k, int nbk, int* st, int* info) {
-  const int64_t b = blockIdx.x;
-  if (st[b]) return;
-  __shared__ __attribute__((aligned(16))) float colL[NB];
-  __shared__ __attribute__((aligned(16))) float rowX[NB];
-  float* Wb = WA + b * C * C + k * C + k;
-  const int i = threadIdx.x;
-  float a[NB], x[NB];
-#pragma unroll
-  for (int c = 0; c < NB; ++c) {
-    a[c] = (i < nbk) ? ((c <= i) ? Wb[(int64_t)i * C + c] : 0.f) : (c == i ? 1.f : 0.f);
-    x[c] = (c == i) ? 1.f : 0.f;
-  }
-  rowX[i] = 0.f;
-  float myrd = 1.f;
-  int fail = 0;
-#pragma clang loop unroll(full)
-  for (int j = 0; j < NB; ++j) {
-    const float djj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a[j]), j));
-    if (!(djj > 0.f)) {  // also catches NaN; wave-uniform
-      fail = j + 1;
-      break;
+// Two wave64s per layer; rows at or past nbk are identity rows.  Lane i of
+// wave 0 holds row i of the trailing matrix A, lane i of wave 1 column i of
+// the inverse X = L⁻¹ being formed, both as a register array v rotated so
+// that entry 0 is always the current pivot column / row: before step j,
+// wave 0 has v[c] = A[i][j + c] and wave 1 v[c] = (e_i − Σ_{k<j} L[·][k]·X[k][i])[j + c].
+// Step j:
+//   wave 0: pivot d = sqrt(A[j][j]) (read from lane j), m = l_ij = A[i][j]/d
+//           (i > j); publishes column j of L below the diagonal and 1/d
+//           through LDS (double buffered by step parity);
+//   barrier;
+//   wave 1: m = X[j][i] = v[0]/d;
+//   both:   v[c] ← v[c+1] − m·L[j+1+c][j]
+// i.e. the right-looking Cholesky and the forward substitution of L·x = e_i
+// sharing the broadcast column, one per wave so each runs half the FMAs.
+// Entries that correspond to columns past the block hold finite leftovers
+// that are never read.
+//
+// The step code is a loop, not unrolled: a wave executing straight-line code
+// once per launch is bound by instruction fetch.  The 64 steps run as four
+// 16-step phases over 64, 48, 32 and 16 live entries (the rotated arrays
+// shrink by one column per step), so the compiled kernel stays a few KB.  A
+// non-positive (or NaN) pivot is recorded and the block is not stored.
+constexpr int XP = NB + 1;  // LDS row pitch of the X / load staging buffer
+
+template <int LEN>
+__device__ __forceinline__ void chol_inv_phase(float (&v)[NB], int j0, int i, int w,
+                                               float (*colL)[NB], float* rdl, float* Xs,
+                                               int& fail) {
+#pragma clang loop unroll(disable)
+  for (int jj = 0; jj < 16; ++jj) {
+    const int j = j0 + jj;
+    const int buf = j & 1;
+    float m = 0.f;
+    if (w == 0) {
+      const float djj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[0]), j));
+      fail = (fail == 0 && !(djj > 0.f)) ? j + 1 : fail;  // also catches NaN
+      // 1/sqrt from the hardware reciprocal square root (about 1 ulp): the
+      // factor is held to fp32 tolerance, not to correctly rounded bits.
+      const float rd = __builtin_amdgcn_rsqf(djj);
+      m = (i > j) ? v[0] * rd : 0.f;
+      if (i > j) colL[buf][i - j - 1] = m;
+      if (i == 0) rdl[buf] = rd;
     }
-    // 1/sqrt and sqrt from the hardware reciprocal square root (about 1 ulp):
-    // the factor is held to fp32 tolerance, not to correctly rounded bits, and
-    // this keeps two long correctly-rounded sequences off the pivot chain.
-    const float rd = __builtin_amdgcn_rsqf(djj);
-    const float d = djj * rd;
-    const float lij = (i > j) ? a[j] * rd : 0.f;
-    a[j] = (i == j) ? d : lij;
-    myrd = (i == j) ? rd : myrd;
-    colL[i] = lij;
-    if (i == j) {
-#pragma unroll
-      for (int c = 0; c <= j; c += 4)
-        *reinterpret_cast<float4*>(&rowX[c]) = make_float4(
-            x[c], c + 1 <= j ? x[c + 1] : 0.f, c + 2 <= j ? x[c + 2] : 0.f, c + 3 <= j ? x[c + 3] : 0.f);
+    __syncthreads();
+    if (w == 1) {
+      m = v[0] * rdl[buf];
+      Xs[j * XP + i] = m;
     }
-    __builtin_amdgcn_wave_barrier();
-    float cl[NB], rx[NB];
+    float cl[LEN];
 #pragma unroll
-    for (int q = j / 4; q < NB / 4; ++q) {
-      const float4 u = *reinterpret_cast<const float4*>(&colL[4 * q]);
+    for (int q = 0; q < LEN / 4; ++q) {
+      const float4 u = *reinterpret_cast<const float4*>(&colL[buf][4 * q]);
       cl[4 * q] = u.x; cl[4 * q + 1] = u.y; cl[4 * q + 2] = u.z; cl[4 * q + 3] = u.w;
     }
 #pragma unroll
-    for (int q = 0; q <= j / 4; ++q) {
-      const float4 v = *reinterpret_cast<const float4*>(&rowX[4 * q]);
-      rx[4 * q] = v.x; rx[4 * q + 1] = v.y; rx[4 * q + 2] = v.z; rx[4 * q + 3] = v.w;
-    }
-    const float m = lij * rd;
-#pragma unroll
-    for (int c = j + 1; c < NB; ++c) a[c] -= lij * cl[c];
-#pragma unroll
-    for (int c = 0; c <= j; ++c) x[c] -= m * rx[c];
-    __builtin_amdgcn_wave_barrier();
+    for (int c = 0; c + 1 < LEN; ++c) v[c] = v[c + 1] - m * cl[c];
+    v[LEN - 1] = 0.f;
   }
+}
+
+__global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1))) void potrf_diag_kernel(
+    float* WA, int64_t C, int64_t k, int nbk, int* st, int* info) {
+  const int64_t b = blockIdx.x;
+  if (st[b]) return;
+  __shared__ __attribute__((aligned(16))) float Xs[NB * XP];
+  __shared__ __attribute__((aligned(16))) float colL[2][NB];
+  __shared__ float rdl[2];
+  __shared__ int fail_s;
+  float* Wb = WA + b * C * C + k * C + k;
+  const int i = threadIdx.x & 63, w = threadIdx.x >> 6;
+  // Lower triangle of the block: row r through lane i of wave r & 1
+  // (coalesced; addresses clamped into the block so the loads need no
+  // branches), all 32 rows of a wave in flight together, transposed through
+  // LDS so that lane i of wave 0 holds row i.
+  {
+    const int ci = i < nbk ? i : nbk - 1;
+    float x[NB / 2];
+#pragma unroll
+    for (int h = 0; h < NB / 2; ++h) {
+      const int r = 2 * h + w;
+      const int rr = r < nbk ? r : nbk - 1;
+      x[h] = Wb[(int64_t)rr * C + ci];
+    }
+#pragma unroll
+    for (int h = 0; h < NB / 2; ++h) {
+      const int r = 2 * h + w;
+      Xs[r * XP + i] = (r < nbk && i < nbk) ? (i <= r ? x[h] : 0.f) : (r == i ? 1.f : 0.f);
+    }
+    colL[w][i] = 0.f;
+  }
+  __syncthreads();
+  float v[NB];
+#pragma unroll
+  for (int c = 0; c < NB; ++c) v[c] = (w == 0) ? Xs[i * XP + c] : (c == i ? 1.f : 0.f);
+  __syncthreads();
+  int fail = 0;
+  chol_inv_phase<64>(v, 0, i, w, colL, rdl, Xs, fail);
+  chol_inv_phase<48>(v, 16, i, w, colL, rdl, Xs, fail);
+  chol_inv_phase<32>(v, 32, i, w, colL, rdl, Xs, fail);
+  chol_inv_phase<16>(v, 48, i, w, colL, rdl, Xs, fail);
+  if (w == 0 && i == 0) fail_s = fail;
+  __syncthreads();
+  fail = fail_s;
   if (fail) {
-    if (i == 0) {
+    if (threadIdx.x == 0) {
       info[b] = (int)(k + fail);
       st[b] = 1;
     }
     return;
   }
   if (i < nbk) {
-#pragma unroll
-    for (int c = 0; c < NB; ++c)
-      if (c < nbk) Wb[(int64_t)i * C + c] = (c <= i) ? x[c] * myrd : 0.f;
+#pragma unroll 4
+    for (int r = w; r < nbk; r += 2) Wb[(int64_t)r * C + i] = (i <= r) ? Xs[r * XP + i] : 0.f;
   }
 }
 
@@ -272,7 +302,7 @@ extern "C" int g2ptq_inv_chol_upper(void* stream, const float* H, int64_t B, int
   auto factor_panel = [&](int64_t k, int64_t kb) -> int {
     for (int64_t j = k; j < k + kb; j += NB) {
       const int nbk = (int)std::min<int64_t>(NB, k + kb - j);
-      hipLaunchKernelGGL(potrf_diag_kernel, dim3((unsigned)B), dim3(64), 0, s, WA, C, j, nbk,
+      hipLaunchKernelGGL(potrf_diag_kernel, dim3((unsigned)B), dim3(128), 0, s, WA, C, j, nbk,
                          st, info);
       G2PTQ_LAUNCHED();
       const int64_t rest = C - j - nbk;
