@@ -98,29 +98,40 @@ __global__ void reverse_damp_kernel(const float* __restrict__ H, int64_t C, floa
 // non-positive (or NaN) pivot is recorded and the block is not stored.
 constexpr int XP = NB + 1;  // LDS row pitch of the X / load staging buffer
 
+// Wave 0's pivot step for column j: d = sqrt(v[0] of lane j), m = l_ij, and
+// column j of L below the diagonal plus 1/d published in LDS buffer j & 1.
+__device__ __forceinline__ float chol_pivot(float v0, int j, int i, float (*colL)[NB], float* rdl,
+                                            int& fail) {
+  const float djj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v0), j));
+  fail = (fail == 0 && !(djj > 0.f)) ? j + 1 : fail;  // also catches NaN
+  // 1/sqrt from the hardware reciprocal square root (about 1 ulp): the factor
+  // is held to fp32 tolerance, not to correctly rounded bits.
+  const float rd = __builtin_amdgcn_rsqf(djj);
+  const float m = (i > j) ? v0 * rd : 0.f;
+  if (i > j) colL[j & 1][i - j - 1] = m;
+  if (i == 0) rdl[j & 1] = rd;
+  return m;
+}
+
+// Steps j0 .. j0+15 over LEN live entries.  Wave 0 enters step j with its
+// multiplier m already computed and column j published; it updates v[0] (the
+// next pivot column) first and publishes column j+1 before the rest of step
+// j's updates, so the LDS write latency and the pivot chain overlap the bulk
+// FMAs.  Buffers alternate by step parity: column j+1 goes to the buffer that
+// wave 1 finished reading before the barrier of step j.
 template <int LEN>
 __device__ __forceinline__ void chol_inv_phase(float (&v)[NB], int j0, int i, int w,
-                                               float (*colL)[NB], float* rdl, float* Xs,
+                                               float (*colL)[NB], float* rdl, float* Xs, float& m,
                                                int& fail) {
 #pragma clang loop unroll(disable)
   for (int jj = 0; jj < 16; ++jj) {
     const int j = j0 + jj;
     const int buf = j & 1;
-    float m = 0.f;
-    if (w == 0) {
-      const float djj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[0]), j));
-      fail = (fail == 0 && !(djj > 0.f)) ? j + 1 : fail;  // also catches NaN
-      // 1/sqrt from the hardware reciprocal square root (about 1 ulp): the
-      // factor is held to fp32 tolerance, not to correctly rounded bits.
-      const float rd = __builtin_amdgcn_rsqf(djj);
-      m = (i > j) ? v[0] * rd : 0.f;
-      if (i > j) colL[buf][i - j - 1] = m;
-      if (i == 0) rdl[buf] = rd;
-    }
-    __syncthreads();
+    __syncthreads();  // column j and 1/d_j are published
+    float mm = m;
     if (w == 1) {
-      m = v[0] * rdl[buf];
-      Xs[j * XP + i] = m;
+      mm = v[0] * rdl[buf];
+      Xs[j * XP + i] = mm;
     }
     float cl[LEN];
 #pragma unroll
@@ -128,8 +139,10 @@ __device__ __forceinline__ void chol_inv_phase(float (&v)[NB], int j0, int i, in
       const float4 u = *reinterpret_cast<const float4*>(&colL[buf][4 * q]);
       cl[4 * q] = u.x; cl[4 * q + 1] = u.y; cl[4 * q + 2] = u.z; cl[4 * q + 3] = u.w;
     }
+    v[0] = v[1] - mm * cl[0];
+    if (w == 0 && j + 1 < NB) m = chol_pivot(v[0], j + 1, i, colL, rdl, fail);
 #pragma unroll
-    for (int c = 0; c + 1 < LEN; ++c) v[c] = v[c + 1] - m * cl[c];
+    for (int c = 1; c + 1 < LEN; ++c) v[c] = v[c + 1] - mm * cl[c];
     v[LEN - 1] = 0.f;
   }
 }
@@ -137,13 +150,13 @@ __device__ __forceinline__ void chol_inv_phase(float (&v)[NB], int j0, int i, in
 __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1))) void potrf_diag_kernel(
     float* WA, int64_t C, int64_t k, int nbk, int* st, int* info) {
   const int64_t b = blockIdx.x;
-  if (st[b]) return;
   __shared__ __attribute__((aligned(16))) float Xs[NB * XP];
   __shared__ __attribute__((aligned(16))) float colL[2][NB];
   __shared__ float rdl[2];
   __shared__ int fail_s;
   float* Wb = WA + b * C * C + k * C + k;
   const int i = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int skip = st[b];
   // Lower triangle of the block: row r through lane i of wave r & 1
   // (coalesced; addresses clamped into the block so the loads need no
   // branches), all 32 rows of a wave in flight together, transposed through
@@ -168,15 +181,21 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   float v[NB];
 #pragma unroll
   for (int c = 0; c < NB; ++c) v[c] = (w == 0) ? Xs[i * XP + c] : (c == i ? 1.f : 0.f);
-  __syncthreads();
+  __syncthreads();  // Xs is reused for X below
   int fail = 0;
-  chol_inv_phase<64>(v, 0, i, w, colL, rdl, Xs, fail);
-  chol_inv_phase<48>(v, 16, i, w, colL, rdl, Xs, fail);
-  chol_inv_phase<32>(v, 32, i, w, colL, rdl, Xs, fail);
-  chol_inv_phase<16>(v, 48, i, w, colL, rdl, Xs, fail);
+  float m = 0.f;
+  if (w == 0) m = chol_pivot(v[0], 0, i, colL, rdl, fail);
+  chol_inv_phase<64>(v, 0, i, w, colL, rdl, Xs, m, fail);
+  chol_inv_phase<48>(v, 16, i, w, colL, rdl, Xs, m, fail);
+  chol_inv_phase<32>(v, 32, i, w, colL, rdl, Xs, m, fail);
+  chol_inv_phase<16>(v, 48, i, w, colL, rdl, Xs, m, fail);
   if (w == 0 && i == 0) fail_s = fail;
   __syncthreads();
   fail = fail_s;
+  // Layers already done (a damp retry) run the steps on whatever the block
+  // holds and store nothing: testing the flag only here lets its load overlap
+  // the block loads instead of preceding them.
+  if (skip) return;
   if (fail) {
     if (threadIdx.x == 0) {
       info[b] = (int)(k + fail);
