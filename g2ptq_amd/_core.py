@@ -265,10 +265,14 @@ def compensate(variant, W, U, quantizers, blocksize, groupsize, static_groups, q
               _lib.ptr(ztab), _lib.ptr(Q), _lib.ptr(W_int), _lib.ptr(Scale), _lib.ptr(flags),
               _lib.ptr(ws), ws.numel())
     if dynamic:
-        for i, q in enumerate(quantizers):
-            q.scale = stab[i].view(B * R, 1)
-            q.zero = ztab[i].view(B * R, 1)
-            q._ready = True
+        scales = stab.view(len(quantizers), B * R, 1).unbind(0)
+        zeros = ztab.view(len(quantizers), B * R, 1).unbind(0)
+        for q, s_i, z_i in zip(quantizers, scales, zeros):
+            # the registered buffers, set directly (nn.Module.__setattr__ per
+            # attribute costs more than the rest of this loop)
+            q._buffers["scale"] = s_i
+            q._buffers["zero"] = z_i
+            q.__dict__["_ready"] = True
     return Q, W_int, Scale
 
 

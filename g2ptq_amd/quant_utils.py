@@ -84,6 +84,24 @@ class WeightQuantizer(torch.nn.Module):
         self.register_buffer("zero", torch.zeros(shape))
         self._ready = False
 
+    def __deepcopy__(self, memo):
+        """An independent copy, as ``copy.deepcopy`` of the module would make,
+        without nn.Module's generic deep-copy machinery (make_group_quantizers
+        copies one quantizer per group: 112 copies for a 14336-column layer)."""
+        cls = self.__class__
+        new = cls.__new__(cls)
+        memo[id(self)] = new
+        d = new.__dict__
+        for k, v in self.__dict__.items():
+            if k == "_buffers":
+                v = v.__class__((n, None if b is None else b.clone()) for n, b in v.items())
+            elif isinstance(v, (dict, set, list)):
+                v = v.copy()
+            elif isinstance(v, torch.Tensor):
+                v = v.clone()
+            d[k] = v
+        return new
+
     def configure(self, bits, perchannel: bool = False, sym: bool = True, mse: bool = False,
                   norm: float = 2.4, grid: int = 50, maxshrink: float = 0.5,
                   weight_groupsize: int = -1, hclip: bool = False) -> None:

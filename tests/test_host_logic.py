@@ -98,3 +98,25 @@ def test_shared_input_hessian_membership():
     sh2 = SharedInputHessian([(c, 0)])
     sh2.finalize()
     assert not hasattr(c, "_shared_factor")             # not every slot is a member
+
+
+def test_weight_quantizer_deepcopy_is_independent():
+    """make_group_quantizers deep-copies one quantizer per group: the copies are
+    independent modules with the same configuration and buffers."""
+    import copy
+    from g2ptq_amd import WeightQuantizer, make_group_quantizers
+    q = WeightQuantizer()
+    q.configure(3, perchannel=True, sym=False, mse=True, grid=25)
+    q.scale = torch.full((4, 1), 0.5)
+    q.zero = torch.full((4, 1), -2.0)
+    c = copy.deepcopy(q)
+    assert type(c) is WeightQuantizer
+    assert (c.bits, c.sym, c.mse, c.grid, c.maxq, c.minq) == (3, False, True, 25, 3, -4)
+    assert torch.equal(c.scale, q.scale) and torch.equal(c.zero, q.zero)
+    c.scale.mul_(2)
+    c.bits = 4
+    assert q.scale[0, 0] == 0.5 and q.bits == 3
+    assert list(dict(c.named_buffers())) == ["scale", "zero"]
+    assert set(c.state_dict()) == {"scale", "zero"}
+    qs = make_group_quantizers(q, 300, 128)
+    assert len(qs) == 3 and len({id(x.scale) for x in qs}) == 3
