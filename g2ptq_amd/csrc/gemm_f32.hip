@@ -61,13 +61,33 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmF32 g, int64_t tm,
   const int z = blockIdx.z;
   const int64_t b1 = z / g.batch2, b2 = z % g.batch2;
   if (g.skip && g.skip[b1]) return;
-  // XCD-aware renumbering (workgroups go round-robin over 8 XCDs): every XCD
-  // gets a contiguous range of the grouped tile order.
   const int64_t nwg = gridDim.x, bid = blockIdx.x;
-  const int64_t q8 = nwg >> 3, r8 = nwg & 7, xcd = bid & 7;
-  const int64_t id = xcd * q8 + (xcd < r8 ? xcd : r8) + (bid >> 3);
   int64_t im, in;
-  tile_of(id, tm, tn, im, in);
+  if (g.tri == 0) {
+    // XCD-aware renumbering (workgroups go round-robin over 8 XCDs): every
+    // XCD gets a contiguous range of the grouped tile order.
+    const int64_t q8 = nwg >> 3, r8 = nwg & 7, xcd = bid & 7;
+    const int64_t id = xcd * q8 + (xcd < r8 ? xcd : r8) + (bid >> 3);
+    tile_of(id, tm, tn, im, in);
+  } else if (g.tri & 2) {
+    // Triangular B: tile (im, in) multiplies K − n0 columns, so the work falls
+    // from left to right.  Longest first: bands of GH tile-columns from the
+    // left, each walked row by row, in dispatch order (no renumbering, so the
+    // 8 XCDs share every band evenly; consecutive tiles of a row land on
+    // different XCDs, each XCD keeping to one column of the band).
+    const int64_t per = GH * tm;
+    const int64_t band = bid / per, r = bid - band * per;
+    const int64_t c0 = band * GH;
+    const int64_t h = tn - c0 < GH ? tn - c0 : GH;
+    in = c0 + r % h;
+    im = r / h;
+  } else {
+    // Triangular A: tile (im, in) multiplies m0 + BM columns, so the work
+    // grows downwards.  Longest first: the grouped order from the bottom
+    // group up, in dispatch order (each XCD keeps to one row of a group).
+    tile_of(bid, tm, tn, im, in);
+    im = tm - 1 - im;
+  }
   const int64_t m0 = im * BM, n0 = in * BN;
   if (g.uplo == 1 && n0 > m0 + BM - 1) return;
   if (g.uplo == 2 && m0 > n0 + BN - 1) return;
