@@ -392,17 +392,21 @@ __global__ __launch_bounds__(64) void sweep_kernel(SweepArgs a) {
   if (bad && act && a.flags) atomicOr(a.flags, FLAG_BAD_SCALE);
 }
 
-// Quad sweep: the same computation, with each row split over a quad of four
-// lanes (16 rows per wave).  In every 32-column panel lane `sub` of a quad
-// owns columns 4s + sub (s = 0..7).  Column jj's quantisation runs on all
-// lanes but only its owner (sub == jj % 4) holds the column, and its error
-// (and x, z) reach the other three lanes with a DPP quad broadcast; every
+// Split sweep: the same computation, with each row split over L lanes (a quad,
+// L = 4: 16 rows per wave; or a 16-lane DPP row, L = 16: 4 rows per wave).  In
+// every 32-column panel lane `sub` of a row's group owns columns L·s + sub
+// (s < 32/L).  Column jj's quantisation runs on all L lanes but only its owner
+// (sub == jj % L) holds the column, and its error (and x, z) reach the other
+// lanes with a DPP broadcast (quad_perm, or row_newbcast for L = 16); every
 // lane then applies the rank-1 update to the columns it owns.  Each element
 // still receives exactly the reference's sequence of rounded products and
 // differences, in the same order, so the results equal sweep_kernel's bit for
-// bit; the per-wave dependency chain is a quarter as long, and a block is
-// spread over four times as many waves.  A workgroup of four waves (64 rows)
-// stages the block's U triangle once for all of them.
+// bit.  The per-row dependency chain (two divisions per column) is the same
+// for every L; a larger L spreads a block's rows over more waves and gives
+// each lane fewer columns to update, which pays when the block has few rows
+// (a wave per SIMD at most), while L = 4 does less redundant chain work per
+// row when rows are plentiful.  A workgroup of four waves (256/L rows) stages
+// the block's U triangle once for all of them.
 template <int O>
 __device__ __forceinline__ float quad_bcast_c(float v) {
   return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), O * 0x55, 0xf, 0xf, false));
@@ -415,17 +419,45 @@ __device__ __forceinline__ float quad_bcast(float v, int o) {
     default: return quad_bcast_c<3>(v);
   }
 }
+// Lane o of each 16-lane row to the whole row (DPP row_newbcast:o).
+template <int O>
+__device__ __forceinline__ float row_bcast_c(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x150 + O, 0xf, 0xf, false));
+}
+template <int L>
+__device__ __forceinline__ float group_bcast(float v, int o) {
+  if (L == 4) return quad_bcast(v, o);
+  switch (o & 15) {
+    case 0: return row_bcast_c<0>(v);
+    case 1: return row_bcast_c<1>(v);
+    case 2: return row_bcast_c<2>(v);
+    case 3: return row_bcast_c<3>(v);
+    case 4: return row_bcast_c<4>(v);
+    case 5: return row_bcast_c<5>(v);
+    case 6: return row_bcast_c<6>(v);
+    case 7: return row_bcast_c<7>(v);
+    case 8: return row_bcast_c<8>(v);
+    case 9: return row_bcast_c<9>(v);
+    case 10: return row_bcast_c<10>(v);
+    case 11: return row_bcast_c<11>(v);
+    case 12: return row_bcast_c<12>(v);
+    case 13: return row_bcast_c<13>(v);
+    case 14: return row_bcast_c<14>(v);
+    default: return row_bcast_c<15>(v);
+  }
+}
 
-template <int V>
+template <int V, int L>
 __global__ __launch_bounds__(256) void sweep4_kernel(SweepArgs a) {
-  constexpr int PW = 32, RW = 64;  // panel width, rows per workgroup (16 per wave)
+  constexpr int PW = 32, RW = 256 / L;  // panel width, rows per workgroup
+  constexpr int NS = PW / L;            // panel columns per lane
   __shared__ float Us[kTri];
   __shared__ float Ps[(V == 1) ? kTri : 1];
   __shared__ float e_s[kMaxBlock * RW];
   __shared__ float t_s[(V == 1) ? kMaxBlock * RW : 1];
   __shared__ float z_s[(V == 2) ? kMaxBlock * RW : 1];
 
-  const int tid = threadIdx.x, rr = tid >> 2, sub = tid & 3;
+  const int tid = threadIdx.x, rr = tid / L, sub = tid % L;
   const int64_t b = blockIdx.y;
   const int64_t r0 = (int64_t)blockIdx.x * RW + rr;
   const bool act = r0 < a.R;
@@ -504,11 +536,11 @@ __global__ __launch_bounds__(256) void sweep4_kernel(SweepArgs a) {
   float last_x = 0.f;
 
   for (int p0 = 0; p0 < n; p0 += PW) {
-    // ---- panel inputs of the lane's 8 columns, all issued before any store --
-    float w[8], gh[8], sv[8], zv[8], zg[8];
+    // ---- panel inputs of the lane's NS columns, all issued before any store -
+    float w[NS], gh[NS], sv[NS], zv[NS], zg[NS];
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const int j = p0 + 4 * s + sub;
+    for (int s = 0; s < NS; ++s) {
+      const int j = p0 + L * s + sub;
       int gidx = 0;
       if (a.colgroup) gidx = a.colgroup[j];
       else if (a.gsize > 0) gidx = (int)((int)a.col0 + j) / (int)a.gsize;
@@ -529,12 +561,12 @@ __global__ __launch_bounds__(256) void sweep4_kernel(SweepArgs a) {
       const float* Uj = Us + tri_base(j, n) + p0 + sub;
       const float* Pj = (V == 1) ? Ps + tri_base(j, n) + p0 + sub : nullptr;
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        const float u = Uj[4 * s];
+      for (int s = 0; s < NS; ++s) {
+        const float u = Uj[L * s];
         if (V == 0) {
           w[s] = __fsub_rn(w[s], __fmul_rn(u, e));
         } else if (V == 1) {
-          w[s] = __fadd_rn(__fsub_rn(w[s], __fmul_rn(u, e)), __fmul_rn(Pj[4 * s], t));
+          w[s] = __fadd_rn(__fsub_rn(w[s], __fmul_rn(u, e)), __fmul_rn(Pj[L * s], t));
         } else {
           w[s] = __fsub_rn(__fsub_rn(w[s], gh[s]), __fmul_rn(u, e));
           gh[s] = __fsub_rn(gh[s], __fmul_rn(u, zj));
@@ -542,10 +574,10 @@ __global__ __launch_bounds__(256) void sweep4_kernel(SweepArgs a) {
       }
     }
     // ---- sweep the panel column by column -----------------------------------
-    float qb[8], ib[8], eb[8], gb[8];
+    float qb[NS], ib[NS], eb[NS], gb[NS];
 #pragma unroll
     for (int jj = 0; jj < PW; ++jj) {
-      const int sl = jj >> 2, o = jj & 3;
+      const int sl = jj / L, o = jj % L;
       const bool own = sub == o;
       const int j = p0 + jj;
       const float x = w[sl];  // meaningful on the owner lane
@@ -557,9 +589,9 @@ __global__ __launch_bounds__(256) void sweep4_kernel(SweepArgs a) {
       float err0;
       if (V == 2) err0 = __fdiv_rn(__fsub_rn(__fsub_rn(x, deq), gh[sl]), d);
       else err0 = __fdiv_rn(__fsub_rn(x, deq), d);
-      const float err = quad_bcast(err0, o);
-      const float xb = (V == 1 || jj == PW - 1) ? quad_bcast(x, o) : 0.f;
-      const float zj = (V == 2) ? quad_bcast(zg[sl], o) : 0.f;
+      const float err = group_bcast<L>(err0, o);
+      const float xb = (V == 1 || jj == PW - 1) ? group_bcast<L>(x, o) : 0.f;
+      const float zj = (V == 2) ? group_bcast<L>(zg[sl], o) : 0.f;
       bad |= own && !(sc > 0.f);
       qb[sl] = own ? deq : qb[sl];
       ib[sl] = own ? q : ib[sl];
@@ -574,15 +606,15 @@ __global__ __launch_bounds__(256) void sweep4_kernel(SweepArgs a) {
       const float* Uj = Us + tri_base(j, n) + p0 + sub;
       const float* Pj = (V == 1) ? Ps + tri_base(j, n) + p0 + sub : nullptr;
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        if (4 * s + 3 <= jj) continue;           // every column of the slot is done
-        const bool upd = 4 * s > jj || sub > jj - 4 * s;
-        const float u = Uj[4 * s];
+      for (int s = 0; s < NS; ++s) {
+        if (L * s + L - 1 <= jj) continue;       // every column of the slot is done
+        const bool upd = L * s > jj || sub > jj - L * s;
+        const float u = Uj[L * s];
         if (V == 0) {
           const float nw = __fsub_rn(w[s], __fmul_rn(u, err));
           w[s] = upd ? nw : w[s];
         } else if (V == 1) {
-          const float nw = __fadd_rn(__fsub_rn(w[s], __fmul_rn(u, err)), __fmul_rn(Pj[4 * s], xb));
+          const float nw = __fadd_rn(__fsub_rn(w[s], __fmul_rn(u, err)), __fmul_rn(Pj[L * s], xb));
           w[s] = upd ? nw : w[s];
         } else {
           const float nw = __fsub_rn(__fsub_rn(w[s], gh[s]), __fmul_rn(u, err));
@@ -595,8 +627,8 @@ __global__ __launch_bounds__(256) void sweep4_kernel(SweepArgs a) {
     // ---- panel outputs ------------------------------------------------------
     if (act) {
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        const int j = p0 + 4 * s + sub;
+      for (int s = 0; s < NS; ++s) {
+        const int j = p0 + L * s + sub;
         Qo[(int64_t)j * a.qc] = qb[s];
         if (Io) Io[(int64_t)j * a.ic] = ib[s];
         if (Eo) Eo[(int64_t)j * a.ec] = eb[s];
@@ -627,8 +659,15 @@ template <int V>
 void launch_variant(hipStream_t stream, const SweepArgs& a, dim3 grid, bool vec) {
   const bool full = (a.n % 32) == 0;
   if (full) {
-    dim3 g4((unsigned)cdiv(a.R, (int64_t)64), grid.y);
-    hipLaunchKernelGGL((sweep4_kernel<V>), g4, dim3(256), 0, stream, a);
+    // 16 lanes per row while that keeps the block within about two waves per
+    // SIMD (1024 SIMDs), else a quad per row.
+    if ((int64_t)grid.y * a.R <= 8192) {
+      dim3 g16((unsigned)cdiv(a.R, (int64_t)16), grid.y);
+      hipLaunchKernelGGL((sweep4_kernel<V, 16>), g16, dim3(256), 0, stream, a);
+    } else {
+      dim3 g4((unsigned)cdiv(a.R, (int64_t)64), grid.y);
+      hipLaunchKernelGGL((sweep4_kernel<V, 4>), g4, dim3(256), 0, stream, a);
+    }
     return;
   }
   if (vec && full)

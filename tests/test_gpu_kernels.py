@@ -27,6 +27,9 @@ CASES = (
     ("symmetric_4bit_block32", 3, 32, 17, 7, False, 403),
     ("asymmetric_2bit_block64", 1, 64, 45, 1, True, 404),
     ("symmetric_8bit_block96", 2, 96, 70, 127, False, 405),
+    # more than 8192 rows in all: the quad-per-row sweep (fewer rows: 16 lanes per row)
+    ("symmetric_4bit_block64_many_rows", 2, 64, 4200, 7, False, 406),
+    ("asymmetric_3bit_block32_many_rows", 1, 32, 8500, 3, True, 407),
 )
 
 
