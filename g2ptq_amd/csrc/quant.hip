@@ -20,6 +20,28 @@ __device__ __forceinline__ float clamp_nan(float v, float lo, float hi) {
   return v < lo ? lo : (v > hi ? hi : v);
 }
 
+// a / b correctly rounded, from y = RN(1/b): Markstein's sequence
+// q = RN(a·y), r = a − b·q (exact through the FMA), RN(q + r·y) (P. Markstein,
+// "Computation of elementary functions on the IBM RISC System/6000
+// processor", IBM J. Res. Dev. 34(1), 1990).  It equals the IEEE quotient
+// whenever r is exactly representable and nothing overflows, which holds for
+// |a|, |q| in [2^-100, 2^100]; any lane outside that range (zero, tiny, huge,
+// infinite or NaN operands) takes the IEEE division, on a wave-uniform branch
+// that real data never enters.  Three dependent operations instead of the
+// eleven of the IEEE division sequence on the sweep's per-column chain.
+__device__ __forceinline__ float div_rn_recip(float a, float b, float y) {
+  const float q = __fmul_rn(a, y);
+  const float r = __fmaf_rn(-b, q, a);
+  float res = __fmaf_rn(r, y, q);
+  const float aa = fabsf(a), aq = fabsf(q);
+  const bool slow = !(aa >= 0x1p-100f && aa <= 0x1p100f && aq >= 0x1p-100f && aq <= 0x1p100f);
+  if (__builtin_amdgcn_ballot_w64(slow) != 0) {
+    asm volatile("" ::: "memory");  // keeps the branch: the division is not speculated
+    res = slow ? __fdiv_rn(a, b) : res;
+  }
+  return res;
+}
+
 // ---------------------------------------------------------------------------
 // find_params: one quantization group per row, 16 lanes per row.
 // ---------------------------------------------------------------------------
@@ -456,6 +478,8 @@ __global__ __launch_bounds__(256) void sweep4_kernel(SweepArgs a) {
   __shared__ float e_s[kMaxBlock * RW];
   __shared__ float t_s[(V == 1) ? kMaxBlock * RW : 1];
   __shared__ float z_s[(V == 2) ? kMaxBlock * RW : 1];
+  __shared__ __attribute__((aligned(16))) float rdiag[kMaxBlock];  // RN(1 / U_jj)
+  __shared__ __attribute__((aligned(16))) float dg[kMaxBlock];     // U_jj
 
   const int tid = threadIdx.x, rr = tid / L, sub = tid % L;
   const int64_t b = blockIdx.y;
@@ -519,6 +543,12 @@ __global__ __launch_bounds__(256) void sweep4_kernel(SweepArgs a) {
     }
   }
   __syncthreads();
+  if (tid < n) {
+    const float d = Us[tri_base(tid, n) + tid];
+    dg[tid] = d;
+    rdiag[tid] = __fdiv_rn(1.f, d);
+  }
+  __syncthreads();
 
   const float* Win = a.W + b * a.wb + r * a.wr;
   const float* Sp = a.S + b * a.sb + r * a.sr;
@@ -553,42 +583,83 @@ __global__ __launch_bounds__(256) void sweep4_kernel(SweepArgs a) {
       }
     }
     // ---- replay updates of the columns swept in earlier panels (LDS only) ---
-    for (int j = 0; j < p0; ++j) {
-      const float e = e_s[j * RW + rr];
-      float t = 0.f, zj = 0.f;
-      if (V == 1) t = t_s[j * RW + rr];
-      if (V == 2) zj = z_s[j * RW + rr];
-      const float* Uj = Us + tri_base(j, n) + p0 + sub;
-      const float* Pj = (V == 1) ? Ps + tri_base(j, n) + p0 + sub : nullptr;
+    // Eight columns at a time: their LDS operands are all read before the
+    // updates, which then run in the reference's column order.
+    for (int j0 = 0; j0 < p0; j0 += 8) {
+      constexpr int RB = 8;
+      float e[RB], t[RB], zj[RB], u[RB][NS], pu[RB][NS];
 #pragma unroll
-      for (int s = 0; s < NS; ++s) {
-        const float u = Uj[L * s];
-        if (V == 0) {
-          w[s] = __fsub_rn(w[s], __fmul_rn(u, e));
-        } else if (V == 1) {
-          w[s] = __fadd_rn(__fsub_rn(w[s], __fmul_rn(u, e)), __fmul_rn(Pj[L * s], t));
-        } else {
-          w[s] = __fsub_rn(__fsub_rn(w[s], gh[s]), __fmul_rn(u, e));
-          gh[s] = __fsub_rn(gh[s], __fmul_rn(u, zj));
+      for (int q = 0; q < RB; ++q) {
+        const int j = j0 + q;
+        e[q] = e_s[j * RW + rr];
+        if (V == 1) t[q] = t_s[j * RW + rr];
+        if (V == 2) zj[q] = z_s[j * RW + rr];
+        const float* Uj = Us + tri_base(j, n) + p0 + sub;
+        const float* Pj = (V == 1) ? Ps + tri_base(j, n) + p0 + sub : nullptr;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+          u[q][s] = Uj[L * s];
+          if (V == 1) pu[q][s] = Pj[L * s];
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < RB; ++q) {
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+          if (V == 0) {
+            w[s] = __fsub_rn(w[s], __fmul_rn(u[q][s], e[q]));
+          } else if (V == 1) {
+            w[s] = __fadd_rn(__fsub_rn(w[s], __fmul_rn(u[q][s], e[q])), __fmul_rn(pu[q][s], t[q]));
+          } else {
+            w[s] = __fsub_rn(__fsub_rn(w[s], gh[s]), __fmul_rn(u[q][s], e[q]));
+            gh[s] = __fsub_rn(gh[s], __fmul_rn(u[q][s], zj[q]));
+          }
         }
       }
     }
     // ---- sweep the panel column by column -----------------------------------
-    float qb[NS], ib[NS], eb[NS], gb[NS];
+    // The panel's pivots and their reciprocals are read up front, and each
+    // column's U row one column ahead, so the per-column dependency chain
+    // (quantise, error, broadcast, update) never waits for LDS.
+    float qb[NS], ib[NS], eb[NS], gb[NS], ysv[NS], dcol[PW], ycol[PW];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) ysv[s] = __fdiv_rn(1.f, sv[s]);
+#pragma unroll
+    for (int q4 = 0; q4 < PW / 4; ++q4) {
+      const float4 dv = *reinterpret_cast<const float4*>(&dg[p0 + 4 * q4]);
+      const float4 yv = *reinterpret_cast<const float4*>(&rdiag[p0 + 4 * q4]);
+      dcol[4 * q4] = dv.x; dcol[4 * q4 + 1] = dv.y; dcol[4 * q4 + 2] = dv.z; dcol[4 * q4 + 3] = dv.w;
+      ycol[4 * q4] = yv.x; ycol[4 * q4 + 1] = yv.y; ycol[4 * q4 + 2] = yv.z; ycol[4 * q4 + 3] = yv.w;
+    }
+    float uc[NS], pc[NS];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      uc[s] = Us[tri_base(p0, n) + p0 + sub + L * s];
+      if (V == 1) pc[s] = Ps[tri_base(p0, n) + p0 + sub + L * s];
+    }
 #pragma unroll
     for (int jj = 0; jj < PW; ++jj) {
       const int sl = jj / L, o = jj % L;
       const bool own = sub == o;
       const int j = p0 + jj;
+      float un[NS], pn[NS];
+      if (jj + 1 < PW) {
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+          un[s] = Us[tri_base(j + 1, n) + p0 + sub + L * s];
+          if (V == 1) pn[s] = Ps[tri_base(j + 1, n) + p0 + sub + L * s];
+        }
+      }
       const float x = w[sl];  // meaningful on the owner lane
       const float sc = sv[sl];
       const float z0 = zv[sl];
-      const float q = clamp_nan(__fadd_rn(rintf(__fdiv_rn(x, sc)), z0), minq, fmaxq);
+      const float q = clamp_nan(__fadd_rn(rintf(div_rn_recip(x, sc, ysv[sl])), z0), minq, fmaxq);
       const float deq = __fmul_rn(sc, __fsub_rn(q, z0));
-      const float d = Us[tri_base(j, n) + j];
+      const float d = dcol[jj];
+      const float yd = ycol[jj];
       float err0;
-      if (V == 2) err0 = __fdiv_rn(__fsub_rn(__fsub_rn(x, deq), gh[sl]), d);
-      else err0 = __fdiv_rn(__fsub_rn(x, deq), d);
+      if (V == 2) err0 = div_rn_recip(__fsub_rn(__fsub_rn(x, deq), gh[sl]), d, yd);
+      else err0 = div_rn_recip(__fsub_rn(x, deq), d, yd);
       const float err = group_bcast<L>(err0, o);
       const float xb = (V == 1 || jj == PW - 1) ? group_bcast<L>(x, o) : 0.f;
       const float zj = (V == 2) ? group_bcast<L>(zg[sl], o) : 0.f;
@@ -603,24 +674,29 @@ __global__ __launch_bounds__(256) void sweep4_kernel(SweepArgs a) {
         if (V == 2) z_s[j * RW + rr] = zj;
       }
       if (jj == PW - 1) last_x = xb;
-      const float* Uj = Us + tri_base(j, n) + p0 + sub;
-      const float* Pj = (V == 1) ? Ps + tri_base(j, n) + p0 + sub : nullptr;
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
         if (L * s + L - 1 <= jj) continue;       // every column of the slot is done
         const bool upd = L * s > jj || sub > jj - L * s;
-        const float u = Uj[L * s];
+        const float u = uc[s];
         if (V == 0) {
           const float nw = __fsub_rn(w[s], __fmul_rn(u, err));
           w[s] = upd ? nw : w[s];
         } else if (V == 1) {
-          const float nw = __fadd_rn(__fsub_rn(w[s], __fmul_rn(u, err)), __fmul_rn(Pj[L * s], xb));
+          const float nw = __fadd_rn(__fsub_rn(w[s], __fmul_rn(u, err)), __fmul_rn(pc[s], xb));
           w[s] = upd ? nw : w[s];
         } else {
           const float nw = __fsub_rn(__fsub_rn(w[s], gh[s]), __fmul_rn(u, err));
           const float ng = __fsub_rn(gh[s], __fmul_rn(u, zj));
           w[s] = upd ? nw : w[s];
           gh[s] = upd ? ng : gh[s];
+        }
+      }
+      if (jj + 1 < PW) {
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+          uc[s] = un[s];
+          if (V == 1) pc[s] = pn[s];
         }
       }
     }
