@@ -25,11 +25,6 @@ def check_backend(backend):
             "(every compensation kernel of this package is a HIP kernel)")
 
 
-def check_export(export_compressed_tensors):
-    if export_compressed_tensors:
-        raise NotImplementedError("compressed-tensors export is not part of this build")
-
-
 def f32(x):
     """Round a Python number to float32 the way a 0-d fp32 tensor op would."""
     return float(np.float32(x))

@@ -12,6 +12,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libg2ptq_hi
 
 FLAG_BAD_SCALE = 1
 FLAG_NAN_OUTPUT = 2
+FLAG_GROUP_SCALE = 4
 VARIANT_GPTQ, VARIANT_GPTAQ, VARIANT_G2PTQ = 0, 1, 2
 
 _p = ctypes.c_void_p
@@ -58,6 +59,8 @@ SIGNATURES = {
     "g2ptq_permute_sym": [_p, _p, _p, _i64, _i64, _p],
     "g2ptq_cast_check": [_p, _p, _p, _i64, _i32, _p],
     "g2ptq_to_f32": [_p, _p, _p, _i64, _i32],
+    "g2ptq_pack_quantized": [_p, _p, _i64, _p, _i64, _i64, _i64, _i32, _i64, _p, _i64, _p, _i32, _i64,
+                             _p],
     "g2ptq_gemm_f32": [_p, _i64, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _i32, _p, _i64, _i64,
                        _p, _i64, _i64, _f32, _f32],
 }

@@ -15,6 +15,7 @@ import torch
 from . import _core, _lib
 from .common_utils import fake_quantize_grouped
 from ._stage import KIND_WEIGHTED, GramStager, staged_attr
+from .compressed_tensors_utils import compress_layers
 from .gptq_utils import _compensate
 from .graph_utils import run_graph, validate_tensors
 
@@ -177,7 +178,6 @@ class G2PTQ:
                     export_compressed_tensors=False, backend="hip", graph=False):
         """g2ptq_utils.py:349-519."""
         _core.check_backend(backend)
-        _core.check_export(export_compressed_tensors)
         if self.quantizer[0].hclip:
             raise NotImplementedError("hclip (Hessian-diagonal clip search) is not implemented")
         W = _core.stack_weights_f32(self.layers)
@@ -234,6 +234,9 @@ class G2PTQ:
             W_int = _core.permute_cols(W_int, invperm)
             Scale = _core.permute_cols(Scale, invperm)
         Q = Q.view(B, R, C)
+        if export_compressed_tensors:
+            compress_layers(self.layers, Scale.view(B, R, C), W_int.view(B, R, C),
+                            self.quantizer[0].bits, groupsize, C)
         _core.write_back(self.layers, Q, flags)
         _core.finish(flags)
 

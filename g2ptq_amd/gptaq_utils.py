@@ -10,6 +10,7 @@ import torch
 
 from . import _core, _lib
 from ._stage import KIND_GPTAQ, GramStager, staged_attr
+from .compressed_tensors_utils import compress_layers
 from .gptq_utils import _compensate
 from .graph_utils import run_graph, validate_tensors
 
@@ -142,7 +143,6 @@ class GPTAQ:
                     backend="hip", graph=False):
         """gptaq_utils.py:263-391."""
         _core.check_backend(backend)
-        _core.check_export(export_compressed_tensors)
         if self.quantizer[0].hclip:
             raise NotImplementedError("hclip (Hessian-diagonal clip search) is not implemented")
         W = _core.stack_weights_f32(self.layers)
@@ -173,6 +173,9 @@ class GPTAQ:
             Q = _core.permute_cols(Q, invperm)
             W_int = _core.permute_cols(W_int, invperm)
             Scale = _core.permute_cols(Scale, invperm)
+        if export_compressed_tensors:
+            compress_layers(self.layers, Scale.view(B, R, C), W_int.view(B, R, C),
+                            self.quantizer[0].bits, groupsize, C)
         _core.write_back(self.layers, Q, flags)
         _core.finish(flags)
 

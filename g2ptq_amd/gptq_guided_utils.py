@@ -8,6 +8,7 @@ import torch
 
 from . import _core, _lib
 from ._stage import KIND_WEIGHTED, GramStager
+from .compressed_tensors_utils import compress_layers
 from .gptq_utils import GPTQ, _compensate
 
 
@@ -86,7 +87,6 @@ class GPTQGuided(GPTQ):
                     graph=False):
         """gptq_guided_utils.py:83-211."""
         _core.check_backend(backend)
-        _core.check_export(export_compressed_tensors)
         if self.quantizer[0].hclip:
             raise NotImplementedError("hclip (Hessian-diagonal clip search) is not implemented")
         W = _core.stack_weights_f32(self.layers)
@@ -112,6 +112,11 @@ class GPTQGuided(GPTQ):
                                       perm if static_groups and actorder else None, flags, graph)
         if actorder:
             Q = _core.permute_cols(Q, invperm)
+            W_int = _core.permute_cols(W_int, invperm)
+            Scale = _core.permute_cols(Scale, invperm)
+        if export_compressed_tensors:
+            compress_layers(self.layers, Scale.view(B, R, C), W_int.view(B, R, C),
+                            self.quantizer[0].bits, groupsize, C)
         _core.write_back(self.layers, Q.view(B, R, C), flags)
         _core.finish(flags)
 

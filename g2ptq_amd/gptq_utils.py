@@ -10,6 +10,7 @@ import torch
 
 from . import _core, _lib
 from ._stage import GramStager, staged_attr
+from .compressed_tensors_utils import compress_layers
 from .graph_utils import run_graph, validate_tensors
 
 
@@ -130,7 +131,6 @@ class GPTQ:
                     graph=False):
         """gptq_utils.py:234-353."""
         _core.check_backend(backend)
-        _core.check_export(export_compressed_tensors)
         W = _core.stack_weights_f32(self.layers)
         B, R, C = W.shape
         W_flat = W.view(B * R, C)
@@ -156,6 +156,9 @@ class GPTQ:
             Q = _core.permute_cols(Q, invperm)
             W_int = _core.permute_cols(W_int, invperm)
             Scale = _core.permute_cols(Scale, invperm)
+        if export_compressed_tensors:
+            compress_layers(self.layers, Scale.view(B, R, C), W_int.view(B, R, C),
+                            self.quantizer[0].bits, groupsize, C)
         _core.write_back(self.layers, Q, flags)
         _core.finish(flags)
 

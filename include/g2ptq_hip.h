@@ -35,6 +35,7 @@ extern "C" {
 /* Device-side flag bits (OR-ed into an int32 the caller owns). */
 #define G2PTQ_FLAG_BAD_SCALE 1   /* a scale was <= 0 or NaN (quant_utils.py:432 assert) */
 #define G2PTQ_FLAG_NAN_OUTPUT 2  /* NaN in quantized weights (gptq_utils.py:346-350) */
+#define G2PTQ_FLAG_GROUP_SCALE 4 /* scales differ within a group (compressed_tensors_utils.py:35 assert) */
 
 /* Compensation variants. */
 #define G2PTQ_VARIANT_GPTQ 0
@@ -259,6 +260,25 @@ int g2ptq_cast_check(void* stream, const float* in, void* out, int64_t n, int dt
 
 /* out fp32 = in (bf16/fp16/fp32 by dtype code as above), n elements. */
 int g2ptq_to_f32(void* stream, const void* in, float* out, int64_t n, int dtype);
+
+/* ------------------------------------------------------------------------
+ * compressed-tensors export
+ * ---------------------------------------------------------------------- */
+
+/* One layer's pack-quantized checkpoint tensors, the work of
+ * utils/compressed_tensors_utils.py:22-45 (compress) with compressed-tensors
+ * 0.18.0's pack_to_int32:
+ *   packed[r][w] = OR_{i < 32/bits} ((int8(codes[r][w·(32/bits) + i]) + 2^(bits−1))
+ *                  mod 2^bits) << (bits·i), columns past cols contributing 0;
+ *   scale_out[r][k] = scale[r][k·groupsize] cast to dtype (0 bf16, 1 fp16, 2 fp32),
+ *   and G2PTQ_FLAG_GROUP_SCALE in flags if any scale of a group differs from
+ *   the group's first (the reference asserts).
+ * codes, scale: rows × cols fp32 (ld ldc, lds); packed: rows × ceil(cols·bits/32)
+ * int32 (ld ldp); scale_out (nullable: pack only): rows × cols/groupsize (ld ldo). */
+int g2ptq_pack_quantized(void* stream, const float* codes, int64_t ldc, const float* scale,
+                         int64_t lds, int64_t rows, int64_t cols, int bits, int64_t groupsize,
+                         int32_t* packed, int64_t ldp, void* scale_out, int dtype, int64_t ldo,
+                         int* flags);
 
 /* Generic batched fp32 GEMM (MFMA): D = alpha·A·op(B) + beta·C for `batch`
  * matrices; A row-major M×K, B row-major K×N (b_trans = 0) or N×K

@@ -60,8 +60,6 @@ def test_backends_other_than_hip_are_rejected():
     with pytest.raises(NotImplementedError):
         _core.check_backend("torch")
     _core.check_backend("hip")
-    with pytest.raises(NotImplementedError):
-        _core.check_export(True)
 
 
 def test_f32_rounding():

@@ -13,6 +13,7 @@ from oracle import factor as ofactor
 from oracle import flows as oflows
 from oracle import hessian as ohess
 from oracle import original_loops as oloops
+from oracle import pack as opack
 from oracle import quant as oquant
 from tests._util import g2_inputs, gen, gptaq_p, ref_inputs
 
@@ -470,3 +471,74 @@ def test_trust_region_beta_bounds_and_identities():
     assert torch.allclose(GH, beta.unsqueeze(2) * torch.bmm(grad, Ainv), rtol=1e-3, atol=1e-9)
     b0, Z0, G0 = oflows.g2ptq_trust_region(grad, Ainv, U, Q, W, 0.0, False)
     assert torch.all(b0 == 0) and torch.all(Z0 == 0) and torch.all(G0 == 0)
+
+
+# ---------------------------------------------------------------------------
+# compressed-tensors packing (oracle/pack.py)
+# ---------------------------------------------------------------------------
+
+def _unpack_bits(packed, num_bits, cols):
+    """Independent unpacker: bit by bit through Python integers."""
+    pf = 32 // num_bits
+    out = []
+    for row in packed.tolist():
+        vals = []
+        for word in row:
+            u = word & 0xFFFFFFFF
+            for i in range(pf):
+                field = 0
+                for bit in range(num_bits):
+                    field |= ((u >> (num_bits * i + bit)) & 1) << bit
+                vals.append(field - (1 << (num_bits - 1)))
+        out.append(vals[:cols])
+    return torch.tensor(out, dtype=torch.int8)
+
+
+def test_pack_known_answers():
+    # 4 bits: codes -8..7 become fields 0..15 (uint4b8), first column lowest
+    codes = torch.arange(-8, 8, dtype=torch.int8).reshape(1, 16)
+    p = opack.pack_to_int32(codes, 4)
+    assert p.dtype == torch.int32 and p.shape == (1, 2)
+    assert p[0, 0].item() == 0x76543210
+    assert p[0, 1].item() == 0xFEDCBA98 - (1 << 32)
+    # 8 bits (uint8b128): [-128, -1, 0, 127] -> fields [0, 127, 128, 255]
+    p8 = opack.pack_to_int32(torch.tensor([[-128, -1, 0, 127]], dtype=torch.int8), 8)
+    assert p8[0, 0].item() == 0xFF807F00 - (1 << 32)
+    # 2 bits: [-2, -1, 0, 1] -> fields [0, 1, 2, 3]; the 12 missing columns are zero fields
+    p2 = opack.pack_to_int32(torch.tensor([[-2, -1, 0, 1]], dtype=torch.int8), 2)
+    assert p2.shape == (1, 1) and p2[0, 0].item() == (0 | 1 << 2 | 2 << 4 | 3 << 6)
+    with pytest.raises(ValueError):
+        opack.pack_to_int32(codes.int(), 4)
+    with pytest.raises(ValueError):
+        opack.pack_to_int32(codes, 9)
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 8])
+def test_pack_round_trip_and_layout(bits):
+    g = gen(600 + bits)
+    lo, hi = -(1 << (bits - 1)), (1 << (bits - 1)) - 1
+    codes = torch.randint(lo, hi + 1, (5, 37), generator=g).to(torch.int8)
+    p = opack.pack_to_int32(codes, bits)
+    pf = 32 // bits
+    assert p.shape == (5, -(-37 // pf))
+    assert torch.equal(_unpack_bits(p, bits, 37), codes)
+    # fields past the last column are zero (not offset codes)
+    tail = 37 % pf
+    if tail:
+        used = bits * tail
+        assert all((w & 0xFFFFFFFF) >> used == 0 for w in p[:, -1].tolist())
+
+
+def test_compress_group_scales_and_assert():
+    g = gen(610)
+    rows, cols, gs = 6, 256, 128
+    codes = torch.randint(-8, 8, (rows, cols), generator=g).float()
+    gscale = torch.rand(rows, cols // gs, generator=g) + 0.5
+    Scale = gscale.repeat_interleave(gs, dim=1)
+    out = opack.compress((rows, cols), torch.bfloat16, Scale, codes, 4, gs)
+    assert torch.equal(out["weight_scale"], gscale.to(torch.bfloat16))
+    assert out["weight_shape"].tolist() == [rows, cols]
+    assert torch.equal(_unpack_bits(out["weight_packed"], 4, cols), codes.to(torch.int8))
+    Scale[2, 5] += 1.0
+    with pytest.raises(AssertionError):
+        opack.compress((rows, cols), torch.bfloat16, Scale, codes, 4, gs)
