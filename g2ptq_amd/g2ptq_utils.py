@@ -206,7 +206,7 @@ class G2PTQ:
                 W_sub = _core.permute_cols(W_sub, perm)
                 H_sub.copy_(_core.permute_sym(H_sub, perm))
                 grads = _core.permute_cols(grads, perm)
-            Hinv, _ = _core.factor(H_sub, percdamp)
+            Hinv = self._factor(H_sub, percdamp, bool(actorder))
             if Q_sub is not None and actorder:
                 Q_sub = _core.permute_cols(Q_sub, perm)
         if gradient_step:
@@ -240,8 +240,32 @@ class G2PTQ:
         _core.write_back(self.layers, Q, flags)
         _core.finish(flags)
 
+    def _factor(self, H_sub, percdamp, actorder):
+        """The dampened inverse-Cholesky factor of the prepared Hessians.
+
+        The α autotune (g2ptq_utils.py:1481-1577) re-runs ``fasterquant`` for
+        every α with the Hessians restored in between: U depends on the
+        prepared H and the damp only, not on α (only the trust-region β
+        does), so it is kept with a copy of the H it came from and reused
+        while that H matches exactly (one device comparison instead of a
+        factorization).  Not used with offloaded Hessians, whose point is to
+        keep C² matrices off the device.
+        """
+        if self.offload_hessians:
+            return _core.factor(H_sub, percdamp)[0]
+        key = (percdamp, actorder)
+        cache = getattr(self, "_factor_cache", None)
+        if cache is not None and cache[0] == key and cache[1].shape == H_sub.shape \
+                and torch.equal(cache[1], H_sub):
+            return cache[2]
+        self._factor_cache = None
+        U, _ = _core.factor(H_sub, percdamp)
+        self._factor_cache = (key, H_sub.clone(), U)
+        return U
+
     def free(self):
         """g2ptq_utils.py:521-527."""
+        self._factor_cache = None
         self.H = None
         self.Losses = None
         self.gradients = None
