@@ -54,7 +54,186 @@ def parse():
     p.add_argument("--calibrate-copy", action="store_true",
                    help="run one 1 GiB device copy first (the known-size reference kernel "
                         "for rocprofv3 FETCH_SIZE / WRITE_SIZE scaling)")
+    p.add_argument("--workload", default="cfg2", choices=["cfg1", "cfg2", "cfg3", "cfg5"],
+                   help="BASELINE.json config (cfg2 is the benchmark line; the others "
+                        "report per-stage times of the parity configs)")
     return p.parse_args()
+
+
+# ---------------------------------------------------------------------------
+# The other BASELINE.json configs, reported per stage (not the benchmark line).
+# ---------------------------------------------------------------------------
+
+def _lognormal_channels(C, g, dev):
+    return torch.exp(torch.randn(C, device=dev, generator=g))
+
+
+def _tokens(n, C, sig, g, dev, chunk=16384):
+    x = torch.empty(n, C, device=dev, dtype=torch.bfloat16)
+    for t0 in range(0, n, chunk):
+        t1 = min(n, t0 + chunk)
+        x[t0:t1] = (torch.randn(t1 - t0, C, device=dev, generator=g) * sig).bfloat16()
+    return x
+
+
+def _linear(R, C, dtype, g, dev, outlier_cols=0):
+    lin = torch.nn.Linear(C, R, bias=False, device=dev, dtype=dtype)
+    w = torch.randn(R, C, device=dev, generator=g) * 0.02
+    if outlier_cols:
+        cols = torch.randperm(C, device=dev, generator=g)[:outlier_cols]
+        w[:, cols] *= 10
+    with torch.no_grad():
+        lin.weight.copy_(w.to(dtype))
+    return lin
+
+
+def workload_cfg1(dev, steps, warmup):
+    """one 4096×4096 fp32 linear (1 % of input columns ×10), GPTQ W4
+    asym g128, 262144 tokens in batches of 8192."""
+    from g2ptq_amd import GPTQ, WeightQuantizer, make_group_quantizers
+    g = torch.Generator(device=dev).manual_seed(42)
+    C, R, n = 4096, 4096, N_TOKENS
+    X = _tokens(n, C, _lognormal_channels(C, g, dev), g, dev)
+    lin = _linear(R, C, torch.float32, g, dev, outlier_cols=round(0.01 * C))
+    w0 = lin.weight.detach().clone()
+
+    def step(ev):
+        lin.weight.data.copy_(w0)
+        gq = GPTQ([lin])
+        q = WeightQuantizer()
+        q.configure(4, perchannel=True, sym=False)
+        gq.quantizer = make_group_quantizers(q, C, 128)
+        e = ev()
+        e[0].record()
+        for t0 in range(0, n, 8192):
+            gq.add_batch(0, X[t0:t0 + 8192].view(-1, SEQ, C), None)
+        gq.H  # fold the staged tokens
+        e[1].record()
+        e[2].record()
+        gq.fasterquant(blocksize=128, percdamp=0.01, groupsize=128, backend="hip")
+        e[3].record()
+        return e, 2.0 * n * C * C
+    return step, "llama-free single linear 4096x4096 fp32, GPTQ W4 asym g128, 1% outlier columns"
+
+
+def workload_cfg3(dev, steps, warmup):
+    """the 8B-shaped block with G2PTQ W3 g128, 4 row groups, α = 0.1,
+    gradients 1e-3·N(0,1)·|StudentT(3)| per row, saliencies σ_t²·χ²_{R/G}/(R/G)
+    with σ_t ~ LogNormal(0, 0.5).  Saliency-weighted Hessians are per linear."""
+    from g2ptq_amd import G2PTQ, WeightQuantizer, make_group_quantizers
+    g = torch.Generator(device=dev).manual_seed(42 + 2)
+    G, n, tb = 4, N_TOKENS, BSZ * SEQ
+    acts = {k: _tokens(n, C, _lognormal_channels(C, g, dev), g, dev) for k, C in INPUT_DIM.items()}
+    lins = {name: _linear(R, C, torch.bfloat16, g, dev) for name, (R, C, _) in LINEARS.items()}
+    w0 = {k: v.weight.detach().clone() for k, v in lins.items()}
+    grads, sals = {}, {}
+    t_dist = torch.distributions.StudentT(torch.tensor(3.0, device=dev))
+    for name, (R, C, key) in LINEARS.items():
+        tau = t_dist.sample((R,)).abs()
+        grads[name] = torch.randn(R, C, device=dev, generator=g) * 1e-3 * tau[:, None]
+        chi = torch.distributions.Chi2(torch.tensor(float(R // G), device=dev))
+        sal = []
+        for _ in range(0, n, tb):
+            sig = torch.exp(0.5 * torch.randn(tb, 1, device=dev, generator=g))
+            sal.append((sig ** 2 * chi.sample((tb, G)) / (R // G)).float())
+        sals[name] = sal
+    flops = 0.0
+    for name, (R, C, key) in LINEARS.items():
+        flops += G * 2.0 * n * C * C
+
+    def step(ev):
+        for k, v in lins.items():
+            v.weight.data.copy_(w0[k])
+        e = ev()
+        e[0].record()
+        insts = []
+        for names in SEQUENTIAL:
+            # same-shape linears of a group are layer-batched (k/v, gate/up)
+            by_shape = {}
+            for nm in names:
+                by_shape.setdefault(tuple(lins[nm].weight.shape), []).append(nm)
+            for shape, nms in by_shape.items():
+                gq = G2PTQ([lins[nm] for nm in nms], [list(sals[nm]) for nm in nms],
+                           [grads[nm] for nm in nms], G)
+                q = WeightQuantizer()
+                q.configure(3, perchannel=True, sym=True)
+                gq.quantizer = make_group_quantizers(q, shape[1], 128)
+                X = acts[LINEARS[nms[0]][2]]
+                for t0 in range(0, n, tb):
+                    for b in range(len(nms)):
+                        gq.add_batch(b, X[t0:t0 + tb], None)
+                gq.H
+                insts.append(gq)
+        e[1].record()
+        e[2].record()
+        for gq in insts:
+            gq.fasterquant(blocksize=128, percdamp=0.01, groupsize=128, alpha=0.1,
+                           enable_gradient_update=True, backend="hip")
+            gq.free()
+        e[3].record()
+        return e, flops
+    return step, "llama3-8b-block G2PTQ W3 sym g128, 4 row groups, alpha 0.1, 262144 tokens"
+
+
+def workload_cfg5(dev, steps, warmup):
+    """Llama-3-70B down_proj 8192×28672 bf16, GPTAQ W2 sym g64,
+    α = 0.25, X_fp = X + N(0, 0.05·σ_c), 262144 tokens in batches of 8192."""
+    from g2ptq_amd import GPTAQ, WeightQuantizer, make_group_quantizers
+    g = torch.Generator(device=dev).manual_seed(42 + 4)
+    C, R, n, tb = 28672, 8192, N_TOKENS, 8192
+    sig = _lognormal_channels(C, g, dev)
+    X = _tokens(n, C, sig, g, dev)
+    Xfp = torch.empty_like(X)
+    for t0 in range(0, n, 8192):
+        Xfp[t0:t0 + 8192] = (X[t0:t0 + 8192].float() + 0.05 * sig *
+                             torch.randn(8192, C, device=dev, generator=g)).bfloat16()
+    lin = _linear(R, C, torch.bfloat16, g, dev)
+    w0 = lin.weight.detach().clone()
+
+    def step(ev):
+        lin.weight.data.copy_(w0)
+        gq = GPTAQ([lin])
+        q = WeightQuantizer()
+        q.configure(2, perchannel=True, sym=True)
+        gq.quantizer = make_group_quantizers(q, C, 64)
+        e = ev()
+        e[0].record()
+        for t0 in range(0, n, tb):
+            gq.fp_inp[0].append(Xfp[t0:t0 + tb])
+            gq.add_batch(0, X[t0:t0 + tb].view(-1, 4096, C), None)
+        gq.H
+        e[1].record()
+        e[2].record()
+        gq.fasterquant(blocksize=128, percdamp=0.01, groupsize=64, alpha=0.25, backend="hip")
+        e[3].record()
+        gq.free()
+        return e, 4.0 * n * C * C
+    return step, "llama3-70b down_proj 8192x28672, GPTAQ W2 sym g64, alpha 0.25, 262144 tokens"
+
+
+def run_other(args, dev):
+    make = {"cfg1": workload_cfg1, "cfg3": workload_cfg3, "cfg5": workload_cfg5}[args.workload]
+    step, desc = make(dev, args.steps, args.warmup)
+    torch.cuda.synchronize()
+
+    def ev():
+        return [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+
+    for _ in range(args.warmup):
+        step(ev)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    recs = [step(ev) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / args.steps
+    h = sum(e[0].elapsed_time(e[1]) for e, _ in recs) / len(recs)
+    qz = sum(e[2].elapsed_time(e[3]) for e, _ in recs) / len(recs)
+    flops = recs[0][1]
+    print(json.dumps({"workload": args.workload, "config": desc, "sec_per_step": round(wall, 4),
+                      "stages_ms": {"hessian": round(h, 2), "factor_and_compensation": round(qz, 2)},
+                      "hessian_tflops": round(flops / (h / 1e3) / 1e12, 1),
+                      "hessian_flop_convention": "2*N*C^2 per Hessian product (GEMM convention)",
+                      "steps": args.steps, "warmup": args.warmup}), flush=True)
 
 
 def make_inputs(dev, n_tokens):
@@ -216,6 +395,9 @@ def main():
     dev = torch.device("cuda:0")
     from g2ptq_amd import _lib
     _lib.load()
+    if args.workload != "cfg2":
+        run_other(args, dev)
+        return
     acts, layers, w0 = make_inputs(dev, args.tokens)
     torch.cuda.synchronize()
     if args.calibrate_copy:

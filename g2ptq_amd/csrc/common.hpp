@@ -81,7 +81,9 @@ struct GemmF32 {
   int uplo = 0;
   // Structural zeros the kernel may skip (optimisation only; the skipped
   // products must be zero): bit 1 = A lower triangular (A[m][k] = 0 for
-  // k > m), bit 2 = B lower triangular (B[k][n] = 0 for k < n).
+  // k > m), bit 2 = B lower triangular (B[k][n] = 0 for k < n), bit 4 = A
+  // upper triangular (A[m][k] = 0 for k < m), bit 8 = B upper triangular
+  // (B[k][n] = 0 for k > n).
   int tri = 0;
   const int* skip = nullptr;  // optional per-b1 flag: nonzero => skip that entry
 };

@@ -250,11 +250,13 @@ extern "C" int g2ptq_gptaq_p(void* stream, const float* Dx, const float* U, int6
   hipStream_t s = as_stream(stream);
   float* T = static_cast<float*>(ws);
   const int64_t CC = C * C;
-  GemmF32 a;  // T = Dx · Uᵀ
+  GemmF32 a;  // T = Dx · Uᵀ, upper tiles only (triu(T, 1) is all that is used)
   a.M = C; a.N = C; a.K = C; a.batch = B;
   a.A = Dx; a.lda = C; a.sA = CC;
   a.B = U; a.ldb = C; a.sB = CC; a.b_kcontig = 1;
   a.D = T; a.ldd = C; a.sD = CC;
+  a.uplo = 2;
+  a.tri = 2;  // Uᵀ[k][n] = U[n][k] = 0 for k < n
   G2PTQ_TRY(gemm_f32(s, a));
   dim3 grid((unsigned)cdiv(C, 64), (unsigned)cdiv(C, 16), (unsigned)B);
   hipLaunchKernelGGL(triu1_kernel, grid, dim3(256), 0, s, T, C);
@@ -265,6 +267,9 @@ extern "C" int g2ptq_gptaq_p(void* stream, const float* Dx, const float* U, int6
   b.B = U; b.ldb = C; b.sB = CC;
   b.D = P; b.ldd = C; b.sD = CC;
   b.alpha = alpha;
+  // triu(T, 1)[m][k] = 0 for k <= m, U[k][n] = 0 for k > n: tile (m, n) sums
+  // k in [m0, n0 + BN) only, and tiles below the diagonal write zeros.
+  b.tri = 4 | 8;
   G2PTQ_TRY(gemm_f32(s, b));
   return G2PTQ_OK;
 }

@@ -69,6 +69,17 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmF32 g, int64_t tm,
     const int64_t q8 = nwg >> 3, r8 = nwg & 7, xcd = bid & 7;
     const int64_t id = xcd * q8 + (xcd < r8 ? xcd : r8) + (bid >> 3);
     tile_of(id, tm, tn, im, in);
+  } else if (g.tri & 8) {
+    // Triangular upper B: tile (im, in) multiplies at most n0 + BN columns
+    // (fewer still when A is upper too), so the work grows to the right.
+    // Longest first: bands of GH tile-columns from the right, each walked
+    // row by row from the top, in dispatch order.
+    const int64_t per = GH * tm;
+    const int64_t band = bid / per, r = bid - band * per;
+    const int64_t c0 = band * GH;
+    const int64_t h = tn - c0 < GH ? tn - c0 : GH;
+    in = tn - 1 - (c0 + r % h);
+    im = r / h;
   } else if (g.tri & 2) {
     // Triangular B: tile (im, in) multiplies K − n0 columns, so the work falls
     // from left to right.  Longest first: bands of GH tile-columns from the
@@ -99,6 +110,8 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmF32 g, int64_t tm,
   int64_t klo = 0, K = g.K;
   if (g.tri & 1) K = K < m0 + BM ? K : m0 + BM;
   if (g.tri & 2) klo = n0 / BK * BK;
+  if ((g.tri & 4) && m0 / BK * BK > klo) klo = m0 / BK * BK;
+  if (g.tri & 8) K = K < n0 + BN ? K : n0 + BN;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;

@@ -63,6 +63,30 @@ def test_gemm_f32_matches_fp64(dev, M, N, K, batch, b_trans):
     assert err <= 1e-5 * (K ** 0.5) * 4 + 1e-5, err
 
 
+@pytest.mark.parametrize("C,B", [(300, 2), (700, 1)])
+def test_gptaq_p_matches_fp64(dev, C, B):
+    """P = α·triu(dXXT·Uᵀ, 1)·U (gptaq_utils.py:349-352): both GEMMs skip the
+    structural zeros of the triangular operands (Uᵀ lower, triu(T, 1) and U
+    upper) and the first computes upper tiles only."""
+    from g2ptq_amd import _lib
+    g = gen(810 + C)
+    Dx = torch.randn(B, C, C, generator=g)
+    U = torch.triu(torch.randn(B, C, C, generator=g)) + 2 * torch.eye(C)
+    alpha = 0.25
+    ref = torch.stack([alpha * torch.triu(Dx[b].double() @ U[b].double().T, 1) @ U[b].double()
+                       for b in range(B)])
+    Dd, Ud = Dx.to(dev), U.to(dev)
+    P = torch.full((B, C, C), 3.0, device=dev)
+    ws = torch.empty(B * C * C * 4 + 256, dtype=torch.uint8, device=dev)
+    _lib.call("g2ptq_gptaq_p", _lib.stream_ptr(), _lib.ptr(Dd), _lib.ptr(Ud), B, C, alpha,
+              _lib.ptr(P), _lib.ptr(ws), ws.numel())
+    torch.cuda.synchronize()
+    P = P.cpu().double()
+    assert torch.all(torch.tril(P) == 0)  # strictly upper, zeros written below
+    err = (P - ref).abs().max().item()
+    assert err <= 2e-5 * ref.abs().max().item(), err
+
+
 @pytest.mark.parametrize("bits", [2, 3, 4, 8])
 @pytest.mark.parametrize("sym", [True, False])
 def test_find_params_bitexact(dev, bits, sym):
