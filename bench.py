@@ -54,7 +54,7 @@ def parse():
     p.add_argument("--calibrate-copy", action="store_true",
                    help="run one 1 GiB device copy first (the known-size reference kernel "
                         "for rocprofv3 FETCH_SIZE / WRITE_SIZE scaling)")
-    p.add_argument("--workload", default="cfg2", choices=["cfg1", "cfg2", "cfg3", "cfg5"],
+    p.add_argument("--workload", default="cfg2", choices=["cfg1", "cfg2", "cfg3", "cfg4", "cfg5"],
                    help="BASELINE.json config (cfg2 is the benchmark line; the others "
                         "report per-stage times of the parity configs)")
     return p.parse_args()
@@ -211,8 +211,87 @@ def workload_cfg5(dev, steps, warmup):
     return step, "llama3-70b down_proj 8192x28672, GPTAQ W2 sym g64, alpha 0.25, 262144 tokens"
 
 
+def workload_cfg4(dev, steps, warmup):
+    """Qwen3-MoE-style block, hidden 2048, 128 experts (gate/up
+    768×2048, down 2048×768), top-8 routing of 262144 tokens with Zipf(1.1)
+    expert popularity (Gumbel-top-8 on log p_e, p_e ∝ (e+1)^-1.1), GPTQ W4 sym
+    g128.  Each calibration batch (8192 tokens) delivers every expert its
+    routed tokens as a 2-D input (one sample, as the reference's MoE hooks);
+    an expert's gate and up share one Hessian; the 384 linears are
+    layer-batched 64 per launch by shape."""
+    from g2ptq_amd import GPTQ, WeightQuantizer, build_chunk_specs, make_group_quantizers
+    from g2ptq_amd.shared import SharedInputHessian
+    g = torch.Generator(device=dev).manual_seed(42 + 3)
+    E, topk, H, I, n, tb = 128, 8, 2048, 768, N_TOKENS, BSZ * SEQ
+    X = _tokens(n, H, _lognormal_channels(H, g, dev), g, dev)
+    sig_i = _lognormal_channels(I, g, dev)
+    logp = -1.1 * torch.log(torch.arange(1, E + 1, device=dev, dtype=torch.float32))
+    logp = logp - torch.logsumexp(logp, 0)
+    routed = []  # per batch: per expert (gate/up input, down input)
+    counts = torch.zeros(E, dtype=torch.int64, device=dev)
+    for t0 in range(0, n, tb):
+        u = torch.rand(tb, E, device=dev, generator=g).clamp_(1e-20, 1.0)
+        top = torch.topk(logp - torch.log(-torch.log(u)), topk, dim=1).indices
+        order = torch.argsort(top.reshape(-1), stable=True)
+        tok = torch.div(order, topk, rounding_mode="floor")
+        per = torch.bincount(top.reshape(-1), minlength=E)
+        counts += per
+        splits = per.tolist()
+        xs = X[t0:t0 + tb][tok].split(splits)
+        batch = []
+        for e in range(E):
+            xi = (torch.randn(splits[e], I, device=dev, generator=g) * sig_i).bfloat16()
+            batch.append((xs[e], xi))
+        routed.append(batch)
+    names = [f"e{e}.{k}" for e in range(E) for k in ("gate", "up", "down")]
+    shapes = {"gate": (I, H), "up": (I, H), "down": (H, I)}
+    lins = {nm: _linear(*shapes[nm.split(".")[1]], torch.bfloat16, g, dev) for nm in names}
+    w0 = {k: v.weight.detach().clone() for k, v in lins.items()}
+    flops = float((counts * (2 * H * H + 2 * I * I)).sum().item())
+    stats = {"min_tokens": int(counts.min()), "max_tokens": int(counts.max())}
+
+    def step(ev):
+        for k, v in lins.items():
+            v.weight.data.copy_(w0[k])
+        e_ = ev()
+        e_[0].record()
+        specs = build_chunk_specs(lins, 64)
+        slot, insts = {}, []
+        for spec in specs:
+            gq = GPTQ([lins[nm] for nm in spec.chunk_names])
+            q = WeightQuantizer()
+            q.configure(4, perchannel=True, sym=True)
+            gq.quantizer = make_group_quantizers(q, spec.columns, 128)
+            insts.append(gq)
+            for i, nm in enumerate(spec.chunk_names):
+                slot[nm] = (gq, i)
+        shares = [SharedInputHessian([slot[f"e{e}.gate"], slot[f"e{e}.up"]]) for e in range(E)]
+        for batch in routed:
+            for e in range(E):
+                xg, xd = batch[e]
+                if xg.shape[0]:
+                    shares[e].add_batch(xg)
+                    gq, i = slot[f"e{e}.down"]
+                    gq.add_batch(i, xd, None)
+        for sh in shares:
+            sh.finalize()
+        for gq in insts:
+            gq.H
+        e_[1].record()
+        e_[2].record()
+        for gq in insts:
+            gq.fasterquant(blocksize=128, percdamp=0.01, groupsize=128, backend="hip")
+            gq.free()
+        e_[3].record()
+        return e_, flops
+    return step, (f"qwen3-moe-style block, 128 experts (768x2048 gate/up, 2048x768 down), top-8 "
+                  f"Zipf(1.1) routing of 262144 tokens (per-expert tokens {stats['min_tokens']}.."
+                  f"{stats['max_tokens']}), GPTQ W4 sym g128, 64 linears per launch")
+
+
 def run_other(args, dev):
-    make = {"cfg1": workload_cfg1, "cfg3": workload_cfg3, "cfg5": workload_cfg5}[args.workload]
+    make = {"cfg1": workload_cfg1, "cfg3": workload_cfg3, "cfg4": workload_cfg4,
+            "cfg5": workload_cfg5}[args.workload]
     step, desc = make(dev, args.steps, args.warmup)
     torch.cuda.synchronize()
 
