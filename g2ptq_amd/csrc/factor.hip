@@ -20,6 +20,7 @@
 #include <mutex>
 
 #include "common.hpp"
+#include "potrf.hpp"
 
 namespace g2ptq {
 namespace {
@@ -72,86 +73,14 @@ __global__ void reverse_damp_kernel(const float* __restrict__ H, int64_t C, floa
   }
 }
 
-// Cholesky + in-place inverse of the nbk×nbk (nbk <= 64) diagonal block at (k, k).
-//
-// Two wave64s per layer; rows at or past nbk are identity rows.  Lane i of
-// wave 0 holds row i of the trailing matrix A, lane i of wave 1 column i of
-// the inverse X = L⁻¹ being formed, both as a register array v rotated so
-// that entry 0 is always the current pivot column / row: before step j,
-// wave 0 has v[c] = A[i][j + c] and wave 1 v[c] = (e_i − Σ_{k<j} L[·][k]·X[k][i])[j + c].
-// Step j:
-//   wave 0: pivot d = sqrt(A[j][j]) (read from lane j), m = l_ij = A[i][j]/d
-//           (i > j); publishes column j of L below the diagonal and 1/d
-//           through LDS (double buffered by step parity);
-//   barrier;
-//   wave 1: m = X[j][i] = v[0]/d;
-//   both:   v[c] ← v[c+1] − m·L[j+1+c][j]
-// i.e. the right-looking Cholesky and the forward substitution of L·x = e_i
-// sharing the broadcast column, one per wave so each runs half the FMAs.
-// Entries that correspond to columns past the block hold finite leftovers
-// that are never read.
-//
-// The step code is a loop, not unrolled: a wave executing straight-line code
-// once per launch is bound by instruction fetch.  The 64 steps run as four
-// 16-step phases over 64, 48, 32 and 16 live entries (the rotated arrays
-// shrink by one column per step), so the compiled kernel stays a few KB.  A
-// non-positive (or NaN) pivot is recorded and the block is not stored.
-constexpr int XP = NB + 1;  // LDS row pitch of the X / load staging buffer
-
-// Wave 0's pivot step for column j: d = sqrt(v[0] of lane j), m = l_ij, and
-// column j of L below the diagonal plus 1/d published in LDS buffer j & 1.
-__device__ __forceinline__ float chol_pivot(float v0, int j, int i, float (*colL)[NB], float* rdl,
-                                            int& fail) {
-  const float djj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v0), j));
-  fail = (fail == 0 && !(djj > 0.f)) ? j + 1 : fail;  // also catches NaN
-  // 1/sqrt from the hardware reciprocal square root (about 1 ulp): the factor
-  // is held to fp32 tolerance, not to correctly rounded bits.
-  const float rd = __builtin_amdgcn_rsqf(djj);
-  const float m = (i > j) ? v0 * rd : 0.f;
-  if (i > j) colL[j & 1][i - j - 1] = m;
-  if (i == 0) rdl[j & 1] = rd;
-  return m;
-}
-
-// Steps j0 .. j0+15 over LEN live entries.  Wave 0 enters step j with its
-// multiplier m already computed and column j published; it updates v[0] (the
-// next pivot column) first and publishes column j+1 before the rest of step
-// j's updates, so the LDS write latency and the pivot chain overlap the bulk
-// FMAs.  Buffers alternate by step parity: column j+1 goes to the buffer that
-// wave 1 finished reading before the barrier of step j.
-template <int LEN>
-__device__ __forceinline__ void chol_inv_phase(float (&v)[NB], int j0, int i, int w,
-                                               float (*colL)[NB], float* rdl, float* Xs, float& m,
-                                               int& fail) {
-#pragma clang loop unroll(disable)
-  for (int jj = 0; jj < 16; ++jj) {
-    const int j = j0 + jj;
-    const int buf = j & 1;
-    __syncthreads();  // column j and 1/d_j are published
-    float mm = m;
-    if (w == 1) {
-      mm = v[0] * rdl[buf];
-      Xs[j * XP + i] = mm;
-    }
-    float cl[LEN];
-#pragma unroll
-    for (int q = 0; q < LEN / 4; ++q) {
-      const float4 u = *reinterpret_cast<const float4*>(&colL[buf][4 * q]);
-      cl[4 * q] = u.x; cl[4 * q + 1] = u.y; cl[4 * q + 2] = u.z; cl[4 * q + 3] = u.w;
-    }
-    v[0] = v[1] - mm * cl[0];
-    if (w == 0 && j + 1 < NB) m = chol_pivot(v[0], j + 1, i, colL, rdl, fail);
-#pragma unroll
-    for (int c = 1; c + 1 < LEN; ++c) v[c] = v[c + 1] - mm * cl[c];
-    v[LEN - 1] = 0.f;
-  }
-}
-
+// Cholesky + in-place inverse of the nbk×nbk (nbk <= 64) diagonal block at
+// (k, k) of each layer: load, potrf_core (potrf.hpp), store X = L⁻¹ (lower,
+// zeros above) or record the failing pivot.
 __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1))) void potrf_diag_kernel(
     float* WA, int64_t C, int64_t k, int nbk, int* st, int* info) {
   const int64_t b = blockIdx.x;
-  __shared__ __attribute__((aligned(16))) float Xs[NB * XP];
-  __shared__ __attribute__((aligned(16))) float colL[2][NB];
+  __shared__ __attribute__((aligned(16))) float Xs[POT_NB * XP];
+  __shared__ __attribute__((aligned(16))) float colL[2][POT_NB];
   __shared__ float rdl[2];
   __shared__ int fail_s;
   float* Wb = WA + b * C * C + k * C + k;
@@ -163,35 +92,21 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   // LDS so that lane i of wave 0 holds row i.
   {
     const int ci = i < nbk ? i : nbk - 1;
-    float x[NB / 2];
+    float x[POT_NB / 2];
 #pragma unroll
-    for (int h = 0; h < NB / 2; ++h) {
+    for (int h = 0; h < POT_NB / 2; ++h) {
       const int r = 2 * h + w;
       const int rr = r < nbk ? r : nbk - 1;
       x[h] = Wb[(int64_t)rr * C + ci];
     }
 #pragma unroll
-    for (int h = 0; h < NB / 2; ++h) {
+    for (int h = 0; h < POT_NB / 2; ++h) {
       const int r = 2 * h + w;
       Xs[r * XP + i] = (r < nbk && i < nbk) ? (i <= r ? x[h] : 0.f) : (r == i ? 1.f : 0.f);
     }
-    colL[w][i] = 0.f;
   }
   __syncthreads();
-  float v[NB];
-#pragma unroll
-  for (int c = 0; c < NB; ++c) v[c] = (w == 0) ? Xs[i * XP + c] : (c == i ? 1.f : 0.f);
-  __syncthreads();  // Xs is reused for X below
-  int fail = 0;
-  float m = 0.f;
-  if (w == 0) m = chol_pivot(v[0], 0, i, colL, rdl, fail);
-  chol_inv_phase<64>(v, 0, i, w, colL, rdl, Xs, m, fail);
-  chol_inv_phase<48>(v, 16, i, w, colL, rdl, Xs, m, fail);
-  chol_inv_phase<32>(v, 32, i, w, colL, rdl, Xs, m, fail);
-  chol_inv_phase<16>(v, 48, i, w, colL, rdl, Xs, m, fail);
-  if (w == 0 && i == 0) fail_s = fail;
-  __syncthreads();
-  fail = fail_s;
+  const int fail = potrf_core(Xs, colL, rdl, &fail_s);
   // Layers already done (a damp retry) run the steps on whatever the block
   // holds and store nothing: testing the flag only here lets its load overlap
   // the block loads instead of preceding them.
@@ -318,12 +233,19 @@ extern "C" int g2ptq_inv_chol_upper(void* stream, const float* H, int64_t B, int
   // panel: the trailing update beyond the next panel runs on a second stream
   // while the next panel (updated first, on the caller's stream) is factored,
   // so the latency-bound panel chain overlaps the bandwidth/MFMA-bound SYRK.
+  // The first diagonal block of a panel is factored by potrf_diag_kernel; every
+  // later one by the panel-remainder update that produces it (its top-left
+  // workgroup factors the block in LDS right after computing it).
   auto factor_panel = [&](int64_t k, int64_t kb) -> int {
+    bool fused = false;
     for (int64_t j = k; j < k + kb; j += NB) {
       const int nbk = (int)std::min<int64_t>(NB, k + kb - j);
-      hipLaunchKernelGGL(potrf_diag_kernel, dim3((unsigned)B), dim3(128), 0, s, WA, C, j, nbk,
-                         st, info);
-      G2PTQ_LAUNCHED();
+      if (!fused) {
+        hipLaunchKernelGGL(potrf_diag_kernel, dim3((unsigned)B), dim3(128), 0, s, WA, C, j, nbk,
+                           st, info);
+        G2PTQ_LAUNCHED();
+      }
+      fused = false;
       const int64_t rest = C - j - nbk;
       if (rest <= 0) break;
       GemmF32 t;  // panel ← panel · inv(L_jj)ᵀ
@@ -342,7 +264,10 @@ extern "C" int g2ptq_inv_chol_upper(void* stream, const float* H, int64_t B, int
       y.C = WA + (j + nbk) * C + (j + nbk); y.ldc = C; y.sC = CC;
       y.D = WA + (j + nbk) * C + (j + nbk); y.ldd = C; y.sD = CC;
       y.alpha = -1.f; y.beta = 1.f; y.uplo = 1; y.skip = st;
+      y.pot_nb = (int)std::min<int64_t>(NB, pw); y.pot_k = j + nbk;
+      y.pot_st = st; y.pot_info = info;
       G2PTQ_TRY(gemm_f32(s, y));
+      fused = true;
     }
     return G2PTQ_OK;
   };
