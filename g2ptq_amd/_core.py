@@ -222,19 +222,37 @@ def param_tables(quantizers, BR, groupsize, static_groups, device):
 
 
 def mse_config(quantizer):
-    if getattr(quantizer, "hclip", False):
-        raise NotImplementedError("hclip (Hessian-diagonal clip search) is not implemented")
     if getattr(quantizer, "mse", False):
         return int(quantizer.grid), float(quantizer.norm), float(quantizer.maxshrink)
     return 0, 2.4, 0.5
 
 
+def hclip_rows(quantizers, H_diag, groupsize, static_groups, rows, C, dev):
+    """The (blocks, C) Hessian diagonal the dynamic-group clip searches of the
+    compensation loop weight their error with (gptq_utils.py:194-205 passes
+    ``H_diag[:, i:i+g]`` to ``find_params``), or None when they use none."""
+    q0 = quantizers[0]
+    if groupsize == -1 or static_groups or not getattr(q0, "hclip", False):
+        return None
+    if H_diag is None:
+        raise AttributeError("WeightQuantizer with hclip=True needs H_diag "
+                             "('NoneType' object has no attribute 'shape')")
+    nb = H_diag.shape[0]
+    if H_diag.dim() != 2 or H_diag.shape[1] != C or nb == 0 or rows % nb != 0:
+        raise RuntimeError(f"H_diag of shape {tuple(H_diag.shape)} does not split {rows} rows "
+                           f"of {C} columns")
+    if not getattr(q0, "mse", False):
+        return None  # only the clip search reads it
+    return H_diag.to(device=dev, dtype=torch.float32).contiguous()
+
+
 def compensate(variant, W, U, quantizers, blocksize, groupsize, static_groups, qparam_perm,
-               flags, P=None, Z=None, GH=None):
+               flags, P=None, Z=None, GH=None, H_diag=None):
     """Native lazy-batch loop (``_run_compensation``); returns (Q, W_int, Scale).
 
     W (B, R, C) is updated in place with every block tail, like the reference.
-    Dynamic group quantizers receive their fitted parameters.
+    Dynamic group quantizers receive their fitted parameters.  ``H_diag``
+    (blocks, C) weights their clip search when the quantizers use ``hclip``.
     """
     B, R, C = W.shape
     dev = W.device
@@ -248,6 +266,7 @@ def compensate(variant, W, U, quantizers, blocksize, groupsize, static_groups, q
     if groupsize != -1 and static_groups and qparam_perm is not None:
         colgroup = (qparam_perm.to(dev).long() // groupsize).to(torch.int32).contiguous()
     grid, norm, shrink = mse_config(quantizers[0])
+    hd = hclip_rows(quantizers, H_diag, groupsize, static_groups, B * R, C, dev)
     Q = torch.empty_like(W)
     W_int = torch.empty_like(W)
     Scale = torch.empty_like(W)
@@ -256,7 +275,8 @@ def compensate(variant, W, U, quantizers, blocksize, groupsize, static_groups, q
     bits = quantizers[0].bits
     _lib.call("g2ptq_compensate", stream(), variant, B, R, C, blocksize, _lib.ptr(W), _lib.ptr(U),
               _lib.ptr(P), _lib.ptr(Z), _lib.ptr(GH), bits, int(quantizers[0].sym), groupsize,
-              int(bool(static_groups)), grid, norm, shrink, _lib.ptr(colgroup), _lib.ptr(stab),
+              int(bool(static_groups)), grid, norm, shrink, _lib.ptr(hd),
+              hd.shape[0] if hd is not None else 0, _lib.ptr(colgroup), _lib.ptr(stab),
               _lib.ptr(ztab), _lib.ptr(Q), _lib.ptr(W_int), _lib.ptr(Scale), _lib.ptr(flags),
               _lib.ptr(ws), ws.numel())
     if dynamic:
@@ -271,15 +291,25 @@ def compensate(variant, W, U, quantizers, blocksize, groupsize, static_groups, q
     return Q, W_int, Scale
 
 
-def fit_static_params(quantizers, W_flat, groupsize, static_groups, flags):
+def fit_static_params(quantizers, W_flat, groupsize, static_groups, flags, H_diag=None):
     """gptq_utils.py:259-270: fit group params on the unpermuted weights."""
     if groupsize == -1 or static_groups:
         for i, q in enumerate(quantizers):
             if not q.ready():
                 if groupsize == -1:
-                    q.find_params(W_flat, _flags=flags)
+                    q.find_params(W_flat, H_diag, _flags=flags)
                 else:
-                    q.find_params(W_flat[:, i * groupsize:(i + 1) * groupsize], _flags=flags)
+                    sl = slice(i * groupsize, (i + 1) * groupsize)
+                    q.find_params(W_flat[:, sl], None if H_diag is None else H_diag[:, sl],
+                                  _flags=flags)
+
+
+def hessian_diag(H, hclip):
+    """``torch.diagonal(H, dim1=-2, dim2=-1).clone()`` when hclip is on
+    (gptq_utils.py:253-257), else None."""
+    if not hclip:
+        return None
+    return torch.diagonal(H, dim1=-2, dim2=-1).clone()
 
 
 @contextlib.contextmanager

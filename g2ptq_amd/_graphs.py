@@ -18,20 +18,22 @@ def clear():
 
 
 def compensate_graph(variant, W, U, quantizers, blocksize, groupsize, static_groups, qparam_perm,
-                     flags, P=None, Z=None, GH=None):
+                     flags, P=None, Z=None, GH=None, H_diag=None):
     B, R, C = W.shape
     dev = W.device
     q0 = quantizers[0]
     grid, norm, shrink = _core.mse_config(q0)
+    hd = _core.hclip_rows(quantizers, H_diag, groupsize, static_groups, B * R, C, dev)
+    nhd = hd.shape[0] if hd is not None else 0
     stab, ztab, dynamic = _core.param_tables(quantizers, B * R, groupsize, static_groups, dev)
     colgroup = None
     if groupsize != -1 and static_groups and qparam_perm is not None:
         colgroup = (qparam_perm.to(dev).long() // groupsize).to(torch.int32).contiguous()
     key = (variant, tuple(W.shape), blocksize, groupsize, bool(static_groups), colgroup is not None,
-           q0.bits, bool(q0.sym), grid, norm, shrink, P is not None, Z is not None,
+           q0.bits, bool(q0.sym), grid, norm, shrink, nhd, P is not None, Z is not None,
            dev.index if dev.index is not None else torch.cuda.current_device())
     live = {"W": W, "U": U, "P": P, "Z": Z, "GH": GH, "stab": stab, "ztab": ztab,
-            "colgroup": colgroup, "flags": flags}
+            "colgroup": colgroup, "flags": flags, "hd": hd}
     state = _CACHE.get(key)
     if state is None:
         static = {k: (v.clone() if v is not None else None) for k, v in live.items()}
@@ -46,7 +48,8 @@ def compensate_graph(variant, W, U, quantizers, blocksize, groupsize, static_gro
                       _lib.ptr(static["W"]), _lib.ptr(static["U"]), _lib.ptr(static["P"]),
                       _lib.ptr(static["Z"]), _lib.ptr(static["GH"]), q0.bits, int(q0.sym),
                       groupsize, int(bool(static_groups)), grid, norm, shrink,
-                      _lib.ptr(static["colgroup"]), _lib.ptr(static["stab"]),
+                      _lib.ptr(static["hd"]), nhd, _lib.ptr(static["colgroup"]),
+                      _lib.ptr(static["stab"]),
                       _lib.ptr(static["ztab"]), _lib.ptr(static["Q"]), _lib.ptr(static["W_int"]),
                       _lib.ptr(static["Scale"]), _lib.ptr(static["flags"]),
                       _lib.ptr(static["ws"]), static["ws"].numel())

@@ -26,7 +26,8 @@ _szp = ctypes.POINTER(ctypes.c_size_t)
 SIGNATURES = {
     "g2ptq_abi_version": [],
     "g2ptq_find_params": [_p, _p, _i64, _i64, _i64, _i32, _i32, _p, _p, _i64, _p],
-    "g2ptq_find_params_mse": [_p, _p, _i64, _i64, _i64, _i32, _i32, _f32, _i32, _f32, _p, _p, _i64, _p],
+    "g2ptq_find_params_mse": [_p, _p, _i64, _i64, _i64, _i32, _i32, _f32, _i32, _f32, _p, _i64,
+                              _i64, _i64, _p, _p, _i64, _p],
     "g2ptq_fake_quantize": [_p, _p, _i64, _i64, _i64, _i64, _p, _p, _i64, _i32, _p, _i64, _p, _i64, _p],
     "g2ptq_hessian_workspace": [_i64, _i64, _i32, _i64, _szp],
     "g2ptq_hessian_update": [_p, _p, _i64, _i64, _i64, _f32, _f32, _p, _i64, _p, _sz],
@@ -50,7 +51,7 @@ SIGNATURES = {
     "g2ptq_block_sweep": [_p, _i32, _i64, _i64, _i64, _i32, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p],
     "g2ptq_compensate_workspace": [_i32, _i64, _i64, _i64, _i64, _szp],
     "g2ptq_compensate": [_p, _i32, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _i32, _i32, _i64, _i32,
-                         _i32, _f32, _f32, _p, _p, _p, _p, _p, _p, _p, _p, _sz],
+                         _i32, _f32, _f32, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _sz],
     "g2ptq_gptaq_p": [_p, _p, _p, _i64, _i64, _f32, _p, _p, _sz],
     "g2ptq_trust_region": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _f32, _i32, _p, _p, _p, _p, _sz],
     "g2ptq_trust_region_workspace": [_i64, _i64, _i64, _szp],

@@ -134,9 +134,10 @@ extern "C" int g2ptq_compensate(void* stream, int variant, int64_t B, int64_t R,
                                 int64_t bs, float* W, const float* U, const float* P,
                                 const float* Z, float* GH, int bits, int sym, int64_t groupsize,
                                 int static_groups, int mse_grid, float mse_norm,
-                                float mse_maxshrink, const int* colgroup, float* scale_tab,
-                                float* zero_tab, float* Q, float* Wint, float* Scale, int* flags,
-                                void* ws, size_t ws_bytes) {
+                                float mse_maxshrink, const float* hdiag, int64_t hblocks,
+                                const int* colgroup,
+                                float* scale_tab, float* zero_tab, float* Q, float* Wint,
+                                float* Scale, int* flags, void* ws, size_t ws_bytes) {
   G2PTQ_CHECK(W && U && scale_tab && zero_tab && Q, "compensate: null pointer");
   G2PTQ_CHECK(bits >= 2 && bits <= 16, "compensate: bits=%d unsupported", bits);
   G2PTQ_CHECK(bs >= 1 && bs <= kMaxBlock, "compensate: blocksize %lld not in [1, %d]",
@@ -198,10 +199,13 @@ extern "C" int g2ptq_compensate(void* stream, int variant, int64_t B, int64_t R,
         for (int64_t gs = (i1 + groupsize - 1) / groupsize * groupsize; gs < i2; gs += groupsize) {
           const int64_t gi = gs / groupsize;
           const int64_t width = std::min(groupsize, C - gs);
-          if (mse_grid > 0)
+          if (mse_grid > 0) {
+            HDiag hd;  // H_diag[:, gs:gs + width] (hblocks × C)
+            if (hdiag) { hd.h = hdiag + gs; hd.ld = C; hd.nblocks = hblocks; }
             G2PTQ_TRY(launch_find_params_mse(s, W + gs, B * R, width, C, maxq, sym, mse_norm,
-                                             mse_grid, mse_maxshrink, scale_tab + gi * B * R,
+                                             mse_grid, mse_maxshrink, hd, scale_tab + gi * B * R,
                                              zero_tab + gi * B * R, 1, flags));
+          }
           else
             G2PTQ_TRY(launch_find_params(s, W + gs, B * R, width, C, maxq, sym,
                                          scale_tab + gi * B * R, zero_tab + gi * B * R, 1, flags));

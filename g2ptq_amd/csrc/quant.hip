@@ -98,18 +98,47 @@ __global__ __launch_bounds__(256) void find_params_kernel(const float* __restric
 // ---------------------------------------------------------------------------
 // MSE clip search (quant_utils.py:406-425): one wave per row.  Candidate
 // (i, j) shrinks xmin by (1 - i/grid) and xmax by (1 - j/grid); the error is
-// sum(|fq - x|^norm); a candidate replaces the incumbent only when strictly
-// better, scanning i-major exactly like the reference loop.
+// sum(|fq - x|^norm), or with Hessian-diagonal weights sum((fq - x)^2 * h)
+// (_quant_err, :84-105); a candidate replaces the incumbent only when
+// strictly better, scanning i-major exactly like the reference loop.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(64) void find_params_mse_kernel(const float* __restrict__ x,
                                                              int64_t rows, int64_t cols,
                                                              int64_t ldx, int maxq, int sym,
                                                              float norm, int grid, int steps,
-                                                             float* scale, float* zero,
+                                                             HDiag hd, float* scale, float* zero,
                                                              int64_t ldp, int* flags) {
   const int64_t row = blockIdx.x;
   const int lane = threadIdx.x;
   const float* xr = x + row * ldx;
+  // The weights are dropped (plain |err|^norm search) when every entry of the
+  // given H_diag is equal (quant_utils.py:393-397: min == max, which a NaN
+  // never satisfies).  Every wave checks the whole H_diag (nblocks·gpr·cols
+  // values, L2-resident) against the search's steps² passes over its row.
+  const float* hr = nullptr;
+  if (hd.h) {
+    const int64_t hc = hd.gpr * cols;
+    float hmn = INFINITY, hmx = -INFINITY;
+    int hnan = 0;
+    for (int64_t b = 0; b < hd.nblocks; ++b)
+      for (int64_t c = lane; c < hc; c += 64) {
+        const float v = hd.h[b * hd.ld + c];
+        hnan |= (v != v);
+        hmn = fminf(hmn, v);
+        hmx = fmaxf(hmx, v);
+      }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      hmn = fminf(hmn, __shfl_xor(hmn, o));
+      hmx = fmaxf(hmx, __shfl_xor(hmx, o));
+      hnan |= __shfl_xor(hnan, o);
+    }
+    if (hnan || hmn != hmx) {
+      const int64_t orow = row / hd.gpr, k = row - orow * hd.gpr;
+      const int64_t share = rows / hd.gpr / hd.nblocks;  // original rows per block
+      hr = hd.h + (orow / share) * hd.ld + k * cols;
+    }
+  }
   float mn = INFINITY, mx = -INFINITY;
   int nan = 0;
   for (int64_t c = lane; c < cols; c += 64) {
@@ -152,7 +181,8 @@ __global__ __launch_bounds__(64) void find_params_mse_kernel(const float* __rest
         const float v = xr[c];
         const float q = clamp_nan(__fadd_rn(rintf(__fdiv_rn(v, s1)), z1), minq, fmaxq);
         const float fq = __fmul_rn(s1, __fsub_rn(q, z1));
-        err += powf(fabsf(__fsub_rn(fq, v)), norm);
+        const float d = __fsub_rn(fq, v);
+        err += hr ? __fmul_rn(__fmul_rn(d, d), hr[c]) : powf(fabsf(d), norm);
       }
 #pragma unroll
       for (int o = 32; o > 0; o >>= 1) err += __shfl_xor(err, o);
@@ -795,15 +825,23 @@ int launch_find_params(hipStream_t stream, const float* x, int64_t rows, int64_t
 
 int launch_find_params_mse(hipStream_t stream, const float* x, int64_t rows, int64_t cols,
                            int64_t ldx, int maxq, int sym, float norm, int grid, float maxshrink,
-                           float* scale, float* zero, int64_t ldp, int* flags) {
+                           const HDiag& hd, float* scale, float* zero, int64_t ldp, int* flags) {
   G2PTQ_CHECK(grid > 0, "find_params_mse: grid must be positive");
   if (rows <= 0) return G2PTQ_OK;
   G2PTQ_CHECK(cols > 0, "find_params_mse: empty group");
   G2PTQ_CHECK(rows < (1ll << 31), "find_params_mse: too many rows");
+  if (hd.h) {
+    G2PTQ_CHECK(hd.nblocks >= 1 && hd.gpr >= 1 && hd.ld >= hd.gpr * cols,
+                "find_params_mse: bad H_diag layout (%lld blocks, %lld groups per row, ld %lld)",
+                (long long)hd.nblocks, (long long)hd.gpr, (long long)hd.ld);
+    G2PTQ_CHECK(rows % hd.gpr == 0 && (rows / hd.gpr) % hd.nblocks == 0,
+                "find_params_mse: %lld rows do not split into %lld H_diag blocks",
+                (long long)(rows / hd.gpr), (long long)hd.nblocks);
+  }
   // int(self.maxshrink * self.grid) with Python's float product.
   const int steps = (int)((double)maxshrink * (double)grid);
   hipLaunchKernelGGL(find_params_mse_kernel, dim3((unsigned)rows), dim3(64), 0, stream, x, rows,
-                     cols, ldx, maxq, sym, norm, grid, steps, scale, zero, ldp, flags);
+                     cols, ldx, maxq, sym, norm, grid, steps, hd, scale, zero, ldp, flags);
   G2PTQ_LAUNCHED();
   return G2PTQ_OK;
 }
@@ -824,13 +862,16 @@ extern "C" int g2ptq_find_params(void* stream, const float* x, int64_t rows, int
 
 extern "C" int g2ptq_find_params_mse(void* stream, const float* x, int64_t rows, int64_t cols,
                                      int64_t ldx, int bits, int sym, float norm, int grid,
-                                     float maxshrink, float* scale, float* zero, int64_t ldp,
-                                     int* flags) {
+                                     float maxshrink, const float* hdiag, int64_t ldh,
+                                     int64_t hblocks, int64_t groups_per_row, float* scale,
+                                     float* zero, int64_t ldp, int* flags) {
   G2PTQ_CHECK(bits >= 2 && bits <= 16, "find_params_mse: bits=%d unsupported", bits);
   G2PTQ_CHECK(x && scale && zero, "find_params_mse: null pointer");
   const int maxq = (1 << (bits - 1)) - 1;
+  HDiag hd;
+  hd.h = hdiag; hd.ld = ldh; hd.nblocks = hblocks; hd.gpr = groups_per_row;
   return launch_find_params_mse(as_stream(stream), x, rows, cols, ldx, maxq, sym, norm, grid,
-                                maxshrink, scale, zero, ldp, flags);
+                                maxshrink, hd, scale, zero, ldp, flags);
 }
 
 extern "C" int g2ptq_fake_quantize(void* stream, const float* x, int64_t rows, int64_t cols,

@@ -36,8 +36,21 @@ int launch_sweep(hipStream_t stream, int variant, const SweepArgs& a, int64_t B)
 int launch_find_params(hipStream_t stream, const float* x, int64_t rows, int64_t cols,
                        int64_t ldx, int maxq, int sym, float* scale, float* zero, int64_t ldp,
                        int* flags);
+// Hessian-diagonal weights of the clip search (WeightQuantizer with hclip,
+// utils/quant_utils.py:393-397 and _quant_err :84-105): the searched rows
+// split into `nblocks` equal consecutive shares, share b weighted by row b of
+// h (nblocks × gpr·cols, pitch ld).  With gpr > 1 each original row was
+// split into gpr column groups of `cols` (weight_groupsize > 0): searched row
+// r is group r % gpr of original row r / gpr.  h == nullptr: no weights.
+struct HDiag {
+  const float* h = nullptr;
+  int64_t ld = 0;
+  int64_t nblocks = 0;
+  int64_t gpr = 1;
+};
+
 int launch_find_params_mse(hipStream_t stream, const float* x, int64_t rows, int64_t cols,
                            int64_t ldx, int maxq, int sym, float norm, int grid, float maxshrink,
-                           float* scale, float* zero, int64_t ldp, int* flags);
+                           const HDiag& hd, float* scale, float* zero, int64_t ldp, int* flags);
 
 }  // namespace g2ptq

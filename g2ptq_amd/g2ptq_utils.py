@@ -165,11 +165,10 @@ class G2PTQ:
                           qparam_perm, backend, graph, H_diag=None):
         """g2ptq_utils.py:252-347 (GHinv receives the block-tail updates in place)."""
         _core.check_backend(backend)
-        if H_diag is not None:
-            raise NotImplementedError("hclip (H_diag) is not implemented by the HIP path")
         flags = torch.zeros(1, dtype=torch.int32, device=W.device)
         out = _compensate(_lib.VARIANT_G2PTQ, self.quantizer, W, Hinv, blocksize, groupsize,
-                          static_groups, qparam_perm, flags, graph, Z=Z.contiguous(), GH=GHinv)
+                          static_groups, qparam_perm, flags, graph, Z=Z.contiguous(), GH=GHinv,
+                          H_diag=H_diag)
         self._last_flags = flags
         return out
 
@@ -178,8 +177,6 @@ class G2PTQ:
                     export_compressed_tensors=False, backend="hip", graph=False):
         """g2ptq_utils.py:349-519."""
         _core.check_backend(backend)
-        if self.quantizer[0].hclip:
-            raise NotImplementedError("hclip (Hessian-diagonal clip search) is not implemented")
         W = _core.stack_weights_f32(self.layers)
         B, R, C = W.shape
         G = self.num_groups
@@ -191,7 +188,9 @@ class G2PTQ:
         gradient_step = bool(enable_gradient_update and alpha > 0)
         with self._maybe_onload_hessian_grad():
             H_sub = self.H.view(B * G, C, C)
-            _core.fit_static_params(self.quantizer, W_flat, groupsize, static_groups, flags)
+            H_diag = _core.hessian_diag(H_sub, self.quantizer[0].hclip)
+            _core.fit_static_params(self.quantizer, W_flat, groupsize, static_groups, flags,
+                                    H_diag)
             _core.prepare_hessian(H_sub, W_sub, Grad=grads)
             Q_sub = None
             if gradient_step:
@@ -206,6 +205,8 @@ class G2PTQ:
                 W_sub = _core.permute_cols(W_sub, perm)
                 H_sub.copy_(_core.permute_sym(H_sub, perm))
                 grads = _core.permute_cols(grads, perm)
+                if H_diag is not None:
+                    H_diag = _core.permute_cols(H_diag, perm)
             Hinv = self._factor(H_sub, percdamp, bool(actorder))
             if Q_sub is not None and actorder:
                 Q_sub = _core.permute_cols(Q_sub, perm)
@@ -221,14 +222,14 @@ class G2PTQ:
             Q, W_int, Scale = _compensate(_lib.VARIANT_G2PTQ, self.quantizer, W_sub, Hinv,
                                           blocksize, groupsize, static_groups,
                                           perm if static_groups and actorder else None, flags,
-                                          graph, Z=Z, GH=GH)
+                                          graph, Z=Z, GH=GH, H_diag=H_diag)
         else:
             # β = 0 ⇒ Z = GHinv = 0 and the G2PTQ sweep reduces, operation for
             # operation, to the GPTQ sweep.
             Q, W_int, Scale = _compensate(_lib.VARIANT_GPTQ, self.quantizer, W_sub, Hinv,
                                           blocksize, groupsize, static_groups,
                                           perm if static_groups and actorder else None, flags,
-                                          graph)
+                                          graph, H_diag=H_diag)
         if actorder:
             Q = _core.permute_cols(Q, invperm)
             W_int = _core.permute_cols(W_int, invperm)

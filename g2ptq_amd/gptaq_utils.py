@@ -130,11 +130,10 @@ class GPTAQ:
                           backend, graph, H_diag=None):
         """gptaq_utils.py:193-261."""
         _core.check_backend(backend)
-        if H_diag is not None:
-            raise NotImplementedError("hclip (H_diag) is not implemented by the HIP path")
         flags = torch.zeros(1, dtype=torch.int32, device=W.device)
         out = _compensate(_lib.VARIANT_GPTAQ, self.quantizer, W, Hinv, blocksize, groupsize,
-                          static_groups, qparam_perm, flags, graph, P=P.contiguous())
+                          static_groups, qparam_perm, flags, graph, P=P.contiguous(),
+                          H_diag=H_diag)
         self._last_flags = flags
         return out
 
@@ -143,8 +142,6 @@ class GPTAQ:
                     backend="hip", graph=False):
         """gptaq_utils.py:263-391."""
         _core.check_backend(backend)
-        if self.quantizer[0].hclip:
-            raise NotImplementedError("hclip (Hessian-diagonal clip search) is not implemented")
         W = _core.stack_weights_f32(self.layers)
         B, R, C = W.shape
         W_flat = W.view(B * R, C)
@@ -152,7 +149,9 @@ class GPTAQ:
         with self._maybe_onload_hessian():
             H = self.H
             self.H = None
-            _core.fit_static_params(self.quantizer, W_flat, groupsize, static_groups, flags)
+            H_diag = _core.hessian_diag(H, self.quantizer[0].hclip)
+            _core.fit_static_params(self.quantizer, W_flat, groupsize, static_groups, flags,
+                                    H_diag)
             _core.prepare_hessian(H, W, Dx=self.dXXT)
             perm = invperm = None
             if actorder:
@@ -160,6 +159,8 @@ class GPTAQ:
                 W = _core.permute_cols(W, perm)
                 H = _core.permute_sym(H, perm)
                 self.dXXT.copy_(_core.permute_sym(self.dXXT, perm))
+                if H_diag is not None:
+                    H_diag = _core.permute_cols(H_diag, perm)
             Hinv, _ = _core.factor(H, percdamp)
             P = torch.empty_like(Hinv)
             ws = _lib.workspace(B * C * C * 4 + 256, self.dev)
@@ -168,7 +169,7 @@ class GPTAQ:
         Q, W_int, Scale = _compensate(_lib.VARIANT_GPTAQ, self.quantizer, W, Hinv, blocksize,
                                       groupsize, static_groups,
                                       perm if static_groups and actorder else None, flags, graph,
-                                      P=P)
+                                      P=P, H_diag=H_diag)
         if actorder:
             Q = _core.permute_cols(Q, invperm)
             W_int = _core.permute_cols(W_int, invperm)

@@ -87,8 +87,6 @@ class GPTQGuided(GPTQ):
                     graph=False):
         """gptq_guided_utils.py:83-211."""
         _core.check_backend(backend)
-        if self.quantizer[0].hclip:
-            raise NotImplementedError("hclip (Hessian-diagonal clip search) is not implemented")
         W = _core.stack_weights_f32(self.layers)
         B, R, C = W.shape
         G = self.num_groups
@@ -99,17 +97,22 @@ class GPTQGuided(GPTQ):
             H = self.H
             self.H = None
             H_sub = H.view(B * G, C, C)
-            _core.fit_static_params(self.quantizer, W_flat, groupsize, static_groups, flags)
+            H_diag = _core.hessian_diag(H_sub, self.quantizer[0].hclip)
+            _core.fit_static_params(self.quantizer, W_flat, groupsize, static_groups, flags,
+                                    H_diag)
             _core.prepare_hessian(H_sub, W_sub)
             perm = invperm = None
             if actorder:
                 perm, invperm = _core.act_order(self.act_square, 1)
                 W_sub = _core.permute_cols(W_sub, perm)
                 H_sub = _core.permute_sym(H_sub, perm)
+                if H_diag is not None:
+                    H_diag = _core.permute_cols(H_diag, perm)
             Hinv, _ = _core.factor(H_sub, percdamp)
         Q, W_int, Scale = _compensate(_lib.VARIANT_GPTQ, self.quantizer, W_sub, Hinv, blocksize,
                                       groupsize, static_groups,
-                                      perm if static_groups and actorder else None, flags, graph)
+                                      perm if static_groups and actorder else None, flags, graph,
+                                      H_diag=H_diag)
         if actorder:
             Q = _core.permute_cols(Q, invperm)
             W_int = _core.permute_cols(W_int, invperm)

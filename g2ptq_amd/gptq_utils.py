@@ -118,11 +118,9 @@ class GPTQ:
         ``graph=True`` replays the loop from a HIP graph captured per shape.
         """
         _core.check_backend(backend)
-        if H_diag is not None:
-            raise NotImplementedError("hclip (H_diag) is not implemented by the HIP path")
         flags = torch.zeros(1, dtype=torch.int32, device=W.device)
         out = _compensate(_lib.VARIANT_GPTQ, self.quantizer, W, Hinv, blocksize, groupsize,
-                          static_groups, qparam_perm, flags, graph)
+                          static_groups, qparam_perm, flags, graph, H_diag=H_diag)
         self._last_flags = flags  # device-side failure flags, read by the caller's sync
         return out
 
@@ -134,24 +132,27 @@ class GPTQ:
         W = _core.stack_weights_f32(self.layers)
         B, R, C = W.shape
         W_flat = W.view(B * R, C)
-        if self.quantizer[0].hclip:
-            raise NotImplementedError("hclip (Hessian-diagonal clip search) is not implemented")
         flags = torch.zeros(1, dtype=torch.int32, device=self.dev)
         with self._maybe_onload_hessian():
             H = self.H
             self.H = None
-            _core.fit_static_params(self.quantizer, W_flat, groupsize, static_groups, flags)
+            H_diag = _core.hessian_diag(H, self.quantizer[0].hclip)
+            _core.fit_static_params(self.quantizer, W_flat, groupsize, static_groups, flags,
+                                    H_diag)
             _core.prepare_hessian(H, W)
             perm = invperm = None
             if actorder:
                 perm, invperm = _core.act_order(H, 0)
                 W = _core.permute_cols(W, perm)
                 H = _core.permute_sym(H, perm)
+                if H_diag is not None:
+                    H_diag = _core.permute_cols(H_diag, perm)
             Hinv, _ = _core.factor(H, percdamp, getattr(self, "_shared_factor", None),
                                    key=bool(actorder))
         Q, W_int, Scale = _compensate(_lib.VARIANT_GPTQ, self.quantizer, W, Hinv, blocksize,
                                       groupsize, static_groups,
-                                      perm if static_groups and actorder else None, flags, graph)
+                                      perm if static_groups and actorder else None, flags, graph,
+                                      H_diag=H_diag)
         if actorder:
             Q = _core.permute_cols(Q, invperm)
             W_int = _core.permute_cols(W_int, invperm)
@@ -171,10 +172,10 @@ class GPTQ:
 
 
 def _compensate(variant, quantizers, W, U, blocksize, groupsize, static_groups, qparam_perm,
-                flags, graph, P=None, Z=None, GH=None):
+                flags, graph, P=None, Z=None, GH=None, H_diag=None):
     if not graph:
         return _core.compensate(variant, W, U, quantizers, blocksize, groupsize, static_groups,
-                                qparam_perm, flags, P=P, Z=Z, GH=GH)
+                                qparam_perm, flags, P=P, Z=Z, GH=GH, H_diag=H_diag)
     from ._graphs import compensate_graph
     return compensate_graph(variant, W, U, quantizers, blocksize, groupsize, static_groups,
-                            qparam_perm, flags, P=P, Z=Z, GH=GH)
+                            qparam_perm, flags, P=P, Z=Z, GH=GH, H_diag=H_diag)

@@ -123,28 +123,32 @@ class WeightQuantizer(torch.nn.Module):
     def find_params(self, x, H_diag=None, _flags=None) -> None:
         """utils/quant_utils.py:377-433 on the GPU.
 
+        ``H_diag`` (needed when ``hclip`` is set) weights the MSE clip search's
+        error by the Hessian diagonal: its rows apply to equal consecutive
+        shares of the rows of ``x`` (one per layer or saliency group).
         ``_flags`` (int32 device tensor) collects the scale>0 check without a
         host sync; without it the check runs synchronously and raises like the
         reference's device assert would.
         """
         if self.bits == 16:
             return
-        if self.hclip:
-            raise NotImplementedError("hclip (Hessian-diagonal clip search) is not implemented "
-                                      "by the HIP quantizer")
         _require_cuda(x)
         init_shape = x.shape
+        gpr = 1  # column groups per row of x
         if self.weight_groupsize > 0:
             rows, columns = init_shape
             g = self.weight_groupsize
-            xg = x.reshape(rows * (columns // g), g)
-            out_shape = (rows, columns // g)
+            gpr = columns // g
+            xg = x.reshape(rows * gpr, g)
+            out_shape = (rows, gpr)
         elif self.perchannel:
             xg = x.flatten(1)
             out_shape = (xg.shape[0], 1)
         else:
             xg = x.reshape(1, -1)
             out_shape = (1, 1)
+        hd = self._hdiag(H_diag, xg.shape[0] // gpr, gpr * xg.shape[1], x.device) \
+            if self.hclip else None
         xg = xg.float()
         if xg.stride(-1) != 1:
             xg = xg.contiguous()
@@ -154,9 +158,14 @@ class WeightQuantizer(torch.nn.Module):
         flags = _flags if _flags is not None else torch.zeros(1, dtype=torch.int32, device=x.device)
         stream = _lib.stream_ptr(x.device)
         if self.mse:
+            nb = hd.shape[0] if hd is not None else 0
+            if hd is not None and (rows // gpr) % nb != 0:
+                raise RuntimeError(f"shape '[{nb}, -1, {gpr}, {cols}]' is invalid for input of "
+                                   f"size {rows * cols}")
             _lib.call("g2ptq_find_params_mse", stream, _lib.ptr(xg), rows, cols, xg.stride(0),
                       self.bits, int(self.sym), float(self.norm), int(self.grid),
-                      float(self.maxshrink), _lib.ptr(scale), _lib.ptr(zero), 1, _lib.ptr(flags))
+                      float(self.maxshrink), _lib.ptr(hd), gpr * cols, nb, gpr,
+                      _lib.ptr(scale), _lib.ptr(zero), 1, _lib.ptr(flags))
         else:
             _lib.call("g2ptq_find_params", stream, _lib.ptr(xg), rows, cols, xg.stride(0),
                       self.bits, int(self.sym), _lib.ptr(scale), _lib.ptr(zero), 1, _lib.ptr(flags))
@@ -165,6 +174,22 @@ class WeightQuantizer(torch.nn.Module):
         if _flags is None:
             check_flags(flags)
         self._ready = True
+
+    @staticmethod
+    def _hdiag(H_diag, row_groups, columns, device):
+        """utils/quant_utils.py:393-397: ``H_diag`` as (blocks, columns) fp32 on the
+        device, the rows of the search splitting into ``blocks`` equal shares.
+        Whether the weights apply (not every entry equal) is decided by the
+        kernel, without a host sync."""
+        if H_diag is None:
+            # the reference reshapes H_diag unconditionally when hclip is set
+            raise AttributeError("WeightQuantizer with hclip=True needs H_diag "
+                                 "('NoneType' object has no attribute 'shape')")
+        nb = H_diag.shape[0]
+        if nb == 0 or H_diag.numel() != nb * columns:
+            raise RuntimeError(f"shape '[{nb}, {columns}]' is invalid for input of size "
+                               f"{H_diag.numel()}")
+        return H_diag.to(device=device, dtype=torch.float32).reshape(nb, columns).contiguous()
 
     def fake_quantize(self, x):
         """utils/quant_utils.py:435-459: returns ``(dequantized, codes, scale)``."""

@@ -60,10 +60,18 @@ int g2ptq_find_params(void* stream, const float* x, int64_t rows, int64_t cols, 
 
 /* MSE clip search of WeightQuantizer.find_params with mse=True
  * (utils/quant_utils.py:406-425): grid × maxshrink² candidate ranges per row,
- * error sum(|fq − x|^norm), first strict improvement wins. */
+ * error sum(|fq − x|^norm), first strict improvement wins.
+ * hclip (quant_utils.py:393-397, _quant_err :84-105): hdiag (nullable) is the
+ * H_diag the reference reshapes to (hblocks, groups_per_row, cols), pitch ldh:
+ * the rows split into hblocks equal consecutive shares, share b's error being
+ * sum((fq − x)² · hdiag[b, k·cols + c]) for column group k = r % groups_per_row
+ * (groups_per_row > 1 when weight_groupsize split each original row).  When
+ * every hdiag entry is equal the plain search runs, as in the reference. */
 int g2ptq_find_params_mse(void* stream, const float* x, int64_t rows, int64_t cols, int64_t ldx,
                           int bits, int sym, float norm, int grid, float maxshrink,
-                          float* scale, float* zero, int64_t ldp, int* flags);
+                          const float* hdiag, int64_t ldh, int64_t hblocks,
+                          int64_t groups_per_row, float* scale, float* zero, int64_t ldp,
+                          int* flags);
 
 /* Round-to-nearest fake quantization with per-row, per-group parameters.
  * Replaces WeightQuantizer.fake_quantize (utils/quant_utils.py:435-459) and
@@ -207,16 +215,19 @@ int g2ptq_compensate_workspace(int variant, int64_t B, int64_t R, int64_t C, int
  *   when the loop reaches i (gptq_utils.py:194-205).  Otherwise scale_tab/zero_tab
  *   must already hold every group's params and colgroup (C ints, nullable) maps
  *   column → group (static groups with act-order: perm[c] // g).  mse_grid > 0 fits
- *   dynamic groups with the MSE clip search (g2ptq_find_params_mse semantics).
+ *   dynamic groups with the MSE clip search (g2ptq_find_params_mse semantics);
+ *   hdiag (hblocks × C, nullable) are its hclip weights, the diagonal of the
+ *   undamped Hessians in the loop's column order (gptq_utils.py:253-257,
+ *   314-315); the B·R rows split into hblocks equal shares (one per layer).
  *   scale_tab/zero_tab: ngroups × (B·R) fp32, group-major (row b·R + r of group g
  *   at g·B·R + b·R + r), ngroups = 1 if g == -1 else ceil(C / g).
  *   Q, Wint, Scale: (B,R,C) outputs (Wint and Scale nullable). */
 int g2ptq_compensate(void* stream, int variant, int64_t B, int64_t R, int64_t C,
                      int64_t blocksize, float* W, const float* U, const float* P, const float* Z,
                      float* GH, int bits, int sym, int64_t groupsize, int static_groups,
-                     int mse_grid, float mse_norm, float mse_maxshrink, const int* colgroup,
-                     float* scale_tab, float* zero_tab, float* Q, float* Wint, float* Scale,
-                     int* flags, void* ws, size_t ws_bytes);
+                     int mse_grid, float mse_norm, float mse_maxshrink, const float* hdiag,
+                     int64_t hblocks, const int* colgroup, float* scale_tab, float* zero_tab, float* Q,
+                     float* Wint, float* Scale, int* flags, void* ws, size_t ws_bytes);
 
 /* GPTAQ P = alpha·triu(Dx·Uᵀ, 1)·U for B layers (gptq_utils/gptaq_utils.py:349-352). */
 int g2ptq_gptaq_p(void* stream, const float* Dx, const float* U, int64_t B, int64_t C, float alpha,

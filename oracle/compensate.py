@@ -73,7 +73,8 @@ def g2ptq_block(weight, hinv, scale, zero, z, ghinv, int_weight, error, maxq):
 # Per-layer lazy-batch loops (``_run_compensation``)
 # ---------------------------------------------------------------------------
 
-def _column_quantizers(quantizers, W, i1, i2, groupsize, static_groups, qparam_perm, B, R):
+def _column_quantizers(quantizers, W, i1, i2, groupsize, static_groups, qparam_perm, B, R,
+                       H_diag=None):
     """gptq_utils/gptq_utils.py:185-205 — per-column quantizer selection."""
     if groupsize == -1:
         return [quantizers[0]] * (i2 - i1)
@@ -84,7 +85,8 @@ def _column_quantizers(quantizers, W, i1, i2, groupsize, static_groups, qparam_p
     for i in range(i1, i2):
         qz = quantizers[i // groupsize]
         if i % groupsize == 0:
-            qz.find_params(W[:, :, i:i + groupsize].reshape(B * R, -1))
+            qz.find_params(W[:, :, i:i + groupsize].reshape(B * R, -1),
+                           None if H_diag is None else H_diag[:, i:i + groupsize])
         out.append(qz)
     return out
 
@@ -100,7 +102,7 @@ def _maxq(quantizers):
 
 
 def gptq_compensation(W, Hinv, quantizers, blocksize=128, groupsize=-1, static_groups=False,
-                      qparam_perm=None):
+                      qparam_perm=None, H_diag=None):
     """gptq_utils/gptq_utils.py:165-232 (torch backend, no graph). Mutates W."""
     B, R, C = W.shape
     Q = torch.zeros_like(W)
@@ -109,7 +111,8 @@ def gptq_compensation(W, Hinv, quantizers, blocksize=128, groupsize=-1, static_g
     for i1 in range(0, C, blocksize):
         i2 = min(i1 + blocksize, C)
         W1 = W[:, :, i1:i2].clone()
-        cq = _column_quantizers(quantizers, W, i1, i2, groupsize, static_groups, qparam_perm, B, R)
+        cq = _column_quantizers(quantizers, W, i1, i2, groupsize, static_groups, qparam_perm, B, R,
+                                H_diag)
         S1, Z1 = _stack_params(cq, W1.shape)
         wt = W1.transpose(1, 2).contiguous()
         it, et = torch.empty_like(wt), torch.empty_like(wt)
@@ -124,7 +127,7 @@ def gptq_compensation(W, Hinv, quantizers, blocksize=128, groupsize=-1, static_g
 
 
 def gptaq_compensation(W, Hinv, P, quantizers, blocksize=128, groupsize=-1, static_groups=False,
-                       qparam_perm=None):
+                       qparam_perm=None, H_diag=None):
     """gptq_utils/gptaq_utils.py:193-261. Mutates W."""
     B, R, C = W.shape
     Q = torch.zeros_like(W)
@@ -133,7 +136,8 @@ def gptaq_compensation(W, Hinv, P, quantizers, blocksize=128, groupsize=-1, stat
     for i1 in range(0, C, blocksize):
         i2 = min(i1 + blocksize, C)
         W1 = W[:, :, i1:i2].clone()
-        cq = _column_quantizers(quantizers, W, i1, i2, groupsize, static_groups, qparam_perm, B, R)
+        cq = _column_quantizers(quantizers, W, i1, i2, groupsize, static_groups, qparam_perm, B, R,
+                                H_diag)
         S1, Z1 = _stack_params(cq, W1.shape)
         wt = W1.transpose(1, 2).contiguous()
         it, et = torch.empty_like(wt), torch.empty_like(wt)
@@ -151,7 +155,7 @@ def gptaq_compensation(W, Hinv, P, quantizers, blocksize=128, groupsize=-1, stat
 
 
 def g2ptq_compensation(W, Hinv, Z, GHinv, quantizers, blocksize=128, groupsize=-1,
-                       static_groups=False, qparam_perm=None):
+                       static_groups=False, qparam_perm=None, H_diag=None):
     """gptq_utils/g2ptq_utils.py:252-347 (``approx_grad_beta == 0``). Mutates W and GHinv."""
     B, R, C = W.shape
     Q = torch.zeros_like(W)
@@ -163,7 +167,8 @@ def g2ptq_compensation(W, Hinv, Z, GHinv, quantizers, blocksize=128, groupsize=-
         W1 = W[:, :, i1:i2].clone()
         Z1 = Z[:, :, i1:i2]
         GH1 = GHinv[:, :, i1:i2].clone()
-        cq = _column_quantizers(quantizers, W, i1, i2, groupsize, static_groups, qparam_perm, B, R)
+        cq = _column_quantizers(quantizers, W, i1, i2, groupsize, static_groups, qparam_perm, B, R,
+                                H_diag)
         S1, Zp1 = _stack_params(cq, W1.shape)
         wt = W1.transpose(1, 2).contiguous()
         it, et = torch.empty_like(wt), torch.empty_like(wt)

@@ -10,35 +10,44 @@ import torch
 from . import compensate, factor, quant
 
 
-def _configure(bits, sym, columns, groupsize, mse=False):
-    q = quant.WeightQuantizer().configure(bits, perchannel=True, sym=sym, mse=mse)
+def _configure(bits, sym, columns, groupsize, mse=False, hclip=False):
+    q = quant.WeightQuantizer().configure(bits, perchannel=True, sym=sym, mse=mse, hclip=hclip)
     return quant.make_group_quantizers(q, columns, groupsize)
 
 
-def _static_params(quantizers, W_flat, groupsize, static_groups):
+def _hdiag(quantizers, H):
+    """gptq_utils/gptq_utils.py:253-257: the undamped diagonal when hclip is on."""
+    return torch.diagonal(H, dim1=-2, dim2=-1).clone() if quantizers[0].hclip else None
+
+
+def _static_params(quantizers, W_flat, groupsize, static_groups, H_diag=None):
     """gptq_utils/gptq_utils.py:259-270."""
     if groupsize == -1 or static_groups:
         for i, qz in enumerate(quantizers):
             if not qz.ready():
                 if groupsize == -1:
-                    qz.find_params(W_flat)
+                    qz.find_params(W_flat, H_diag)
                 else:
-                    qz.find_params(W_flat[:, i * groupsize:(i + 1) * groupsize])
+                    sl = slice(i * groupsize, (i + 1) * groupsize)
+                    qz.find_params(W_flat[:, sl], None if H_diag is None else H_diag[:, sl])
 
 
 def gptq_fasterquant(W, H, bits, sym, blocksize=128, percdamp=0.01, groupsize=-1, actorder=False,
-                     static_groups=False, quantizers=None, mse=False):
+                     static_groups=False, quantizers=None, mse=False, hclip=False):
     """gptq_utils/gptq_utils.py:234-353 (returns instead of writing layers)."""
     W = W.clone().float()
     H = H.clone()
     B, R, C = W.shape
     if quantizers is None:
-        quantizers = _configure(bits, sym, C, groupsize, mse)
-    _static_params(quantizers, W.view(B * R, C), groupsize, static_groups)
+        quantizers = _configure(bits, sym, C, groupsize, mse, hclip)
+    H_diag = _hdiag(quantizers, H)
+    _static_params(quantizers, W.view(B * R, C), groupsize, static_groups, H_diag)
     factor.prepare_hessian(H, W)
     perm = invperm = None
     if actorder:
         perm, invperm = factor.act_order_perm(H)
+        if H_diag is not None:
+            H_diag = H_diag[:, perm].contiguous()
     Hinv = torch.empty_like(H)
     damps = []
     for b in range(B):
@@ -49,7 +58,7 @@ def gptq_fasterquant(W, H, bits, sym, blocksize=128, percdamp=0.01, groupsize=-1
         damps.append(d)
     Q, W_int, Scale = compensate.gptq_compensation(
         W, Hinv, quantizers, blocksize, groupsize, static_groups,
-        perm if static_groups and actorder else None)
+        perm if static_groups and actorder else None, H_diag)
     if actorder:
         Q, W_int, Scale = Q[:, :, invperm], W_int[:, :, invperm], Scale[:, :, invperm]
     return {"Q": Q, "W_int": W_int, "Scale": Scale, "quantizers": quantizers, "Hinv": Hinv,
@@ -57,21 +66,25 @@ def gptq_fasterquant(W, H, bits, sym, blocksize=128, percdamp=0.01, groupsize=-1
 
 
 def gptaq_fasterquant(W, H, dXXT, bits, sym, blocksize=128, percdamp=0.01, groupsize=-1,
-                      actorder=False, static_groups=False, alpha=0.25, quantizers=None):
+                      actorder=False, static_groups=False, alpha=0.25, quantizers=None,
+                      mse=False, hclip=False):
     """gptq_utils/gptaq_utils.py:263-391."""
     W = W.clone().float()
     H = H.clone()
     dXXT = dXXT.clone()
     B, R, C = W.shape
     if quantizers is None:
-        quantizers = _configure(bits, sym, C, groupsize)
-    _static_params(quantizers, W.view(B * R, C), groupsize, static_groups)
+        quantizers = _configure(bits, sym, C, groupsize, mse, hclip)
+    H_diag = _hdiag(quantizers, H)
+    _static_params(quantizers, W.view(B * R, C), groupsize, static_groups, H_diag)
     deads = factor.prepare_hessian(H, W)
     for b in range(B):
         dXXT[b, :, deads[b]] = 0
     perm = invperm = None
     if actorder:
         perm, invperm = factor.act_order_perm(H)
+        if H_diag is not None:
+            H_diag = H_diag[:, perm].contiguous()
     Hinv = torch.empty_like(H)
     for b in range(B):
         if actorder:
@@ -82,7 +95,7 @@ def gptaq_fasterquant(W, H, dXXT, bits, sym, blocksize=128, percdamp=0.01, group
     P = compensate.gptaq_P(dXXT, Hinv, alpha)
     Q, W_int, Scale = compensate.gptaq_compensation(
         W, Hinv, P, quantizers, blocksize, groupsize, static_groups,
-        perm if static_groups and actorder else None)
+        perm if static_groups and actorder else None, H_diag)
     if actorder:
         Q, W_int, Scale = Q[:, :, invperm], W_int[:, :, invperm], Scale[:, :, invperm]
     return {"Q": Q, "W_int": W_int, "Scale": Scale, "quantizers": quantizers, "Hinv": Hinv, "P": P}
@@ -108,18 +121,20 @@ def g2ptq_trust_region(gradients_sub, Hinv_init, Hinv, Q_sub, W_sub, alpha, enab
 
 def g2ptq_fasterquant(W, H, gradients, act_square, bits, sym, num_groups, blocksize=128,
                       percdamp=0.01, groupsize=-1, actorder=False, static_groups=False,
-                      enable_gradient_update=True, alpha=0.0, quantizers=None):
+                      enable_gradient_update=True, alpha=0.0, quantizers=None, mse=False,
+                      hclip=False):
     """gptq_utils/g2ptq_utils.py:349-519.  ``H`` is (B, G, C, C), mutated like the reference."""
     W = W.clone().float()
     B, R, C = W.shape
     G = num_groups
     if quantizers is None:
-        quantizers = _configure(bits, sym, C, groupsize)
+        quantizers = _configure(bits, sym, C, groupsize, mse, hclip)
     W_flat = W.view(B * R, C)
     W_sub = W.contiguous().view(B * G, R // G, C)
     grads = gradients.reshape(B * G, R // G, C).clone()
     H_sub = H.view(B * G, C, C)
-    _static_params(quantizers, W_flat, groupsize, static_groups)
+    H_diag = _hdiag(quantizers, H_sub)
+    _static_params(quantizers, W_flat, groupsize, static_groups, H_diag)
     for b in range(B * G):
         if (H_sub[b] == 0).all():
             H_sub[b] = torch.eye(C)
@@ -147,11 +162,13 @@ def g2ptq_fasterquant(W, H, gradients, act_square, bits, sym, num_groups, blocks
         Hinv[b], _, Hinv_init[b] = factor.damp_chol_inv_upper(H_sub[b], percdamp, want_inverse=True)
     if Q_sub is not None and actorder:
         Q_sub = Q_sub[:, :, perm]
+    if H_diag is not None and actorder:
+        H_diag = H_diag[:, perm].contiguous()
     beta, Z, GHinv = g2ptq_trust_region(grads, Hinv_init, Hinv, Q_sub, W_sub, alpha,
                                         enable_gradient_update and alpha > 0)
     Q, W_int, Scale = compensate.g2ptq_compensation(
         W_sub, Hinv, Z, GHinv, quantizers, blocksize, groupsize, static_groups,
-        perm if static_groups and actorder else None)
+        perm if static_groups and actorder else None, H_diag)
     if actorder:
         Q, W_int, Scale = Q[:, :, invperm], W_int[:, :, invperm], Scale[:, :, invperm]
     return {"Q": Q.view(B, R, C), "W_int": W_int.view(B, R, C), "Scale": Scale.view(B, R, C),
@@ -159,17 +176,19 @@ def g2ptq_fasterquant(W, H, gradients, act_square, bits, sym, num_groups, blocks
 
 
 def guided_fasterquant(W, H, act_square, bits, sym, num_groups, blocksize=128, percdamp=0.01,
-                       groupsize=-1, actorder=False, static_groups=False, quantizers=None):
+                       groupsize=-1, actorder=False, static_groups=False, quantizers=None,
+                       mse=False, hclip=False):
     """gptq_utils/gptq_guided_utils.py:83-211."""
     W = W.clone().float()
     B, R, C = W.shape
     G = num_groups
     if quantizers is None:
-        quantizers = _configure(bits, sym, C, groupsize)
+        quantizers = _configure(bits, sym, C, groupsize, mse, hclip)
     W_flat = W.view(B * R, C)
     W_sub = W.contiguous().view(B * G, R // G, C)
     H_sub = H.clone().view(B * G, C, C)
-    _static_params(quantizers, W_flat, groupsize, static_groups)
+    H_diag = _hdiag(quantizers, H_sub)
+    _static_params(quantizers, W_flat, groupsize, static_groups, H_diag)
     for b in range(B * G):
         if (H_sub[b] == 0).all():
             H_sub[b] = torch.eye(C)
@@ -180,6 +199,8 @@ def guided_fasterquant(W, H, act_square, bits, sym, num_groups, blocksize=128, p
     if actorder:
         perm = torch.argsort(torch.mean(act_square, dim=0), descending=True, stable=True)
         invperm = torch.argsort(perm)
+        if H_diag is not None:
+            H_diag = H_diag[:, perm].contiguous()
     Hinv = torch.empty_like(H_sub)
     for b in range(B * G):
         if actorder:
@@ -188,7 +209,7 @@ def guided_fasterquant(W, H, act_square, bits, sym, num_groups, blocksize=128, p
         Hinv[b], _ = factor.damp_chol_inv_upper(H_sub[b], percdamp)
     Q, W_int, Scale = compensate.gptq_compensation(
         W_sub, Hinv, quantizers, blocksize, groupsize, static_groups,
-        perm if static_groups and actorder else None)
+        perm if static_groups and actorder else None, H_diag)
     if actorder:
         Q, W_int, Scale = Q[:, :, invperm], W_int[:, :, invperm], Scale[:, :, invperm]
     return {"Q": Q.view(B, R, C), "W_int": W_int.view(B, R, C), "Scale": Scale.view(B, R, C),

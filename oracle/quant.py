@@ -50,20 +50,32 @@ def params_from_range(xmin, xmax, bits, sym):
     return scale, zero
 
 
-def quant_err(fq, x, norm):
-    """utils/quant_utils.py:84-97 (no Hessian diagonal)."""
-    return fq.sub_(x).abs_().pow_(norm).sum(-1)
+def quant_err(fq, x, norm, H_diag=None):
+    """utils/quant_utils.py:84-105: sum(|fq - x|^norm) over the last dim, or
+    with a Hessian diagonal (blocks, *x.shape[1:]) sum((fq - x)^2 * h), the
+    rows of ``x`` splitting into ``blocks`` consecutive equal shares."""
+    if H_diag is None:
+        return fq.sub_(x).abs_().pow_(norm).sum(-1)
+    shape = fq.shape[:-1]
+    e = fq.sub_(x).pow_(2)
+    e = e.reshape(H_diag.shape[0], -1, *H_diag.shape[1:])
+    e.mul_(H_diag.unsqueeze(1))
+    return e.sum(-1).reshape(shape)
 
 
-def find_params(x, bits, sym, mse=False, norm=2.4, grid=50, maxshrink=0.5):
+def find_params(x, bits, sym, mse=False, norm=2.4, grid=50, maxshrink=0.5, H_diag=None):
     """utils/quant_utils.py:377-433 for a per-channel quantizer.
 
-    ``x`` is (rows, cols); returns ``scale, zero`` of shape (rows, 1), exactly
-    as ``WeightQuantizer.find_params`` leaves them (zero rounded again at :428).
+    ``x`` is (rows, cols), or already the canonical (row_groups, col_groups,
+    groupsize) view; returns ``scale, zero`` of shape (rows, 1) (resp.
+    (row_groups, col_groups)), exactly as ``WeightQuantizer.find_params``
+    leaves them (zero rounded again at :428).  ``H_diag`` (hclip) is taken as
+    given: the caller reshapes it and drops it when all entries are equal
+    (:393-397).
     """
     maxq = 2 ** (bits - 1) - 1
     minq = -(maxq + 1)
-    xg = x.flatten(1).unsqueeze(1)                       # (rows, 1, cols)  :389
+    xg = x if x.dim() == 3 else x.flatten(1).unsqueeze(1)   # (rows, 1, cols)  :389
     xmin, xmax = minmax(xg)
     scale, zero = params_from_range(xmin, xmax, bits, sym)
     if mse:                                              # :406-425
@@ -79,7 +91,7 @@ def find_params(x, bits, sym, mse=False, norm=2.4, grid=50, maxshrink=0.5):
                 else:
                     q, _, _ = asym_quant(xg, scale1, zero1, maxq)
                     fq = asym_dequant(q, scale1, zero1)
-                err = quant_err(fq, xg, norm)
+                err = quant_err(fq, xg, norm, H_diag)
                 better = err < best
                 better_k = better.unsqueeze(-1)
                 scale = torch.where(better_k, scale1, scale)
@@ -109,16 +121,20 @@ class WeightQuantizer:
         return self
 
     def find_params(self, x, H_diag=None):
+        """utils/quant_utils.py:377-433 (per-channel or weight_groupsize)."""
         if self.weight_groupsize > 0:
             rows, cols = x.shape
             g = self.weight_groupsize
-            s, z = find_params(x.reshape(rows * (cols // g), g), self.bits, self.sym,
-                               self.mse, self.norm, self.grid, self.maxshrink)
-            self.scale = s.reshape(rows, cols // g)
-            self.zero = z.reshape(rows, cols // g)
+            xg = x.reshape(rows, cols // g, g)
         else:
-            self.scale, self.zero = find_params(x, self.bits, self.sym, self.mse, self.norm,
-                                                self.grid, self.maxshrink)
+            xg = x.flatten(1).unsqueeze(1)
+        if self.hclip:                                       # :393-397
+            H_diag = H_diag.reshape(H_diag.shape[0], *xg.shape[1:])
+            if (H_diag.min() == H_diag.max()).item():
+                H_diag = None
+        s, z = find_params(xg, self.bits, self.sym, self.mse, self.norm, self.grid,
+                           self.maxshrink, H_diag if self.hclip else None)
+        self.scale, self.zero = s, z
         self._ready = True
 
     def ready(self):

@@ -161,3 +161,84 @@ def test_gptq_fasterquant_matches_oracle(dev, bits, sym, groupsize, actorder):
     # most weights identical (differences cascade only after rounding ties)
     agree = (Qd == Qr).float().mean().item()
     assert agree >= 0.95, agree
+
+
+HCLIP_CASES = ("gptq_dynamic", "gptq_static_actorder", "gptaq_dynamic", "g2ptq_dynamic_actorder",
+               "guided_static")
+
+
+@pytest.mark.parametrize("case", HCLIP_CASES)
+def test_fasterquant_hclip_matches_oracle(dev, case):
+    """--w_clip --w_hclip: the clip search of every group fit (static fits on the
+    unpermuted weights, dynamic fits inside the lazy-batch loop) weights its
+    error with the undamped Hessian diagonal of the row's layer / saliency
+    group, in the loop's column order (gptq_utils.py:248-270, 314-315 and the
+    variants).  Both sides get the same Hessians; codes agree except where a
+    near-tie of the clip search or a rounding tie cascades."""
+    from g2ptq_amd import G2PTQ, GPTAQ, GPTQ, GPTQGuided, WeightQuantizer, make_group_quantizers
+    print(f"hclip flow case {case}", flush=True)
+    B, R, C, G, gs, bits = 2, 64, 128, 2, 32, 3
+    actorder = case.endswith("actorder")
+    static = "static" in case
+    g = gen(4200 + HCLIP_CASES.index(case))
+    layers = [_layer(R, C, 60 + b + 10 * HCLIP_CASES.index(case)).to(dev) for b in range(B)]
+    W0 = torch.stack([l.weight.detach().float().cpu() for l in layers])
+    sig = torch.exp(torch.randn(C, generator=g))
+
+    def gram(groups):
+        X = torch.randn(B, groups, 512, C, generator=g) * sig
+        return (2 / 512) * X.transpose(-1, -2) @ X
+
+    q = WeightQuantizer()
+    q.configure(bits, perchannel=True, sym=True, mse=True, hclip=True)
+    quantizers = make_group_quantizers(q, C, gs)
+    kw = dict(blocksize=128, percdamp=0.01, groupsize=gs, actorder=actorder,
+              static_groups=static)
+    if case.startswith("gptq"):
+        H = gram(1)[:, 0]
+        gq = GPTQ(layers)
+        gq.quantizer = quantizers
+        gq.H = H.to(dev)
+        gq.fasterquant(backend="hip", **kw)
+        ref = oflows.gptq_fasterquant(W0, H, bits, True, mse=True, hclip=True, **kw)
+    elif case.startswith("gptaq"):
+        H = gram(1)[:, 0]
+        D = torch.randn(B, C, C, generator=g) * 0.01
+        gq = GPTAQ(layers)
+        gq.quantizer = quantizers
+        gq.H = H.to(dev)
+        gq.dXXT = D.to(dev)
+        gq.fasterquant(backend="hip", **kw)
+        ref = oflows.gptaq_fasterquant(W0, H, D, bits, True, mse=True, hclip=True, **kw)
+    else:
+        H = gram(G)
+        act = torch.rand(B, C, generator=g)
+        sal = [torch.ones(1, 1, G, device=dev) for _ in range(B)]
+        if case.startswith("g2ptq"):
+            grads = torch.randn(B, R, C, generator=g) * 1e-3
+            gq = G2PTQ(layers, [[s] for s in sal], [grads[b].to(dev) for b in range(B)], G)
+            gq.quantizer = quantizers
+            gq.H = H.clone().to(dev)
+            gq.act_square = act.to(dev)
+            gq.fasterquant(backend="hip", alpha=0.0, **kw)
+            ref = oflows.g2ptq_fasterquant(W0, H.clone(), grads, act, bits, True, G, alpha=0.0,
+                                           mse=True, hclip=True, **kw)
+        else:
+            gq = GPTQGuided(layers, sal, G)
+            gq.quantizer = quantizers
+            gq.H = H.to(dev)
+            gq.act_square = act.to(dev)
+            gq.fasterquant(backend="hip", **kw)
+            ref = oflows.guided_fasterquant(W0, H, act, bits, True, G, mse=True, hclip=True, **kw)
+    torch.cuda.synchronize()
+    Qd = torch.stack([l.weight.detach().float().cpu() for l in layers])
+    Qr = ref["Q"].bfloat16().float()
+    agree = (Qd == Qr).float().mean().item()
+    assert agree >= 0.95, agree
+    s_agree = torch.stack([(a.scale.cpu() == b.scale).float().mean()
+                           for a, b in zip(quantizers, ref["quantizers"])]).mean().item()
+    assert s_agree >= 0.95, s_agree
+    Hr = H if H.dim() == 3 else H.sum(1)
+    e_hip = oflows.reconstruction_error(W0, Qd, Hr)
+    e_ref = oflows.reconstruction_error(W0, Qr, Hr)
+    assert abs(e_hip - e_ref) <= 0.005 * e_ref, (e_hip, e_ref)

@@ -158,6 +158,69 @@ def test_find_params_mse_matches_oracle(dev, bits, sym):
     assert torch.all(e1 <= e0 * (1 + 1e-5))
 
 
+@pytest.mark.parametrize("layout", ["perchannel", "grouped", "uniform", "nan"])
+def test_find_params_hclip_matches_oracle(dev, layout):
+    """hclip (quant_utils.py:393-397, _quant_err :84-105): the clip search's error
+    weighted by the Hessian diagonal of each row's block (3 blocks of 32 rows),
+    per column group with weight_groupsize; a constant H_diag falls back to the
+    plain search, a NaN entry keeps the weights (min == max fails)."""
+    from g2ptq_amd import WeightQuantizer
+    g = gen(91)
+    x = torch.randn(96, 128, generator=g) * 0.03
+    hd = torch.exp(torch.randn(3, 128, generator=g))
+    if layout == "uniform":
+        hd = torch.full((3, 128), 0.7)
+    if layout == "nan":
+        hd[1, 5] = float("nan")
+    wg = 32 if layout == "grouped" else -1
+    bits, sym = (3, False) if layout != "grouped" else (4, True)
+    q = WeightQuantizer()
+    q.configure(bits, perchannel=True, sym=sym, mse=True, hclip=True, weight_groupsize=wg)
+    q.find_params(x.to(dev), hd.to(dev))
+    oq = oquant.WeightQuantizer().configure(bits, sym=sym, mse=True, hclip=True,
+                                           weight_groupsize=wg)
+    oq.find_params(x, hd)
+    s, z = q.scale.cpu(), q.zero.cpu()
+    assert s.shape == oq.scale.shape
+    if layout == "nan":
+        # rows of block 1 score NaN for every candidate and keep the min/max fit
+        assert torch.equal(s[32:64], oq.scale[32:64]) and torch.equal(z[32:64], oq.zero[32:64])
+    same = (s == oq.scale) & (z == oq.zero)
+    assert same.float().mean() >= 0.97
+    if layout == "uniform":
+        plain = WeightQuantizer()
+        plain.configure(bits, perchannel=True, sym=sym, mse=True)
+        plain.find_params(x.to(dev))
+        assert torch.equal(plain.scale.cpu(), s) and torch.equal(plain.zero.cpu(), z)
+        return
+    if layout == "nan":
+        return
+
+    def err(s_, z_):
+        maxq = 2 ** (bits - 1) - 1
+        xx = x.double().reshape(96, -1, 128 if wg == -1 else wg)
+        ss, zz = s_.double().unsqueeze(-1), z_.double().unsqueeze(-1)
+        qq = torch.clamp(torch.round(xx / ss) + zz, -(maxq + 1), maxq)
+        w = hd.double().reshape(3, 1, *xx.shape[1:]).expand(3, 32, *xx.shape[1:])
+        return ((ss * (qq - zz) - xx) ** 2 * w.reshape(xx.shape)).sum(-1)
+    assert torch.all(err(s, z) <= err(oq.scale, oq.zero) * (1 + 1e-5))
+
+
+def test_find_params_hclip_needs_hdiag(dev):
+    """The reference reshapes H_diag whenever hclip is set: a missing one is an
+    AttributeError, a mis-shaped one a RuntimeError."""
+    from g2ptq_amd import WeightQuantizer
+    q = WeightQuantizer()
+    q.configure(4, perchannel=True, sym=True, mse=True, hclip=True)
+    x = torch.randn(8, 16, device=dev)
+    with pytest.raises(AttributeError):
+        q.find_params(x)
+    with pytest.raises(RuntimeError):
+        q.find_params(x, torch.ones(3, 15, device=dev))
+    with pytest.raises(RuntimeError):
+        q.find_params(x, torch.ones(3, 16, device=dev))  # 8 rows do not split into 3 blocks
+
+
 @pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
 def test_gptq_block_bitexact(dev, case):
     from g2ptq_amd.gptq_utils import run_eager

@@ -90,6 +90,84 @@ def test_quant_mse_never_worse_than_minmax():
         assert torch.all(err(s1, z1) <= err(s0, z0) + 1e-12)
 
 
+def test_quant_hclip_uniform_weights():
+    """hclip: a constant H_diag of 4 (an exact power-of-two scale of every error
+    term) ranks candidates exactly like the unweighted squared error (norm 2),
+    not like |err|^2.4; and the quantizer drops a constant H_diag altogether
+    (quant_utils.py:395-397), giving the plain norm-2.4 search."""
+    x = torch.randn(24, 64, generator=gen(11)) * 0.02
+    for sym in (True, False):
+        h4 = torch.full((1, 1, 64), 4.0)
+        s_h, z_h = oquant.find_params(x, 3, sym, mse=True, H_diag=h4)
+        s_2, z_2 = oquant.find_params(x, 3, sym, mse=True, norm=2.0)
+        s_24, z_24 = oquant.find_params(x, 3, sym, mse=True)
+        assert torch.equal(s_h, s_2) and torch.equal(z_h, z_2)
+        assert not torch.equal(s_2, s_24)  # the data tells the two objectives apart
+        q = oquant.WeightQuantizer().configure(3, sym=sym, mse=True, hclip=True)
+        q.find_params(x, torch.full((2, 64), 0.3))
+        assert torch.equal(q.scale, s_24) and torch.equal(q.zero, z_24)
+
+
+def _brute_force_clip(xrow, w, bits, sym, grid=50, maxshrink=0.5):
+    """First strict minimum over the clip grid of sum_c (fq_c - x_c)^2 * w_c,
+    one row at a time with scalar fp32 arithmetic (independent of the
+    oracle's tensor reshapes)."""
+    maxq = 2 ** (bits - 1) - 1
+    minq = -(maxq + 1)
+    f = lambda v: torch.tensor(v, dtype=torch.float32)
+    xmin = min(f(xrow.min().item()), f(0.0))
+    xmax = max(f(xrow.max().item()), f(0.0))
+    best, choice = math.inf, None
+    steps = int(maxshrink * grid)
+    for i in range(steps):
+        for j in range(steps):
+            lo = (1 - i / grid) * xmin
+            hi = (1 - j / grid) * xmax
+            if sym:
+                s = torch.maximum(lo.abs(), hi) / ((maxq - minq) / 2)
+                z = f(0.0)
+            else:
+                s = (hi - lo) / (maxq - minq)
+                z = torch.clamp(torch.round(minq - lo / s), minq, maxq)
+            err = 0.0
+            for c in range(xrow.numel()):
+                if w[c] == 0:
+                    continue
+                q = torch.clamp(torch.round(xrow[c] / s) + z, minq, maxq)
+                d = (s * (q - z) - xrow[c]).double().item()
+                err += d * d * float(w[c])
+            if err < best:
+                best, choice = err, (s.item(), torch.round(z).item())
+    return choice
+
+
+def test_quant_hclip_rows_use_their_block_and_group():
+    """hclip weights: rows split into H_diag.shape[0] consecutive blocks, and with
+    weight_groupsize each row's column group k uses H_diag[b, k*g:(k+1)*g].
+    One-hot weights make every row's objective a single column's error, whose
+    first strict minimum is found by brute force."""
+    g = gen(12)
+    x = torch.randn(6, 8, generator=g) * 0.05            # 2 blocks of 3 rows
+    h = torch.zeros(2, 8)
+    h[0, 1] = 1.0
+    h[1, 6] = 2.0
+    q = oquant.WeightQuantizer().configure(3, sym=False, mse=True, hclip=True)
+    q.find_params(x, h)
+    for r in range(6):
+        s, z = _brute_force_clip(x[r], h[r // 3], 3, False)
+        assert q.scale[r, 0].item() == s and q.zero[r, 0].item() == z, r
+    # grouped: 2 groups of 4 columns per row, each with its own weight column
+    h2 = torch.zeros(2, 8)
+    h2[0, 2] = h2[0, 5] = 1.0
+    h2[1, 0] = h2[1, 7] = 1.0
+    q2 = oquant.WeightQuantizer().configure(4, sym=True, mse=True, hclip=True, weight_groupsize=4)
+    q2.find_params(x, h2)
+    for r in range(6):
+        for k in range(2):
+            s, z = _brute_force_clip(x[r, 4 * k:4 * k + 4], h2[r // 3, 4 * k:4 * k + 4], 4, True)
+            assert q2.scale[r, k].item() == s and q2.zero[r, k].item() == z, (r, k)
+
+
 # ---------------------------------------------------------------------------
 # Hessians
 # ---------------------------------------------------------------------------
