@@ -13,6 +13,12 @@
 // 32/bits codes as one contiguous run), and one thread per scale element
 // (comparing it with its group's first scale, and writing the group's value
 // from the group's first column).
+//
+// MoE expert stacking (utils/models/mixins.py:93-144) turns the per-expert
+// tensors of a layer into 3-D checkpoint tensors with torch.stack of
+// torch.cat's; here one launch copies every expert's tensor to its place
+// (concat_kernel: workgroup column y copies source y, 16-byte vectors when
+// both ends are aligned).
 #include <algorithm>
 
 #include "common.hpp"
@@ -73,6 +79,31 @@ __global__ void group_scale_kernel(const float* __restrict__ scale, int64_t lds,
   if (bad && (threadIdx.x & 63) == 0 && flags) atomicOr(flags, G2PTQ_FLAG_GROUP_SCALE);
 }
 
+constexpr int64_t kConcatChunk = 256 * 16 * 8;  // bytes per workgroup pass
+
+__global__ __launch_bounds__(256) void concat_kernel(const uint64_t* __restrict__ src,
+                                                     const int64_t* __restrict__ off,
+                                                     unsigned char* __restrict__ dst) {
+  const int64_t b = blockIdx.y;
+  const int64_t lo = off[b], size = off[b + 1] - lo;
+  const unsigned char* s = reinterpret_cast<const unsigned char*>(src[b]);
+  unsigned char* d = dst + lo;
+  const bool vec = ((reinterpret_cast<uintptr_t>(s) | reinterpret_cast<uintptr_t>(d)) & 15) == 0;
+  for (int64_t c0 = (int64_t)blockIdx.x * kConcatChunk; c0 < size;
+       c0 += (int64_t)gridDim.x * kConcatChunk) {
+    const int64_t c1 = c0 + kConcatChunk < size ? c0 + kConcatChunk : size;
+    int64_t i = c0;
+    if (vec) {
+      const int64_t v1 = c0 + (c1 - c0) / 16 * 16;
+#pragma unroll 8
+      for (int64_t k = c0 + 16 * (int64_t)threadIdx.x; k < v1; k += 16 * 256)
+        *reinterpret_cast<uint4*>(d + k) = *reinterpret_cast<const uint4*>(s + k);
+      i = v1;
+    }
+    for (int64_t k = i + threadIdx.x; k < c1; k += 256) d[k] = s[k];
+  }
+}
+
 unsigned grid_of(int64_t n) {
   return (unsigned)std::max<int64_t>(1, std::min<int64_t>(cdiv(n, 256), 16384));
 }
@@ -81,6 +112,21 @@ unsigned grid_of(int64_t n) {
 }  // namespace g2ptq
 
 using namespace g2ptq;
+
+extern "C" int g2ptq_concat(void* stream, const uint64_t* src, const int64_t* off, int64_t n,
+                            int64_t max_bytes, void* dst) {
+  G2PTQ_CHECK(n >= 0 && n < 65536, "concat: %lld buffers (at most 65535)", (long long)n);
+  G2PTQ_CHECK(max_bytes >= 0, "concat: negative size");
+  if (n == 0 || max_bytes == 0) return G2PTQ_OK;
+  G2PTQ_CHECK(src && off && dst, "concat: null pointer");
+  // enough workgroups per source to cover the largest one, at most ~4096 in all
+  const int64_t per = std::max<int64_t>(1, std::min<int64_t>(cdiv(max_bytes, kConcatChunk),
+                                                             cdiv(4096, n)));
+  hipLaunchKernelGGL(concat_kernel, dim3((unsigned)per, (unsigned)n), dim3(256), 0,
+                     as_stream(stream), src, off, static_cast<unsigned char*>(dst));
+  G2PTQ_LAUNCHED();
+  return G2PTQ_OK;
+}
 
 extern "C" int g2ptq_pack_quantized(void* stream, const float* codes, int64_t ldc,
                                     const float* scale, int64_t lds, int64_t rows, int64_t cols,

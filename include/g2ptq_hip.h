@@ -291,6 +291,15 @@ int g2ptq_pack_quantized(void* stream, const float* codes, int64_t ldc, const fl
                          int32_t* packed, int64_t ldp, void* scale_out, int dtype, int64_t ldo,
                          int* flags);
 
+/* Concatenation of n device buffers into dst: bytes [off[b], off[b+1]) of dst
+ * receive the first off[b+1] − off[b] bytes of src[b].  src (n device
+ * addresses) and off (n + 1 byte offsets, off[0] = 0, non-decreasing) are
+ * themselves in device memory; max_bytes is at least the largest block.
+ * One launch for the torch.stack(torch.cat(...)) expert stacking of
+ * utils/models/mixins.py:93-144 (MoEMixin.stack_experts). */
+int g2ptq_concat(void* stream, const uint64_t* src, const int64_t* off, int64_t n,
+                 int64_t max_bytes, void* dst);
+
 /* Generic batched fp32 GEMM (MFMA): D = alpha·A·op(B) + beta·C for `batch`
  * matrices; A row-major M×K, B row-major K×N (b_trans = 0) or N×K
  * (b_trans = 1).  Exported for the host classes' small products. */

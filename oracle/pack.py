@@ -8,10 +8,13 @@ int8 code plus 2^(bits−1) as an unsigned bits-wide field, 32 // bits
 consecutive input columns per int32 word, the first column in the lowest
 bits, columns past the end zero.
 
+Also the MoE expert stacking of the checkpoint (utils/models/mixins.py:93-144).
+
 Parity: no reference test or fixture covers packing, and the library is
 absent, so this restatement is pinned by hand-derived known answers of the
 format, by an independent bit-by-bit unpacker (round trip) and by the field
-layout (tests/test_oracle_pins.py).
+layout (tests/test_oracle_pins.py).  The stacking is pinned element by
+element against its index map.
 """
 import numpy as np
 import torch
@@ -47,4 +50,35 @@ def compress(weight_shape, weight_dtype, Scale, W_int, bits, groupsize):
         "weight_packed": pack_to_int32(quantized_weight, bits).contiguous(),
         "weight_scale": group_scale[:, :, 0].to(weight_dtype).contiguous(),
         "weight_shape": torch.tensor(weight_shape).contiguous(),
+    }
+
+
+def stack_experts(gate, up, down, weight_packed=False):
+    """utils/models/mixins.py:93-144 on CPU tensors.
+
+    ``gate``, ``up``, ``down``: per-expert dicts of the modules' tensors
+    (``weight``, or ``weight_packed`` / ``weight_scale`` / ``weight_shape``).
+    Returns the attributes the reference sets on the experts container.
+    """
+    E = len(gate)
+    if weight_packed:
+        out = {
+            "gate_up_proj_packed": torch.stack(
+                [torch.cat([gate[i]["weight_packed"], up[i]["weight_packed"]], dim=0)
+                 for i in range(E)], dim=0),
+            "down_proj_packed": torch.stack([down[i]["weight_packed"] for i in range(E)], dim=0),
+            "gate_up_proj_scale": torch.stack(
+                [torch.cat([gate[i]["weight_scale"], up[i]["weight_scale"]], dim=0)
+                 for i in range(E)], dim=0),
+            "down_proj_scale": torch.stack([down[i]["weight_scale"] for i in range(E)], dim=0),
+        }
+        inter = int(gate[0]["weight_shape"][0])
+        hidden = int(gate[0]["weight_shape"][1])
+        out["gate_up_proj_shape"] = torch.tensor((E, 2 * inter, hidden))
+        out["down_proj_shape"] = torch.tensor((E, hidden, inter))
+        return out
+    return {
+        "gate_up_proj": torch.stack([torch.cat([gate[i]["weight"], up[i]["weight"]], dim=0)
+                                     for i in range(E)], dim=0),
+        "down_proj": torch.stack([down[i]["weight"] for i in range(E)], dim=0),
     }

@@ -620,3 +620,40 @@ def test_compress_group_scales_and_assert():
     Scale[2, 5] += 1.0
     with pytest.raises(AssertionError):
         opack.compress((rows, cols), torch.bfloat16, Scale, codes, 4, gs)
+
+
+def test_stack_experts_index_map():
+    """mixins.py:93-144: gate_up[e, r] is gate_e[r] for r < I and up_e[r − I] after;
+    down[e] is down_e; scales likewise; the shape tensors are (E, 2I, H) and
+    (E, H, I).  Checked element by element on distinct values."""
+    E, I, H, W, G = 3, 4, 6, 2, 3
+    val = iter(range(10 ** 6))
+
+    def t(r, c, dtype=torch.int32):
+        return torch.tensor([[next(val) for _ in range(c)] for _ in range(r)], dtype=dtype)
+    gate = [{"weight_packed": t(I, W), "weight_scale": t(I, G, torch.float32),
+             "weight_shape": torch.tensor((I, H))} for _ in range(E)]
+    up = [{"weight_packed": t(I, W), "weight_scale": t(I, G, torch.float32),
+           "weight_shape": torch.tensor((I, H))} for _ in range(E)]
+    down = [{"weight_packed": t(H, 1), "weight_scale": t(H, 1, torch.float32),
+             "weight_shape": torch.tensor((H, I))} for _ in range(E)]
+    out = opack.stack_experts(gate, up, down, weight_packed=True)
+    for e in range(E):
+        for r in range(2 * I):
+            src = gate[e] if r < I else up[e]
+            for c in range(W):
+                assert out["gate_up_proj_packed"][e, r, c] == src["weight_packed"][r % I, c]
+            for c in range(G):
+                assert out["gate_up_proj_scale"][e, r, c] == src["weight_scale"][r % I, c]
+        for r in range(H):
+            assert out["down_proj_packed"][e, r, 0] == down[e]["weight_packed"][r, 0]
+            assert out["down_proj_scale"][e, r, 0] == down[e]["weight_scale"][r, 0]
+    assert out["gate_up_proj_shape"].tolist() == [E, 2 * I, H]
+    assert out["down_proj_shape"].tolist() == [E, H, I]
+    wg = [{"weight": t(I, H, torch.float32)} for _ in range(E)]
+    wu = [{"weight": t(I, H, torch.float32)} for _ in range(E)]
+    wd = [{"weight": t(H, I, torch.float32)} for _ in range(E)]
+    out = opack.stack_experts(wg, wu, wd)
+    assert out["gate_up_proj"].shape == (E, 2 * I, H) and out["down_proj"].shape == (E, H, I)
+    assert out["gate_up_proj"][1, I + 2, 3] == wu[1]["weight"][2, 3]
+    assert out["down_proj"][2, 5, 1] == wd[2]["weight"][5, 1]
