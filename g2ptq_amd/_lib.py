@@ -63,6 +63,8 @@ SIGNATURES = {
     "g2ptq_pack_quantized": [_p, _p, _i64, _p, _i64, _i64, _i64, _i32, _i64, _p, _i64, _p, _i32, _i64,
                              _p],
     "g2ptq_concat": [_p, _p, _p, _i64, _i64, _p],
+    "g2ptq_group_mean_square": [_p, _p, _i32, _i64, _i64, _i64, _i64, _p],
+    "g2ptq_running_mean_update": [_p, _p, _p, _i32, _i64, _f32, _f32, _i32],
     "g2ptq_gemm_f32": [_p, _i64, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64, _i64, _i32, _p, _i64, _i64,
                        _p, _i64, _i64, _f32, _f32],
 }

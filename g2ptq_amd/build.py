@@ -27,7 +27,7 @@ FLAGS = [
 # Per-file extra flags.  The quantize / sweep kernels must round every product
 # and sum separately (the reference's torch ops never fuse); the flag also
 # covers the HIP header's __f*_rn helpers, which a source-level pragma cannot.
-EXTRA = {"quant.hip": ["-ffp-contract=off"]}
+EXTRA = {"quant.hip": ["-ffp-contract=off"], "calib.hip": ["-ffp-contract=off"]}
 
 
 def sources():

@@ -291,6 +291,24 @@ int g2ptq_pack_quantized(void* stream, const float* codes, int64_t ldc, const fl
                          int32_t* packed, int64_t ldp, void* scale_out, int dtype, int64_t ldo,
                          int* flags);
 
+/* ------------------------------------------------------------------------
+ * Calibration statistics — gptq_utils/g2ptq_utils.py (SaliencyCache, GradientCache)
+ * ---------------------------------------------------------------------- */
+
+/* SaliencyCache.grad_hook (g2ptq_utils.py:604-618): out[t][g] = mean over the
+ * g-th of `groups` equal column groups of x[t][·]², x rows × cols (ld ldx,
+ * dtype 0 bf16, 1 fp16, 2 fp32), out rows × groups fp32.  The mean is the
+ * fp32 sum times fp32(1/group size). */
+int g2ptq_group_mean_square(void* stream, const void* x, int dtype, int64_t rows, int64_t cols,
+                            int64_t ldx, int64_t groups, float* out);
+
+/* GradientCache.cache_gradient (g2ptq_utils.py:704-714), elementwise over n:
+ * cache = cache·keep + grad·inv_count in fp32 (keep = fp32(k/(k+1)),
+ * inv_count = fp32(1/fp32(n_tokens·(k+1))), torch's division by a Python
+ * number on the GPU); first != 0: cache = 0 + grad·inv_count (no read). */
+int g2ptq_running_mean_update(void* stream, float* cache, const void* grad, int dtype, int64_t n,
+                              float keep, float inv_count, int first);
+
 /* Concatenation of n device buffers into dst: bytes [off[b], off[b+1]) of dst
  * receive the first off[b+1] − off[b] bytes of src[b].  src (n device
  * addresses) and off (n + 1 byte offsets, off[0] = 0, non-decreasing) are

@@ -118,3 +118,57 @@ def test_weight_quantizer_deepcopy_is_independent():
     assert set(c.state_dict()) == {"scale", "zero"}
     qs = make_group_quantizers(q, 300, 128)
     assert len(qs) == 3 and len({id(x.scale) for x in qs}) == 3
+
+
+def _fp_cache_model():
+    torch.manual_seed(0)
+    return torch.nn.ModuleDict({"q": _linear(8, 16), "k": _linear(4, 16), "v": _linear(4, 16),
+                                "o": _linear(16, 8)})
+
+
+@pytest.mark.parametrize("offload", [False, True])
+def test_fp_inputs_cache_shared_groups(offload):
+    """gptaq_utils.py:442-555: each name's FIFO receives its input per batch (2-D
+    view); offloaded, shared-input members point at the one host slice their
+    first member copied, consecutive batches fill consecutive rows."""
+    from g2ptq_amd.calib_utils import FPInputsCache
+    m = _fp_cache_model()
+    full = dict(m.items())
+    cache = FPInputsCache([["q", "k", "v"], ["o"]], full, nsamples=4, seqlen=5,
+                          dtype=torch.float32, offload_inps=offload,
+                          shared_input_groups=[("q", "k", "v"), ("o",), ("not_here",)])
+    cache.add_hook(full)
+    xs = [torch.randn(1, 5, 16) for _ in range(3)]
+    for x in xs:
+        for n in ("q", "k", "v"):
+            full[n](x)
+        full["o"](torch.randn(1, 5, 8))
+    cache.clear_hook()
+    for n in ("q", "k", "v"):
+        assert len(cache.fp_cache[n]) == 3
+        for got, x in zip(cache.fp_cache[n], xs):
+            assert torch.equal(got, x.reshape(5, 16))
+    if offload:
+        assert set(cache.fp_buffers) == {"q", "o"}
+        assert cache.cursor == {"q": 15, "o": 15}
+        assert cache.fp_cache["k"][1].data_ptr() == cache.fp_cache["q"][1].data_ptr()
+        assert torch.equal(cache.fp_buffers["q"][5:10], xs[1].reshape(5, 16))
+        # a member receiving another tensor than its group-mate is a spec error
+        cache.add_hook(full)
+        full["q"](xs[0])
+        with pytest.raises(AssertionError, match="received a different tensor"):
+            full["k"](torch.randn(1, 5, 16))
+        cache.clear_hook()
+    cache.clear_cache()
+    assert cache.fp_cache == {} and cache.fp_buffers == {}
+
+
+def test_fp_inputs_cache_overflow():
+    from g2ptq_amd.calib_utils import FPInputsCache
+    m = _fp_cache_model()
+    full = dict(m.items())
+    cache = FPInputsCache([["o"]], full, nsamples=1, seqlen=4, dtype=torch.float32,
+                          offload_inps=True, shared_input_groups=[("o",)])
+    cache.add_hook(full)
+    with pytest.raises(AssertionError, match="overflowed"):
+        full["o"](torch.randn(1, 5, 8))

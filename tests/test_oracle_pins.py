@@ -657,3 +657,47 @@ def test_stack_experts_index_map():
     assert out["gate_up_proj"].shape == (E, 2 * I, H) and out["down_proj"].shape == (E, H, I)
     assert out["gate_up_proj"][1, I + 2, 3] == wu[1]["weight"][2, 3]
     assert out["down_proj"][2, 5, 1] == wd[2]["weight"][5, 1]
+
+
+# ---------------------------------------------------------------------------
+# Calibration statistics (gptq_utils/g2ptq_utils.py:586-766)
+# ---------------------------------------------------------------------------
+
+def test_calib_saliency_closed_forms():
+    """Constant gradients give exact group means (c² with power-of-two sizes);
+    random gradients match the fp64 mean of squares per group; groups are
+    consecutive column ranges (a gradient nonzero in one range only lights
+    only that group)."""
+    from oracle import calib as ocalib
+    g = torch.full((2, 3, 64), 0.5)
+    s = ocalib.group_mean_square(g, 4)
+    assert s.shape == (6, 4) and torch.all(s == 0.25)
+    x = torch.randn(5, 96, generator=gen(21))
+    s = ocalib.group_mean_square(x, 3)
+    ref = (x.double() ** 2).view(5, 3, 32).mean(-1)
+    assert torch.allclose(s.double(), ref, rtol=2e-6, atol=0)
+    y = torch.zeros(4, 96)
+    y[:, 40:50] = 1.0
+    s = ocalib.group_mean_square(y, 3)
+    assert s[:, 1].tolist() == [10 / 32] * 4 and torch.all(s[:, [0, 2]] == 0)
+
+
+def test_calib_running_mean_closed_forms():
+    """After K calls, cache = Σ_i grad_i / (n_i·K): the mean over batches of the
+    per-token gradient (fp64 within fp32 rounding); identical batches leave
+    grad/n; the first call is exactly grad·fp32(1/n)."""
+    from oracle import calib as ocalib
+    gg = gen(22)
+    grads = [torch.randn(7, 9, generator=gg) for _ in range(5)]
+    ns = [128, 64, 300, 1, 77]
+    c = None
+    for i, (gr, n) in enumerate(zip(grads, ns)):
+        c = ocalib.running_mean(c, gr, n, i)
+    ref = sum(gr.double() / n for gr, n in zip(grads, ns)) / len(grads)
+    assert torch.allclose(c.double(), ref, rtol=1e-5, atol=1e-7)
+    c = None
+    for i in range(4):
+        c = ocalib.running_mean(c, grads[0], 256, i)
+    assert torch.allclose(c, grads[0] / 256, rtol=1e-6, atol=0)
+    first = ocalib.running_mean(None, grads[1], 3, 0)
+    assert torch.equal(first, grads[1] * torch.tensor(1.0, dtype=torch.float32).div(3.0))
