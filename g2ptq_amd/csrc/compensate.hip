@@ -123,10 +123,12 @@ extern "C" int g2ptq_compensate_workspace(int variant, int64_t B, int64_t R, int
   (void)C;
   G2PTQ_CHECK(bytes != nullptr, "compensate_workspace: null out");
   // The super-block width depends on the group layout; size for the widest
-  // (a dynamic group size that is coprime to the block size is bounded by C).
+  // (a dynamic group size that is coprime to the block size is bounded by C),
+  // twice: the error columns of consecutive super-blocks alternate between
+  // two buffers so that one's far tail can run while the next is swept.
   const int64_t bs = std::max<int64_t>(blocksize, 1);
   const int64_t widest = variant == G2PTQ_VARIANT_G2PTQ ? bs : std::max<int64_t>(512, bs);
-  *bytes = al256((size_t)B * R * widest * 4);
+  *bytes = 2 * al256((size_t)B * R * widest * 4);
   return G2PTQ_OK;
 }
 
@@ -157,12 +159,22 @@ extern "C" int g2ptq_compensate(void* stream, int variant, int64_t B, int64_t R,
     need = al256((size_t)B * R * SB * 4);
   }
   G2PTQ_CHECK(ws && ws_bytes >= need, "compensate: workspace %zu < %zu", ws_bytes, need);
-  float* E = static_cast<float*>(ws);
+  // Lookahead: with room for two error buffers, and outside graph capture,
+  // the tail of a super-block beyond the next super-block's columns (the
+  // "far" tail) runs on the side stream while the next super-block is swept.
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  G2PTQ_HIP(hipStreamIsCapturing(s, &capture));
+  const bool overlap = ws_bytes >= 2 * need && capture == hipStreamCaptureStatusNone && SB < C;
+  SideStream side;
+  if (overlap) G2PTQ_TRY(side_stream(side));
+  float* Ebuf[2] = {static_cast<float*>(ws),
+                    overlap ? static_cast<float*>(ws) + need / 4 : static_cast<float*>(ws)};
   const int64_t RC = R * C, CC = C * C;
 
-  // W[:, :, c0:c1] -= Ecols · U[k0:k1, c0:c1]  (+ GPTAQ: += Q[:, :, k0:k1] · P[k0:k1, c0:c1]).
-  auto tail = [&](const float* Ecols, int64_t lde, int64_t k0, int64_t k1, int64_t c0,
-                  int64_t c1) -> int {
+  // W[:, :, c0:c1] -= Ecols · U[k0:k1, c0:c1]  (+ GPTAQ: += Q[:, :, k0:k1] · P[k0:k1, c0:c1]),
+  // on stream q.  Every tail reads and writes only its own columns c0..c1.
+  auto tail_on = [&](hipStream_t q, const float* Ecols, int64_t lde, int64_t k0, int64_t k1,
+                     int64_t c0, int64_t c1) -> int {
     GemmF32 t;
     t.M = R; t.N = c1 - c0; t.K = k1 - k0; t.batch = B;
     t.A = Ecols; t.lda = lde; t.sA = R * lde;
@@ -174,25 +186,33 @@ extern "C" int g2ptq_compensate(void* stream, int variant, int64_t B, int64_t R,
       // W -= bs·GH[:, c0:] + (E − Z·D)·U_slab, with E2 = E − Z·D from the sweep.
       t.X = GH + c0; t.ldx = C; t.sX = RC; t.gamma = -(float)bs;
     }
-    G2PTQ_TRY(gemm_f32(s, t));
+    G2PTQ_TRY(gemm_f32(q, t));
     if (variant == G2PTQ_VARIANT_GPTAQ) {
       GemmF32 p = t;  // W += Q1 · P[k0:k1, c0:c1]
       p.A = Q + k0; p.lda = C; p.sA = RC;
       p.B = P + k0 * C + c0;
       p.alpha = 1.f;
-      G2PTQ_TRY(gemm_f32(s, p));
+      G2PTQ_TRY(gemm_f32(q, p));
     } else if (variant == G2PTQ_VARIANT_G2PTQ) {
       GemmF32 z = t;  // GH[:, c0:c1] -= Z1 · U_slab
       z.A = Z + k0; z.lda = C; z.sA = RC;
       z.C = GH + c0; z.D = GH + c0;
       z.X = nullptr; z.gamma = 0.f;
-      G2PTQ_TRY(gemm_f32(s, z));
+      G2PTQ_TRY(gemm_f32(q, z));
     }
     return G2PTQ_OK;
   };
+  auto tail = [&](const float* Ecols, int64_t lde, int64_t k0, int64_t k1, int64_t c0,
+                  int64_t c1) -> int { return tail_on(s, Ecols, lde, k0, k1, c0, c1); };
 
-  for (int64_t s0 = 0; s0 < C; s0 += SB) {
+  // Every column receives the tails of the super-blocks before it in order:
+  // the far tail of super-block p (columns from p + 2 on, side stream) lands
+  // before the near tail of p + 1 (columns of p + 2, caller's stream), which
+  // waits for it; that wait also frees p's error buffer for p + 2's sweeps.
+  bool far_pending = false;
+  for (int64_t s0 = 0, sbi = 0; s0 < C; s0 += SB, ++sbi) {
     const int64_t s1 = std::min(s0 + SB, C);
+    float* E = Ebuf[sbi & 1];
     for (int64_t i1 = s0; i1 < s1; i1 += bs) {
       const int64_t i2 = std::min(i1 + bs, C), n = i2 - i1;
       if (dynamic) {
@@ -241,8 +261,24 @@ extern "C" int g2ptq_compensate(void* stream, int variant, int64_t B, int64_t R,
       if (i2 < s1) G2PTQ_TRY(tail(Eb, SB, i1, i2, i2, s1));
     }
     // The super-block's errors applied to every later column at once.
-    if (s1 < C) G2PTQ_TRY(tail(E, SB, s0, s1, s1, C));
+    if (s1 < C) {
+      if (!overlap) {
+        G2PTQ_TRY(tail(E, SB, s0, s1, s1, C));
+        continue;
+      }
+      const int64_t nxt = std::min(s1 + SB, C);  // end of the next super-block's columns
+      if (far_pending) G2PTQ_HIP(hipStreamWaitEvent(s, side.tailed, 0));
+      far_pending = nxt < C;
+      if (far_pending) {
+        G2PTQ_HIP(hipEventRecord(side.swept, s));
+        G2PTQ_HIP(hipStreamWaitEvent(side.stream, side.swept, 0));
+        G2PTQ_TRY(tail_on(side.stream, E, SB, s0, s1, nxt, C));
+        G2PTQ_HIP(hipEventRecord(side.tailed, side.stream));
+      }
+      G2PTQ_TRY(tail(E, SB, s0, s1, s1, nxt));
+    }
   }
+  if (far_pending) G2PTQ_HIP(hipStreamWaitEvent(s, side.tailed, 0));
   return G2PTQ_OK;
 }
 

@@ -153,33 +153,6 @@ struct FactorWs {
   size_t wa, wt, sums, st, total;
 };
 
-// A second stream (default priority) and events per device, created once, for
-// the factor's lookahead.  Calls that overlap on one device would share them:
-// the library's entry points are not meant to run concurrently on one device.
-struct SideStream {
-  hipStream_t stream = nullptr;
-  hipEvent_t factored = nullptr;
-  hipEvent_t done[2] = {nullptr, nullptr};
-};
-
-int side_stream(SideStream& out) {
-  static std::mutex mu;
-  static SideStream cache[64];
-  int dev = 0;
-  G2PTQ_HIP(hipGetDevice(&dev));
-  G2PTQ_CHECK(dev >= 0 && dev < 64, "factor: device index %d", dev);
-  std::lock_guard<std::mutex> lock(mu);
-  SideStream& c = cache[dev];
-  if (c.stream == nullptr) {
-    G2PTQ_HIP(hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking));
-    G2PTQ_HIP(hipEventCreateWithFlags(&c.factored, hipEventDisableTiming));
-    G2PTQ_HIP(hipEventCreateWithFlags(&c.done[0], hipEventDisableTiming));
-    G2PTQ_HIP(hipEventCreateWithFlags(&c.done[1], hipEventDisableTiming));
-  }
-  out = c;
-  return G2PTQ_OK;
-}
-
 FactorWs factor_ws(int64_t B, int64_t C) {
   FactorWs w;
   auto al = [](size_t x) { return (x + 255) / 256 * 256; };
@@ -193,6 +166,24 @@ FactorWs factor_ws(int64_t B, int64_t C) {
 }
 
 }  // namespace
+
+int side_stream(SideStream& out) {
+  static std::mutex mu;
+  static SideStream cache[64];
+  int dev = 0;
+  G2PTQ_HIP(hipGetDevice(&dev));
+  G2PTQ_CHECK(dev >= 0 && dev < 64, "side stream: device index %d", dev);
+  std::lock_guard<std::mutex> lock(mu);
+  SideStream& c = cache[dev];
+  if (c.stream == nullptr) {
+    G2PTQ_HIP(hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking));
+    for (hipEvent_t* e : {&c.factored, &c.done[0], &c.done[1], &c.swept, &c.tailed})
+      G2PTQ_HIP(hipEventCreateWithFlags(e, hipEventDisableTiming));
+  }
+  out = c;
+  return G2PTQ_OK;
+}
+
 }  // namespace g2ptq
 
 using namespace g2ptq;

@@ -428,3 +428,47 @@ def test_factor_damp_retry(dev):
     Uo, d_ref = ofactor.damp_chol_inv_upper(H2, 0.01)
     assert abs(d_ref - 0.016) < 1e-9
     assert abs(damps[0] - d_ref) < 1e-12, (damps[0], d_ref)
+
+
+@pytest.mark.parametrize("variant,groupsize", [(0, 128), (0, -1), (1, 128), (2, 128), (0, 96)])
+def test_compensate_far_tail_lookahead_is_bit_identical(dev, variant, groupsize):
+    """The native loop with room for two error buffers runs each super-block's far
+    tail on the side stream while the next super-block is swept; every column
+    still receives its tails in order, so the results equal the one-buffer
+    (serial) schedule bit for bit.  C = 1664 gives four 512-column super-blocks
+    (G2PTQ: thirteen 128-column blocks), the last one ragged."""
+    from g2ptq_amd import _lib
+    B, R, C, bs, bits = 2, 300, 1664, 128, 4
+    g = gen(7100 + 10 * variant + (groupsize > 0))
+    W0 = torch.randn(B, R, C, generator=g) * 0.05
+    U = torch.triu(torch.randn(B, C, C, generator=g) * (0.5 / C ** 0.5), diagonal=1)
+    U.diagonal(dim1=1, dim2=2).copy_(torch.rand(B, C, generator=g) * 0.5 + 0.75)
+    P = torch.triu(torch.randn(B, C, C, generator=g) * 1e-3, diagonal=1) if variant == 1 else None
+    Z = torch.randn(B, R, C, generator=g) * 1e-3 if variant == 2 else None
+    GH0 = torch.randn(B, R, C, generator=g) * 1e-3 if variant == 2 else None
+    ngroups = 1 if groupsize == -1 else -(-C // groupsize)
+    Ud = U.to(dev)
+    Pd = P.to(dev) if P is not None else None
+    Zd = Z.to(dev) if Z is not None else None
+    full = _lib.query_size("g2ptq_compensate_workspace", variant, B, R, C, bs)
+    outs = []
+    for ws_bytes in (full, full // 2):
+        W = W0.clone().to(dev)
+        GH = GH0.clone().to(dev) if GH0 is not None else None
+        stab = torch.empty(ngroups, B * R, device=dev)
+        ztab = torch.empty(ngroups, B * R, device=dev)
+        if groupsize == -1:
+            amax = W.abs().amax(dim=2).reshape(1, B * R)
+            stab.copy_(amax / 7)
+            ztab.zero_()
+        Q, Wi, Sc = (torch.empty_like(W) for _ in range(3))
+        flags = torch.zeros(1, dtype=torch.int32, device=dev)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        _lib.call("g2ptq_compensate", _lib.stream_ptr(dev), variant, B, R, C, bs, _lib.ptr(W),
+                  _lib.ptr(Ud), _lib.ptr(Pd), _lib.ptr(Zd), _lib.ptr(GH), bits, 1, groupsize, 0,
+                  0, 2.4, 0.5, None, 0, None, _lib.ptr(stab), _lib.ptr(ztab), _lib.ptr(Q),
+                  _lib.ptr(Wi), _lib.ptr(Sc), _lib.ptr(flags), _lib.ptr(ws), ws_bytes)
+        torch.cuda.synchronize()
+        outs.append([t.cpu() for t in (Q, Wi, Sc, W, stab) + ((GH,) if GH is not None else ())])
+    for a, b, name in zip(outs[0], outs[1], ("Q", "W_int", "Scale", "W", "scales", "GH")):
+        assert torch.equal(a, b), name
