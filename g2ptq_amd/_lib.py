@@ -133,7 +133,12 @@ def ptr(t):
 
 
 def stream_ptr(device=None):
-    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+    """The current stream of ``device`` (default: the current device)."""
+    if device is None or device.index is None:
+        index = torch.cuda.current_device()
+    else:
+        index = device.index
+    return ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(index))
 
 
 _WORKSPACES = {}

@@ -137,6 +137,35 @@ class GramStager:
         self.k = 0
 
 
+def lazy_counter(name):
+    """A per-layer int64 device counter (``nsamples``, ``index``, ``total_tokens``)
+    whose ``add_batch`` increments (``bump``) collect on the host and reach the
+    tensor in one in-place add when it is read: a device op per call would
+    cost more host time than the rest of ``add_batch``.  Readers get the
+    stored tensor itself, so in-place updates by callers behave as on the
+    reference's attribute."""
+    private, pend = "_" + name, "_" + name + "_pending"
+
+    def get(self):
+        t = getattr(self, private, None)
+        p = getattr(self, pend, None)
+        if t is not None and p and any(p):
+            t += torch.tensor(p, dtype=t.dtype).to(t.device)
+            setattr(self, pend, [0] * len(p))
+        return t
+
+    def set(self, value):
+        setattr(self, private, value)
+        setattr(self, pend, [0] * (len(value) if value is not None else 0))
+
+    return property(get, set)
+
+
+def bump(owner, name, idx, amount):
+    """``owner.<name>[idx] += amount`` for a ``lazy_counter`` attribute."""
+    getattr(owner, "_" + name + "_pending")[idx] += amount
+
+
 def staged_attr(name):
     """A Hessian attribute whose reads first fold every staged token into it
     (the owner's ``_flush_staged``), and whose deletion (``= None``) folds them

@@ -14,7 +14,7 @@ import torch
 
 from . import _core, _lib
 from .common_utils import fake_quantize_grouped
-from ._stage import KIND_WEIGHTED, GramStager, staged_attr
+from ._stage import KIND_WEIGHTED, GramStager, bump, lazy_counter, staged_attr
 from .compressed_tensors_utils import compress_layers
 from .gptq_utils import _compensate
 from .graph_utils import run_graph, validate_tensors
@@ -78,6 +78,8 @@ class G2PTQ:
     # k batches (k₀ of them already in H) is H = (k₀/k)·H + (1/k)·Σ staged,
     # the reference's running per-batch mean.
     H = staged_attr("H")
+    index = lazy_counter("index")
+    total_tokens = lazy_counter("total_tokens")
 
     def _flush_staged(self, idx=None):
         stagers = getattr(self, "_stagers", None)
@@ -132,8 +134,8 @@ class G2PTQ:
                                   _core.f32(k0 / k), self.act_square[idx], act_alpha, act_beta)
             self._k_flushed[idx] = k
         self._k[idx] = k
-        self.index[idx] += 1
-        self.total_tokens[idx] += n_tokens
+        bump(self, "index", idx, 1)
+        bump(self, "total_tokens", idx, n_tokens)
 
     def _run_compensation_block(self, weight, hinv, scale, zero, z, ghinv, backend, graph,
                                 weight_raw=None):

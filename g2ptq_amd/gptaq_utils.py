@@ -9,7 +9,7 @@ block, ``+Q·P`` in the block tail) run in libg2ptq_hip.so.
 import torch
 
 from . import _core, _lib
-from ._stage import KIND_GPTAQ, GramStager, staged_attr
+from ._stage import KIND_GPTAQ, GramStager, bump, lazy_counter, staged_attr
 from .compressed_tensors_utils import compress_layers
 from .gptq_utils import _compensate
 from .graph_utils import run_graph, validate_tensors
@@ -50,6 +50,7 @@ class GPTAQ:
     # Reads of H or dXXT fold the staged calibration tokens into both first.
     H = staged_attr("H")
     dXXT = staged_attr("dXXT")
+    nsamples = lazy_counter("nsamples")
 
     def _flush_staged(self, idx=None):
         stagers = getattr(self, "_stagers", None)
@@ -97,7 +98,7 @@ class GPTAQ:
                                _core.f32(n0 / n))
             self._n_flushed[idx] = n
         self._n[idx] = n
-        self.nsamples[idx] += tmp
+        bump(self, "nsamples", idx, tmp)
         del self.fp_inp[idx][0]
 
     def _run_compensation_block(self, weight, hinv, p, scale, zero, backend, graph):

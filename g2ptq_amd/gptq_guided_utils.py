@@ -7,13 +7,15 @@ G2PTQ) and GPTQ's compensation, inherited unchanged.
 import torch
 
 from . import _core, _lib
-from ._stage import KIND_WEIGHTED, GramStager
+from ._stage import KIND_WEIGHTED, GramStager, bump, lazy_counter
 from .compressed_tensors_utils import compress_layers
 from .gptq_utils import GPTQ, _compensate
 
 
 class GPTQGuided(GPTQ):
     """gptq_utils/gptq_guided_utils.py:25-219."""
+
+    index = lazy_counter("index")
 
     def __init__(self, layers, saliencies, num_groups: int, offload_hessians: bool = False):
         self.layers = layers
@@ -61,7 +63,7 @@ class GPTQGuided(GPTQ):
         k = self._k[idx]
         sal = self.saliencies[idx][k:k + bsz].to(self.dev)
         self._k[idx] = k + bsz
-        self.index[idx] += bsz
+        bump(self, "index", idx, bsz)
         X = _core.as_bf16_tokens(inp)
         sal = sal.reshape(-1, sal.shape[-1]).float().contiguous()
         n_tokens = X.shape[0]

@@ -9,7 +9,7 @@ the fused lazy-batch compensation in libg2ptq_hip.so.
 import torch
 
 from . import _core, _lib
-from ._stage import GramStager, staged_attr
+from ._stage import GramStager, bump, lazy_counter, staged_attr
 from .compressed_tensors_utils import compress_layers
 from .graph_utils import run_graph, validate_tensors
 
@@ -47,6 +47,7 @@ class GPTQ:
     # (fasterquant, onload/offload, shared-input copies, callers) sees the
     # Hessian of every batch added so far.
     H = staged_attr("H")
+    nsamples = lazy_counter("nsamples")
 
     def _flush_staged(self, idx=None):
         stagers = getattr(self, "_stagers", None)
@@ -87,7 +88,7 @@ class GPTQ:
             _core.hessian_update(self._H[idx], X, _core.sqrt_scale_sq(n), _core.f32(n0 / n))
             self._n_flushed[idx] = n
         self._n[idx] = n
-        self.nsamples[idx] += tmp
+        bump(self, "nsamples", idx, tmp)
 
     def _run_compensation_block(self, weight, hinv, scale, zero, backend, graph):
         """gptq_utils.py:128-163 — one block in (B, R, bs) layout."""

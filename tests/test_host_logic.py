@@ -172,3 +172,28 @@ def test_fp_inputs_cache_overflow():
     cache.add_hook(full)
     with pytest.raises(AssertionError, match="overflowed"):
         full["o"](torch.randn(1, 5, 8))
+
+
+def test_lazy_counter_folds_host_increments_on_read():
+    """nsamples / index: add_batch increments collect on the host and reach the
+    stored tensor in one in-place add when it is read; callers get that tensor
+    itself (in-place updates stick), and assignment resets the pending counts."""
+    from g2ptq_amd._stage import bump, lazy_counter
+
+    class Owner:
+        nsamples = lazy_counter("nsamples")
+
+    o = Owner()
+    o.nsamples = torch.zeros(3, dtype=torch.long)
+    bump(o, "nsamples", 1, 5)
+    bump(o, "nsamples", 1, 2)
+    bump(o, "nsamples", 0, 1)
+    t = o.nsamples
+    assert t.tolist() == [1, 7, 0]
+    t[2] += 4
+    assert o.nsamples is t and o.nsamples.tolist() == [1, 7, 4]
+    bump(o, "nsamples", 2, 1)
+    o.nsamples = torch.ones(3, dtype=torch.long)
+    assert o.nsamples.tolist() == [1, 1, 1]
+    o.nsamples = None
+    assert o.nsamples is None
