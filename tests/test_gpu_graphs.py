@@ -100,3 +100,38 @@ def test_block_graph_replays_match_eager(dev):
         for i, (a, b) in enumerate(zip(g_, e)):
             assert_bitexact(a, b, f"block replay {rep} output {i}")
     clear_graph_cache()
+
+
+@pytest.mark.parametrize("variant", ["G2PTQ", "GPTAQ"])
+def test_block_graph_matches_eager_and_owns_outputs(dev, variant):
+    """tests/test_triton_compensation.py:984-1040: the block operator replayed from
+    a graph equals eager, and the outputs of one replay are not overwritten by
+    the next (each call returns tensors it owns)."""
+    import g2ptq_amd
+    from g2ptq_amd import clear_graph_cache
+    from tests._util import g2_inputs, gptaq_p
+    clear_graph_cache()
+    cls = getattr(g2ptq_amd, variant)
+    B, bs, R, maxq = 2, 16, 193, 7
+    r = object.__new__(cls)
+    r.quantizer = _quantizers(4, False, bs, -1)
+    retained = None
+    for seed in (401, 402):
+        w, h, s, z = ref_inputs(B, bs, R, maxq, True, seed)
+        T = lambda t: t.transpose(1, 2).contiguous().to(dev)  # noqa: E731  (B, R, bs) layout
+        if variant == "G2PTQ":
+            zz, gh = g2_inputs(w, s, seed + 1000)
+            args = (T(w), h.to(dev), T(s), T(z), T(zz), T(gh))
+        else:
+            args = (T(w), h.to(dev), gptaq_p(w, seed + 1000).to(dev), T(s), T(z))
+        eager = r._run_compensation_block(*args, "hip", False)
+        torch.cuda.synchronize()
+        graph_out = r._run_compensation_block(*args, "hip", True)
+        torch.cuda.synchronize()
+        for i, (a, e) in enumerate(zip(graph_out, eager)):
+            assert_bitexact(a, e, f"{variant} seed {seed} output {i}")
+        if retained is not None:
+            for i, (out, snap) in enumerate(zip(*retained)):
+                assert_bitexact(out, snap, f"{variant} earlier output {i} was overwritten")
+        retained = (graph_out, tuple(t.clone() for t in graph_out))
+    clear_graph_cache()

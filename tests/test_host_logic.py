@@ -197,3 +197,10 @@ def test_lazy_counter_folds_host_increments_on_read():
     assert o.nsamples.tolist() == [1, 1, 1]
     o.nsamples = None
     assert o.nsamples is None
+
+
+def test_guided_gptq_reuses_gptq_compensation():
+    """tests/test_triton_compensation.py:908-916."""
+    from g2ptq_amd import GPTQ, GPTQGuided
+    assert GPTQGuided._run_compensation_block is GPTQ._run_compensation_block
+    assert GPTQGuided._run_compensation is GPTQ._run_compensation
