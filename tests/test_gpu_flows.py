@@ -242,3 +242,70 @@ def test_fasterquant_hclip_matches_oracle(dev, case):
     e_hip = oflows.reconstruction_error(W0, Qd, Hr)
     e_ref = oflows.reconstruction_error(W0, Qr, Hr)
     assert abs(e_hip - e_ref) <= 0.005 * e_ref, (e_hip, e_ref)
+
+
+@pytest.mark.parametrize("sym", [True, False])
+def test_gptq_without_calibration_is_rtn(dev, sym):
+    """gptq_utils.py:275-277: an all-zero Hessian becomes the identity, the factor
+    is diagonal, nothing propagates, and the weights equal round-to-nearest with
+    the same groups (gptq_utils.py:598-680), code for code."""
+    from g2ptq_amd import GPTQ, WeightQuantizer, make_group_quantizers
+    B, R, C, gs = 2, 96, 384, 128
+    layers = [_layer(R, C, 70 + b).to(dev) for b in range(B)]
+    W0 = torch.stack([l.weight.detach().float().cpu() for l in layers])
+    gq = GPTQ(layers)
+    q = WeightQuantizer()
+    q.configure(4, perchannel=True, sym=sym)
+    gq.quantizer = make_group_quantizers(q, C, gs)
+    gq.fasterquant(groupsize=gs, backend="hip")
+    torch.cuda.synchronize()
+    Qd = torch.stack([l.weight.detach().float().cpu() for l in layers])
+    fq, _, _ = oflows.rtn(W0, 4, sym, gs)
+    assert torch.equal(Qd, fq.bfloat16().float())
+
+
+def test_dead_columns_are_zeroed(dev):
+    """gptq_utils.py:278-280: input features that never fire (zero Hessian
+    diagonal) get H[d, d] = 1 and W[:, d] = 0, so their weights quantize to 0."""
+    from g2ptq_amd import GPTQ, WeightQuantizer, make_group_quantizers
+    B, R, C, T = 2, 128, 256, 2048
+    layers = [_layer(R, C, 80 + b).to(dev) for b in range(B)]
+    W0 = torch.stack([l.weight.detach().float().cpu() for l in layers])
+    X = _acts(T, C, 81).float()
+    dead = torch.tensor([3, 17, 100, 200, 255])
+    X[:, dead] = 0
+    X = X.bfloat16()
+    gq = GPTQ(layers)
+    q = WeightQuantizer()
+    q.configure(4, perchannel=True, sym=False)
+    gq.quantizer = make_group_quantizers(q, C, 128)
+    st = ohess.gptq_state(B, C)
+    xb = X.reshape(1, T, C)
+    for b in range(B):
+        gq.add_batch(b, xb.to(dev), None)
+        ohess.gptq_add_batch(st, b, xb)
+    gq.fasterquant(groupsize=128, backend="hip")
+    torch.cuda.synchronize()
+    Qd = torch.stack([l.weight.detach().float().cpu() for l in layers])
+    assert torch.all(Qd[:, :, dead] == 0)
+    ref = oflows.gptq_fasterquant(W0, st["H"].clone(), 4, False, groupsize=128)
+    Qr = ref["Q"].bfloat16().float()
+    assert torch.all(Qr[:, :, dead] == 0)
+    assert (Qd == Qr).float().mean().item() >= 0.95
+
+
+def test_nan_hessian_exhausts_the_damp_retry(dev):
+    """gptq_utils.py:288-311: a factor with NaN fails at every damp, the damp
+    climbs by 0.0015 past 1, and fasterquant raises the reference's ValueError."""
+    from g2ptq_amd import GPTQ, WeightQuantizer, make_group_quantizers
+    C = 64
+    layers = [_layer(32, C, 90).to(dev)]
+    gq = GPTQ(layers)
+    q = WeightQuantizer()
+    q.configure(4, perchannel=True, sym=True)
+    gq.quantizer = make_group_quantizers(q, C, -1)
+    H = torch.eye(C).unsqueeze(0).clone()
+    H[0, 5, 7] = H[0, 7, 5] = float("nan")
+    gq.H = H.to(dev)
+    with pytest.raises(ValueError, match="damp_percent"):
+        gq.fasterquant(backend="hip")
