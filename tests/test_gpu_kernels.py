@@ -472,3 +472,28 @@ def test_compensate_far_tail_lookahead_is_bit_identical(dev, variant, groupsize)
         outs.append([t.cpu() for t in (Q, Wi, Sc, W, stab) + ((GH,) if GH is not None else ())])
     for a, b, name in zip(outs[0], outs[1], ("Q", "W_int", "Scale", "W", "scales", "GH")):
         assert torch.equal(a, b), name
+
+
+@pytest.mark.parametrize("K", [64, 128, 1536])
+@pytest.mark.parametrize("b_trans", [0, 1])
+def test_gemm_f32_accuracy_against_fp64(dev, K, b_trans):
+    """The fp32 products (fp32 MFMA below K = 128, the three-way bf16 operand
+    split from K = 128 on) hold fp32 accuracy in the componentwise sense:
+    |D − A·B| ≤ 4e-7 · |A|·|B| elementwise, on operands whose rows and columns
+    span e^±6 in scale; alpha/beta and the C term as the tails use them."""
+    from g2ptq_amd import _lib
+    g = gen(7300 + K + b_trans)
+    M, N = 300, 260
+    A = torch.randn(M, K, generator=g) * torch.exp(2 * torch.randn(M, 1, generator=g))
+    Bm = torch.randn(K, N, generator=g) * torch.exp(2 * torch.randn(1, N, generator=g))
+    Cm = torch.randn(M, N, generator=g)
+    Bx = Bm.t().contiguous() if b_trans else Bm
+    Ad, Bd, Cd = A.to(dev), Bx.to(dev), Cm.to(dev)
+    D = torch.empty(M, N, device=dev)
+    _lib.call("g2ptq_gemm_f32", _lib.stream_ptr(dev), M, N, K, 1, _lib.ptr(Ad), K, 0, _lib.ptr(Bd),
+              Bx.shape[1], 0, b_trans, _lib.ptr(Cd), N, 0, _lib.ptr(D), N, 0, -1.0, 1.0)
+    torch.cuda.synchronize()
+    ref = Cm.double() - A.double() @ Bm.double()
+    bound = A.double().abs() @ Bm.double().abs() + Cm.double().abs()
+    err = ((D.cpu().double() - ref).abs() / bound).max().item()
+    assert err <= 4e-7, err
