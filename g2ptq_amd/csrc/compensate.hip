@@ -2,8 +2,10 @@
 //
 // The block loop stays on the host (it is a dependency chain of kernels);
 // each block is: fit the parameters of groups that start in the block
-// (dynamic groups) → fused sweep (one launch for every row of every layer in
-// the batch) → block-tail update of the remaining columns as fp32 MFMA GEMMs.
+// (dynamic groups; min/max groups that tile the block in 32-column multiples
+// are fitted by the sweep itself) → fused sweep (one launch for every row of
+// every layer in the batch) → block-tail update of the remaining columns as
+// fp32 MFMA GEMMs.
 #include <numeric>
 
 #include "sweep.hpp"
@@ -215,7 +217,11 @@ extern "C" int g2ptq_compensate(void* stream, int variant, int64_t B, int64_t R,
     float* E = Ebuf[sbi & 1];
     for (int64_t i1 = s0; i1 < s1; i1 += bs) {
       const int64_t i2 = std::min(i1 + bs, C), n = i2 - i1;
-      if (dynamic) {
+      // Min/max groups that tile the block in 32-column multiples are fitted
+      // inside the sweep from the same block values.
+      const bool fuse = dynamic && mse_grid == 0 && groupsize % 32 == 0 && bs % groupsize == 0 &&
+                        n % 32 == 0;
+      if (dynamic && !fuse) {
         for (int64_t gs = (i1 + groupsize - 1) / groupsize * groupsize; gs < i2; gs += groupsize) {
           const int64_t gi = gs / groupsize;
           const int64_t width = std::min(groupsize, C - gs);
@@ -243,6 +249,10 @@ extern "C" int g2ptq_compensate(void* stream, int variant, int64_t B, int64_t R,
       a.colgroup = colgroup ? colgroup + i1 : nullptr;
       a.col0 = i1;
       a.gsize = groupsize > 0 ? groupsize : 0;
+      if (fuse) {
+        a.fuse = groupsize; a.sym = sym;
+        a.FS = scale_tab; a.FZ = zero_tab;
+      }
       a.Q = Q + i1; a.qb = RC; a.qr = C; a.qc = 1;
       a.I = Wint ? Wint + i1 : nullptr; a.ib = RC; a.ir = C; a.ic = 1;
       a.Sc = Scale ? Scale + i1 : nullptr; a.cb = RC; a.cr = C; a.cc = 1;

@@ -499,7 +499,7 @@ __device__ __forceinline__ float group_bcast(float v, int o) {
   }
 }
 
-template <int V, int L>
+template <int V, int L, bool F>
 __global__ __launch_bounds__(256) void sweep4_kernel(SweepArgs a) {
   constexpr int PW = 32, RW = 256 / L;  // panel width, rows per workgroup
   constexpr int NS = PW / L;            // panel columns per lane
@@ -594,18 +594,50 @@ __global__ __launch_bounds__(256) void sweep4_kernel(SweepArgs a) {
 
   int bad = 0;
   float last_x = 0.f;
+  float fs = 0.f, fz = 0.f;  // fused group parameters of the current group
 
   for (int p0 = 0; p0 < n; p0 += PW) {
+    if (F && p0 % (int)a.fuse == 0) {
+      // find_params_kernel's fit of the group [p0, p0 + fuse) from the
+      // block's input values (nothing in this kernel writes W): min and max
+      // are exact in any order, NaN is tracked on the side.
+      const int ge = min(p0 + (int)a.fuse, n);
+      float mn = INFINITY, mx = -INFINITY;
+      int nan = 0;
+      for (int j = p0 + sub; j < ge; j += L) {
+        const float v = Win[(int64_t)j * a.wc];
+        nan |= (v != v);
+        mn = fminf(mn, v);
+        mx = fmaxf(mx, v);
+      }
+#pragma unroll
+      for (int o = L / 2; o > 0; o >>= 1) {
+        mn = fminf(mn, __shfl_xor(mn, o, L));
+        mx = fmaxf(mx, __shfl_xor(mx, o, L));
+        nan |= __shfl_xor(nan, o, L);
+      }
+      params_from_minmax(mn, mx, nan != 0, a.maxq, a.sym, fs, fz);
+      if (act && sub == 0) {
+        const int64_t gidx = (a.col0 + p0) / a.gsize;
+        a.FS[b * a.sb + r * a.sr + gidx * a.sg] = fs;
+        a.FZ[b * a.sb + r * a.sr + gidx * a.sg] = fz;
+      }
+    }
     // ---- panel inputs of the lane's NS columns, all issued before any store -
     float w[NS], gh[NS], sv[NS], zv[NS], zg[NS];
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
       const int j = p0 + L * s + sub;
-      int gidx = 0;
-      if (a.colgroup) gidx = a.colgroup[j];
-      else if (a.gsize > 0) gidx = (int)((int)a.col0 + j) / (int)a.gsize;
-      sv[s] = Sp[(int64_t)gidx * a.sg];
-      zv[s] = Zp[(int64_t)gidx * a.sg];
+      if (F) {
+        sv[s] = fs;
+        zv[s] = fz;
+      } else {
+        int gidx = 0;
+        if (a.colgroup) gidx = a.colgroup[j];
+        else if (a.gsize > 0) gidx = (int)((int)a.col0 + j) / (int)a.gsize;
+        sv[s] = Sp[(int64_t)gidx * a.sg];
+        zv[s] = Zp[(int64_t)gidx * a.sg];
+      }
       w[s] = Win[(int64_t)j * a.wc];
       if (V == 2) {
         zg[s] = Zg[(int64_t)j * a.zc];
@@ -769,10 +801,16 @@ void launch_variant(hipStream_t stream, const SweepArgs& a, dim3 grid, bool vec)
     // SIMD (1024 SIMDs), else a quad per row.
     if ((int64_t)grid.y * a.R <= 8192) {
       dim3 g16((unsigned)cdiv(a.R, (int64_t)16), grid.y);
-      hipLaunchKernelGGL((sweep4_kernel<V, 16>), g16, dim3(256), 0, stream, a);
+      if (a.fuse > 0)
+        hipLaunchKernelGGL((sweep4_kernel<V, 16, true>), g16, dim3(256), 0, stream, a);
+      else
+        hipLaunchKernelGGL((sweep4_kernel<V, 16, false>), g16, dim3(256), 0, stream, a);
     } else {
       dim3 g4((unsigned)cdiv(a.R, (int64_t)64), grid.y);
-      hipLaunchKernelGGL((sweep4_kernel<V, 4>), g4, dim3(256), 0, stream, a);
+      if (a.fuse > 0)
+        hipLaunchKernelGGL((sweep4_kernel<V, 4, true>), g4, dim3(256), 0, stream, a);
+      else
+        hipLaunchKernelGGL((sweep4_kernel<V, 4, false>), g4, dim3(256), 0, stream, a);
     }
     return;
   }
@@ -791,6 +829,9 @@ int launch_sweep(hipStream_t stream, int variant, const SweepArgs& a, int64_t B)
               kMaxBlock);
   if (a.R <= 0 || B <= 0) return G2PTQ_OK;
   G2PTQ_CHECK(B < 65536, "block sweep: batch too large");
+  G2PTQ_CHECK(a.fuse == 0 || (a.n % 32 == 0 && a.fuse % 32 == 0 && a.gsize == a.fuse &&
+                              a.col0 % a.fuse == 0 && a.colgroup == nullptr && a.FS && a.FZ),
+              "block sweep: fused group parameters need 32-column panels and aligned groups");
   dim3 grid((unsigned)cdiv(a.R, 64), (unsigned)B);
   const bool vec = sweep_vec_ok(a);
   switch (variant) {

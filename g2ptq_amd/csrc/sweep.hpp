@@ -22,6 +22,13 @@ struct SweepArgs {
   // with group(j) = colgroup[j] if colgroup, else (col0 + j) / gsize (gsize <= 0: 0).
   const float* S; const float* Z0; int64_t sb, sr, sg;
   const int* colgroup; int64_t col0; int64_t gsize;
+  // Fused dynamic-group parameters (fuse > 0): the min/max parameters of each
+  // fuse-wide column group of the block are fitted from the block's input
+  // values at the start of the sweep, written to FS/FZ (the S/Z0 table
+  // layout) and used in place of S/Z0.  Requires fuse % 32 == 0, the block
+  // starting on a group boundary and n % 32 == 0 (the 32-column panel path).
+  int64_t fuse; int sym;
+  float* FS; float* FZ;
   float* Q; int64_t qb, qr, qc;                // dequantized output
   float* I; int64_t ib, ir, ic;                // integer codes (nullable)
   float* E; int64_t eb, er, ec;                // scaled errors (nullable)

@@ -53,7 +53,10 @@ def gptq_loop(weight, hinv, quantizer, groups, blocksize, groupsize, perm):
 
 
 def g2ptq_loop(weight, hinv, z, ghinv, quantizer, groups, blocksize, groupsize, perm):
-    """tests/test_triton_compensation.py:235-310."""
+    """tests/test_triton_compensation.py:235-310.  The tail after the last block
+    is skipped, as the production loop does (gptq_utils/g2ptq_utils.py:324-325):
+    it updates no column, and with a ragged last block the distance vector
+    (blocksize entries) would not match the block's width."""
     batch, rows, columns = weight.shape
     scale = torch.zeros_like(weight)
     int_weight = torch.zeros_like(weight)
@@ -82,6 +85,8 @@ def g2ptq_loop(weight, hinv, z, ghinv, quantizer, groups, blocksize, groupsize, 
         qweight[:, :, i1:i2] = q1
         int_weight[:, :, i1:i2] = n1
         scale[:, :, i1:i2] = s1
+        if i2 == columns:
+            continue
         upd = blocksize * ghinv[:, :, i2:] - torch.bmm(zz * distance.reshape(1, 1, -1),
                                                         hinv[:, i1:i2, i2:])
         weight[:, :, i2:] -= torch.bmm(e1, hinv[:, i1:i2, i2:]) + upd

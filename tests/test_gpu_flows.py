@@ -50,8 +50,14 @@ def _prepare_loop_quantizers(weight, bits, symmetric, groupsize, static_groups):
     return oorig, ogroups, cur
 
 
-CONFIGS = (("ungrouped", -1, False, False), ("dynamic_groups", 4, False, False),
-           ("static_groups_actorder", 4, True, True))
+# (name, groupsize, static_groups, actorder, (rows, columns, blocksize)).  The
+# "fitted_in_sweep" cases have min/max groups that tile 32-column panels, which
+# the sweep fits itself (the last block and its last group ragged in the first).
+CONFIGS = (("ungrouped", -1, False, False, (37, 15, 5)),
+           ("dynamic_groups", 4, False, False, (37, 15, 5)),
+           ("static_groups_actorder", 4, True, True, (37, 15, 5)),
+           ("dynamic_groups_fitted_in_sweep", 64, False, False, (37, 224, 128)),
+           ("dynamic_groups32_fitted_in_sweep", 32, False, False, (21, 192, 64)))
 
 
 @pytest.mark.parametrize("cfg", CONFIGS, ids=[c[0] for c in CONFIGS])
@@ -59,8 +65,9 @@ CONFIGS = (("ungrouped", -1, False, False), ("dynamic_groups", 4, False, False),
 def test_compensation_matches_original_loops(dev, cfg, symmetric):
     """tests/test_triton_compensation.py:581-772 with the HIP loop in place of torch."""
     from g2ptq_amd import G2PTQ, GPTAQ, GPTQ, GPTQGuided
-    name, groupsize, static_groups, actorder = cfg
-    batch, rows, columns, blocksize, bits = 2, 37, 15, 5, 4
+    name, groupsize, static_groups, actorder, (rows, columns, blocksize) = cfg
+    batch, bits = 2, 4
+    print(f"compensation case {name} sym={symmetric}", flush=True)
     g = gen(8000 + CONFIGS.index(cfg) * 100 + int(symmetric))
     original = torch.randn(batch, rows, columns, generator=g)
     perm = None
