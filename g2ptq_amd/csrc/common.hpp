@@ -100,15 +100,18 @@ struct GemmF32 {
 
 int gemm_f32(hipStream_t stream, const GemmF32& g);
 
-// A second stream (default priority) and events per device, created once and
-// kept, for the lookahead of the factor (the trailing updates) and of the
-// compensation loop (the far block tails).  Calls that overlap on one device
-// would share them: the library's entry points are not meant to run
-// concurrently on one device.
+// Two more streams (default priority) and events per device, created once
+// and kept, for the lookahead of the factor (the trailing updates on
+// `stream`, the triangular inverse's block rows on `stream2`) and of the
+// compensation loop (the far block tails on `stream`).  Calls that overlap
+// on one device would share them: the library's entry points are not meant
+// to run concurrently on one device.
 struct SideStream {
   hipStream_t stream = nullptr;
+  hipStream_t stream2 = nullptr;
   hipEvent_t factored = nullptr;                // factor: panel done, on the main stream
   hipEvent_t done[2] = {nullptr, nullptr};      // factor: trailing updates done, on the side
+  hipEvent_t inverted = nullptr;                // factor: inverse block rows done (stream2)
   hipEvent_t swept = nullptr;                   // compensation: a super-block swept (main)
   hipEvent_t tailed = nullptr;                  // compensation: its far tail applied (side)
 };

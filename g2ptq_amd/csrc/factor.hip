@@ -7,15 +7,16 @@
 // index order: one Cholesky plus one triangular inverse (2C³/3).
 //
 //   1. reverse-copy Â = J(H + damp·I)J (lower triangle) into the workspace
-//   2. blocked right-looking Cholesky of Â in panels of NBO = 256 columns,
+//   2. blocked right-looking Cholesky of Â in panels of NBO = 512 columns,
 //      each factored NB = 64 columns at a time: potrf of the diagonal block
 //      in one workgroup (registers), which also inverts it in place;  TRSM
 //      as a GEMM with that inverse;  update of the panel's remaining
-//      columns;  then one SYRK trailing update per panel (K = 256) as a
+//      columns;  then one SYRK trailing update per panel (K = 512) as a
 //      lower-triangular fp32 MFMA GEMM
-//   3. triangular inverse by recursive doubling: diagonal blocks are already
-//      inverted; level s joins pairs of s-sized inverses with
-//      X21 = −X22·(L21·X11), each level two batched GEMMs
+//   3. the triangular inverse X = L̂⁻¹ panel by panel, as soon as each is
+//      factored, on a third stream beside the Cholesky: the diagonal block
+//      by recursive doubling from the NB inverses, then the block row
+//      X[p, 0:p] = −X_pp·(L[p, 0:p]·X[0:p, 0:p]) as two GEMMs
 //   4. un-reverse into U (upper, zeros below) with the reference's NaN check.
 #include <mutex>
 
@@ -27,6 +28,7 @@ namespace {
 
 constexpr int NB = 64;   // diagonal block width (potrf in registers)
 constexpr int NBO = 512; // panel width of the trailing (SYRK) updates
+constexpr int64_t SYRK_CHUNK = 2048;  // columns per launch of the far trailing update
 
 __global__ void diag_sum_kernel(const float* __restrict__ H, int64_t C, const int* skip,
                                 float* sums, int* st, int* info) {
@@ -150,18 +152,19 @@ __global__ void unreverse_kernel(const float* __restrict__ WA, int64_t C, const 
 }
 
 struct FactorWs {
-  size_t wa, wt, sums, st, total;
+  size_t wa, wt, ti, sums, st, total;
 };
 
 FactorWs factor_ws(int64_t B, int64_t C) {
   FactorWs w;
   auto al = [](size_t x) { return (x + 255) / 256 * 256; };
   w.wa = al((size_t)B * C * C * 4);
-  const int64_t half = (C + 1) / 2;
-  w.wt = al((size_t)B * half * half * 4 + 4);
+  const int64_t half = std::min<int64_t>((C + 1) / 2, NBO);
+  w.wt = al((size_t)B * half * half * 4 + 4);        // in-panel inverse products
+  w.ti = al((size_t)B * NBO * C * 4 + 4);            // inverse block-row products
   w.sums = al((size_t)B * 4);
   w.st = al((size_t)B * 4);
-  w.total = w.wa + w.wt + w.sums + w.st;
+  w.total = w.wa + w.wt + w.ti + w.sums + w.st;
   return w;
 }
 
@@ -177,7 +180,8 @@ int side_stream(SideStream& out) {
   SideStream& c = cache[dev];
   if (c.stream == nullptr) {
     G2PTQ_HIP(hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking));
-    for (hipEvent_t* e : {&c.factored, &c.done[0], &c.done[1], &c.swept, &c.tailed})
+    G2PTQ_HIP(hipStreamCreateWithFlags(&c.stream2, hipStreamNonBlocking));
+    for (hipEvent_t* e : {&c.factored, &c.done[0], &c.done[1], &c.inverted, &c.swept, &c.tailed})
       G2PTQ_HIP(hipEventCreateWithFlags(e, hipEventDisableTiming));
   }
   out = c;
@@ -206,8 +210,9 @@ extern "C" int g2ptq_inv_chol_upper(void* stream, const float* H, int64_t B, int
   char* base = static_cast<char*>(ws);
   float* WA = reinterpret_cast<float*>(base);
   float* WT = reinterpret_cast<float*>(base + w.wa);
-  float* sums = reinterpret_cast<float*>(base + w.wa + w.wt);
-  int* st = reinterpret_cast<int*>(base + w.wa + w.wt + w.sums);
+  float* TI = reinterpret_cast<float*>(base + w.wa + w.wt);
+  float* sums = reinterpret_cast<float*>(base + w.wa + w.wt + w.ti);
+  int* st = reinterpret_cast<int*>(base + w.wa + w.wt + w.ti + w.sums);
   const int64_t CC = C * C;
 
   hipLaunchKernelGGL(diag_sum_kernel, dim3((unsigned)B), dim3(256), 0, s, H, C, skip, sums, st,
@@ -217,16 +222,68 @@ extern "C" int g2ptq_inv_chol_upper(void* stream, const float* H, int64_t B, int
   hipLaunchKernelGGL(reverse_damp_kernel, cgrid, dim3(256), 0, s, H, C, percdamp, sums, st, WA);
   G2PTQ_LAUNCHED();
 
+  // Triangular inverse by recursive doubling over rows/columns [i_base,
+  // i_base + n) of Â, whose diagonal blocks of size sz_from are already
+  // inverted in place: level sz joins pairs of sz-sized inverses with
+  // X21 = −X22·(L21·X11) (two batched GEMMs on stream q), up to blocks of
+  // size >= sz_to.
+  auto trtri_levels = [&](hipStream_t q, int64_t i_base, int64_t n, int64_t sz_from,
+                          int64_t sz_to) -> int {
+    for (int64_t sz = sz_from; sz < n && sz < sz_to; sz *= 2) {
+      const int64_t full = n / (2 * sz);             // pairs with a full second block
+      const int64_t tail_i = full * 2 * sz;          // start of a possible ragged pair
+      const int64_t tail_n2 = n - tail_i - sz;       // its second block size (if > 0)
+      for (int part = 0; part < 2; ++part) {
+        int64_t npairs, i0, n2;
+        if (part == 0) {
+          npairs = full; i0 = i_base; n2 = sz;
+        } else {
+          npairs = tail_n2 > 0 ? 1 : 0; i0 = i_base + tail_i; n2 = tail_n2;
+        }
+        if (npairs == 0) continue;
+        const int64_t pstride = 2 * sz * (C + 1);
+        GemmF32 t;  // T = L21 · X11
+        t.M = n2; t.N = sz; t.K = sz; t.batch = B; t.batch2 = npairs;
+        t.A = WA + (i0 + sz) * C + i0; t.lda = C; t.sA = CC; t.sA2 = pstride;
+        t.B = WA + i0 * C + i0; t.ldb = C; t.sB = CC; t.sB2 = pstride;
+        t.D = WT; t.ldd = sz; t.sD = npairs * n2 * sz; t.sD2 = n2 * sz;
+        t.tri = 2;  // X11 is lower triangular
+        t.skip = st;
+        G2PTQ_TRY(gemm_f32(q, t));
+        GemmF32 x;  // X21 = −X22 · T
+        x.M = n2; x.N = sz; x.K = n2; x.batch = B; x.batch2 = npairs;
+        x.A = WA + (i0 + sz) * C + (i0 + sz); x.lda = C; x.sA = CC; x.sA2 = pstride;
+        x.B = WT; x.ldb = sz; x.sB = npairs * n2 * sz; x.sB2 = n2 * sz;
+        x.D = WA + (i0 + sz) * C + i0; x.ldd = C; x.sD = CC; x.sD2 = pstride;
+        x.alpha = -1.f; x.tri = 1;  // X22 is lower triangular
+        x.skip = st;
+        G2PTQ_TRY(gemm_f32(q, x));
+      }
+    }
+    return G2PTQ_OK;
+  };
+
   // Blocked Cholesky of Â (lower) with inverted diagonal blocks, two levels:
   // panels of NBO columns are factored NB columns at a time (potrf + TRSM +
   // update of the panel's own remaining columns), and the trailing matrix
   // receives each whole panel in one SYRK with K = NBO.  Lookahead of one
   // panel: the trailing update beyond the next panel runs on a second stream
   // while the next panel (updated first, on the caller's stream) is factored,
-  // so the latency-bound panel chain overlaps the bandwidth/MFMA-bound SYRK.
-  // The first diagonal block of a panel is factored by potrf_diag_kernel; every
-  // later one by the panel-remainder update that produces it (its top-left
+  // so the latency-bound panel chain overlaps the MFMA-bound SYRK.  The first
+  // diagonal block of a panel is factored by potrf_diag_kernel; every later
+  // one by the panel-remainder update that produces it (its top-left
   // workgroup factors the block in LDS right after computing it).
+  // Once a panel is factored, a third stream inverts it into X = L̂⁻¹:
+  //   the panel's diagonal block (recursive doubling from the NB inverses,
+  //   in place), then, in block-row order so that X[0:k, 0:k] is final,
+  //   TI = L[k:kend, 0:k] · X[0:k, 0:k];  X[k:kend, 0:k] = −X_kk · TI,
+  //   written over L[k:kend, 0:k].
+  // The Cholesky reads neither the diagonal block nor the block row again:
+  // the trailing updates that read the block row completed before the panel
+  // was factored, and those of the panel itself read only the rows below it.
+  SideStream side;
+  G2PTQ_TRY(side_stream(side));
+  bool inv_pending = false;  // inverse work queued on stream2
   auto factor_panel = [&](int64_t k, int64_t kb) -> int {
     bool fused = false;
     for (int64_t j = k; j < k + kb; j += NB) {
@@ -260,10 +317,32 @@ extern "C" int g2ptq_inv_chol_upper(void* stream, const float* H, int64_t B, int
       G2PTQ_TRY(gemm_f32(s, y));
       fused = true;
     }
+    G2PTQ_HIP(hipEventRecord(side.factored, s));
+    G2PTQ_HIP(hipStreamWaitEvent(side.stream2, side.factored, 0));
+    inv_pending = true;
+    G2PTQ_TRY(trtri_levels(side.stream2, k, kb, NB, NBO));
+    if (k > 0) {
+      GemmF32 t;
+      t.M = kb; t.N = k; t.K = k; t.batch = B;
+      t.A = WA + k * C; t.lda = C; t.sA = CC;
+      t.B = WA; t.ldb = C; t.sB = CC;
+      t.D = TI; t.ldd = C; t.sD = NBO * C;
+      t.tri = 2;  // X lower triangular
+      t.skip = st;
+      G2PTQ_TRY(gemm_f32(side.stream2, t));
+      GemmF32 x;
+      x.M = kb; x.N = k; x.K = kb; x.batch = B;
+      x.A = WA + k * C + k; x.lda = C; x.sA = CC;
+      x.B = TI; x.ldb = C; x.sB = NBO * C;
+      x.D = WA + k * C; x.ldd = C; x.sD = CC;
+      x.alpha = -1.f; x.tri = 1;  // X_kk lower triangular
+      x.skip = st;
+      G2PTQ_TRY(gemm_f32(side.stream2, x));
+    }
     return G2PTQ_OK;
   };
   // Rows [c0, C) × columns [c0, c1) (lower part) −= panel [k, k + kb) contribution.
-  auto syrk = [&](hipStream_t q, int64_t k, int64_t kb, int64_t c0, int64_t c1) -> int {
+  auto syrk1 = [&](hipStream_t q, int64_t k, int64_t kb, int64_t c0, int64_t c1) -> int {
     GemmF32 y;
     y.M = C - c0; y.N = c1 - c0; y.K = kb; y.batch = B;
     y.A = WA + c0 * C + k; y.lda = C; y.sA = CC;
@@ -273,8 +352,16 @@ extern "C" int g2ptq_inv_chol_upper(void* stream, const float* H, int64_t B, int
     y.alpha = -1.f; y.beta = 1.f; y.uplo = 1; y.skip = st;
     return gemm_f32(q, y);
   };
-  SideStream side;
-  G2PTQ_TRY(side_stream(side));
+  // The far trailing update goes out as launches of SYRK_CHUNK columns: the
+  // panel chain's kernels on the caller's stream then wait behind one chunk
+  // rather than the whole update (the hardware dispatches a queue's kernels
+  // in order).
+  auto syrk = [&](hipStream_t q, int64_t k, int64_t kb, int64_t c0, int64_t c1) -> int {
+    if (q == s) return syrk1(q, k, kb, c0, c1);
+    for (int64_t c = c0; c < c1; c += SYRK_CHUNK)
+      G2PTQ_TRY(syrk1(q, k, kb, c, std::min(c1, c + SYRK_CHUNK)));
+    return G2PTQ_OK;
+  };
   G2PTQ_TRY(factor_panel(0, std::min<int64_t>(NBO, C)));
   int pend = -1;  // ping-pong slot of the latest trailing update on the side stream
   for (int64_t k = 0, p = 0; k < C; k += NBO, ++p) {
@@ -300,37 +387,9 @@ extern "C" int g2ptq_inv_chol_upper(void* stream, const float* H, int64_t B, int
   }
   if (pend >= 0) G2PTQ_HIP(hipStreamWaitEvent(s, side.done[pend], 0));
 
-  // Triangular inverse by recursive doubling (diagonal NB blocks already inverted).
-  for (int64_t sz = NB; sz < C; sz *= 2) {
-    const int64_t full = C / (2 * sz);             // pairs with a full second block
-    const int64_t tail_i = full * 2 * sz;          // start of a possible ragged pair
-    const int64_t tail_n2 = C - tail_i - sz;       // its second block size (if > 0)
-    for (int part = 0; part < 2; ++part) {
-      int64_t npairs, i0, n2;
-      if (part == 0) {
-        npairs = full; i0 = 0; n2 = sz;
-      } else {
-        npairs = tail_n2 > 0 ? 1 : 0; i0 = tail_i; n2 = tail_n2;
-      }
-      if (npairs == 0) continue;
-      const int64_t pstride = 2 * sz * (C + 1);
-      GemmF32 t;  // T = L21 · X11
-      t.M = n2; t.N = sz; t.K = sz; t.batch = B; t.batch2 = npairs;
-      t.A = WA + (i0 + sz) * C + i0; t.lda = C; t.sA = CC; t.sA2 = pstride;
-      t.B = WA + i0 * C + i0; t.ldb = C; t.sB = CC; t.sB2 = pstride;
-      t.D = WT; t.ldd = sz; t.sD = npairs * n2 * sz; t.sD2 = n2 * sz;
-      t.tri = 2;  // X11 is lower triangular
-      t.skip = st;
-      G2PTQ_TRY(gemm_f32(s, t));
-      GemmF32 x;  // X21 = −X22 · T
-      x.M = n2; x.N = sz; x.K = n2; x.batch = B; x.batch2 = npairs;
-      x.A = WA + (i0 + sz) * C + (i0 + sz); x.lda = C; x.sA = CC; x.sA2 = pstride;
-      x.B = WT; x.ldb = sz; x.sB = npairs * n2 * sz; x.sB2 = n2 * sz;
-      x.D = WA + (i0 + sz) * C + i0; x.ldd = C; x.sD = CC; x.sD2 = pstride;
-      x.alpha = -1.f; x.tri = 1;  // X22 is lower triangular
-      x.skip = st;
-      G2PTQ_TRY(gemm_f32(s, x));
-    }
+  if (inv_pending) {
+    G2PTQ_HIP(hipEventRecord(side.inverted, side.stream2));
+    G2PTQ_HIP(hipStreamWaitEvent(s, side.inverted, 0));
   }
 
   hipLaunchKernelGGL(unreverse_kernel, cgrid, dim3(256), 0, s, WA, C, skip, info, U);
