@@ -503,8 +503,10 @@ template <int V, int L, bool F>
 __global__ __launch_bounds__(256) void sweep4_kernel(SweepArgs a) {
   constexpr int PW = 32, RW = 256 / L;  // panel width, rows per workgroup
   constexpr int NS = PW / L;            // panel columns per lane
-  __shared__ float Us[kTri];
-  __shared__ float Ps[(V == 1) ? kTri : 1];
+  // The triangles plus one spare word per lane (the full-block staging's
+  // sink for entries left of the diagonal).
+  __shared__ float Us[kTri + 64];
+  __shared__ float Ps[(V == 1) ? kTri + 64 : 1];
   __shared__ float e_s[kMaxBlock * RW];
   __shared__ float t_s[(V == 1) ? kMaxBlock * RW : 1];
   __shared__ float z_s[(V == 2) ? kMaxBlock * RW : 1];
@@ -528,45 +530,74 @@ __global__ __launch_bounds__(256) void sweep4_kernel(SweepArgs a) {
     const int total = n * nc;
     const bool vec = ((a.uj & 3) == 0) && ((reinterpret_cast<uintptr_t>(U) & 15) == 0) &&
                      (V != 1 || (reinterpret_cast<uintptr_t>(P) & 15) == 0);
-    for (int base = 0; base < total; base += 256 * 16) {
+    if (n == kMaxBlock && vec) {
+      // Full block: chunk q of thread tid is row j = 8q + tid/32, columns
+      // k..k+3 = 4·(tid % 32), all in bounds (entries left of the diagonal
+      // are U's zeros); those entries are stored to the thread's spare word
+      // instead of branching around the store.
+      static_assert(kMaxBlock == 128, "full-block staging covers 128 rows in 16 chunks of 8");
       float4 uv[16], pv[16];
 #pragma unroll
       for (int q = 0; q < 16; ++q) {
-        const int idx = base + q * 256 + tid;
-        const int j = idx / nc, k = (idx - j * nc) * 4;
-        float4 u = make_float4(0.f, 0.f, 0.f, 0.f), pp = u;
-        if (idx < total && k + 3 >= j) {
-          const float* pu = U + (int64_t)j * a.uj + k;
-          const float* ppp = (V == 1) ? P + (int64_t)j * a.uj + k : nullptr;
-          if (vec && k + 3 < n) {
-            u = *reinterpret_cast<const float4*>(pu);
-            if (V == 1) pp = *reinterpret_cast<const float4*>(ppp);
-          } else {
-            if (k >= j && k < n) { u.x = pu[0]; if (V == 1) pp.x = ppp[0]; }
-            if (k + 1 >= j && k + 1 < n) { u.y = pu[1]; if (V == 1) pp.y = ppp[1]; }
-            if (k + 2 >= j && k + 2 < n) { u.z = pu[2]; if (V == 1) pp.z = ppp[2]; }
-            if (k + 3 >= j && k + 3 < n) { u.w = pu[3]; if (V == 1) pp.w = ppp[3]; }
-          }
-        }
-        uv[q] = u;
-        if (V == 1) pv[q] = pp;
+        const int j = q * 8 + (tid >> 5), k = (tid & 31) * 4;
+        uv[q] = *reinterpret_cast<const float4*>(U + (int64_t)j * a.uj + k);
+        if (V == 1) pv[q] = *reinterpret_cast<const float4*>(P + (int64_t)j * a.uj + k);
       }
+      const int sink = kTri + (tid & 63);
 #pragma unroll
       for (int q = 0; q < 16; ++q) {
-        const int idx = base + q * 256 + tid;
-        const int j = idx / nc, k = (idx - j * nc) * 4;
-        if (idx >= total) continue;
-        const int t0 = tri_base(j, n);
+        const int j = q * 8 + (tid >> 5), k = (tid & 31) * 4;
+        const int t0 = tri_base(j, kMaxBlock);
         const float ue[4] = {uv[q].x, uv[q].y, uv[q].z, uv[q].w};
+        const float pe[4] = {pv[q].x, pv[q].y, pv[q].z, pv[q].w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          if (k + e >= j && k + e < n) Us[t0 + k + e] = ue[e];
+          const int at = (k + e >= j) ? t0 + k + e : sink;
+          Us[at] = ue[e];
+          if (V == 1) Ps[at] = pe[e];
         }
-        if (V == 1) {
-          const float pe[4] = {pv[q].x, pv[q].y, pv[q].z, pv[q].w};
+      }
+    } else {
+      for (int base = 0; base < total; base += 256 * 16) {
+        float4 uv[16], pv[16];
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+          const int idx = base + q * 256 + tid;
+          const int j = idx / nc, k = (idx - j * nc) * 4;
+          float4 u = make_float4(0.f, 0.f, 0.f, 0.f), pp = u;
+          if (idx < total && k + 3 >= j) {
+            const float* pu = U + (int64_t)j * a.uj + k;
+            const float* ppp = (V == 1) ? P + (int64_t)j * a.uj + k : nullptr;
+            if (vec && k + 3 < n) {
+              u = *reinterpret_cast<const float4*>(pu);
+              if (V == 1) pp = *reinterpret_cast<const float4*>(ppp);
+            } else {
+              if (k >= j && k < n) { u.x = pu[0]; if (V == 1) pp.x = ppp[0]; }
+              if (k + 1 >= j && k + 1 < n) { u.y = pu[1]; if (V == 1) pp.y = ppp[1]; }
+              if (k + 2 >= j && k + 2 < n) { u.z = pu[2]; if (V == 1) pp.z = ppp[2]; }
+              if (k + 3 >= j && k + 3 < n) { u.w = pu[3]; if (V == 1) pp.w = ppp[3]; }
+            }
+          }
+          uv[q] = u;
+          if (V == 1) pv[q] = pp;
+        }
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+          const int idx = base + q * 256 + tid;
+          const int j = idx / nc, k = (idx - j * nc) * 4;
+          if (idx >= total) continue;
+          const int t0 = tri_base(j, n);
+          const float ue[4] = {uv[q].x, uv[q].y, uv[q].z, uv[q].w};
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            if (k + e >= j && k + e < n) Ps[t0 + k + e] = pe[e];
+            if (k + e >= j && k + e < n) Us[t0 + k + e] = ue[e];
+          }
+          if (V == 1) {
+            const float pe[4] = {pv[q].x, pv[q].y, pv[q].z, pv[q].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              if (k + e >= j && k + e < n) Ps[t0 + k + e] = pe[e];
+            }
           }
         }
       }
