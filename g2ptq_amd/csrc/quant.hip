@@ -678,17 +678,22 @@ __global__ __launch_bounds__(256) void sweep4_kernel(SweepArgs a) {
     // ---- replay updates of the columns swept in earlier panels (LDS only) ---
     // Eight columns at a time: their LDS operands are all read before the
     // updates, which then run in the reference's column order.
-    for (int j0 = 0; j0 < p0; j0 += 8) {
-      constexpr int RB = 8;
+    // Sixteen columns at a time where the registers allow (16 lanes per row,
+    // no P), so fewer LDS round trips stay exposed; row j + 1 of the packed
+    // triangle starts n − j − 1 entries after row j.
+    constexpr int RB = (L == 16 && V != 1) ? 16 : 8;
+    for (int j0 = 0; j0 < p0; j0 += RB) {
       float e[RB], t[RB], zj[RB], u[RB][NS], pu[RB][NS];
+      const int row0 = tri_base(j0, n) + p0 + sub, step = n - j0 - 1;
 #pragma unroll
       for (int q = 0; q < RB; ++q) {
         const int j = j0 + q;
         e[q] = e_s[j * RW + rr];
         if (V == 1) t[q] = t_s[j * RW + rr];
         if (V == 2) zj[q] = z_s[j * RW + rr];
-        const float* Uj = Us + tri_base(j, n) + p0 + sub;
-        const float* Pj = (V == 1) ? Ps + tri_base(j, n) + p0 + sub : nullptr;
+        const int off = row0 + q * step - q * (q - 1) / 2;  // tri_base(j, n) + p0 + sub
+        const float* Uj = Us + off;
+        const float* Pj = (V == 1) ? Ps + off : nullptr;
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
           u[q][s] = Uj[L * s];
