@@ -117,7 +117,7 @@ def prepare_hessian(H, W, Dx=None, Grad=None):
     B, C, _ = H.shape
     R = W.shape[1]
     Rg = Grad.shape[1] if Grad is not None else 0
-    nbytes = (B * 4 + 255) // 256 * 256 + (B * C * 4 + 255) // 256 * 256
+    nbytes = (B * 8 + 255) // 256 * 256 + (B * C * 4 + 255) // 256 * 256
     ws = _lib.workspace(nbytes, H.device)
     _lib.call("g2ptq_prepare_hessian", stream(), _lib.ptr(H), B, C, _lib.ptr(W), R, _lib.ptr(Dx),
               _lib.ptr(Grad), Rg, _lib.ptr(ws), ws.numel())

@@ -26,9 +26,24 @@ __global__ void fill_kernel(float* p, int64_t n, float v) {
     p[i] = v;
 }
 
-// nz[b] = any(H[b] != 0)   (NaN counts as nonzero, like `(H == 0).all()` being False).
+// nz[b] |= any(diag H[b] != 0): a nonzero diagonal entry settles the test
+// below without reading the rest (every real Hessian has one).
+__global__ void nonzero_diag_kernel(const float* __restrict__ H, int64_t C, int* nz) {
+  const int64_t b = blockIdx.y;
+  const float* Hb = H + b * C * C;
+  int any = 0;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < C;
+       i += (int64_t)gridDim.x * blockDim.x)
+    any |= !(Hb[i * C + i] == 0.f);
+  any = __any(any);
+  if (any && (threadIdx.x & 63) == 0) atomicOr(&nz[b], 1);
+}
+
+// nz[b] = any(H[b] != 0)   (NaN counts as nonzero, like `(H == 0).all()` being False);
+// only layers whose diagonal is all zero are scanned.
 __global__ void nonzero_kernel(const float* __restrict__ H, int64_t CC, int* nz) {
   const int64_t b = blockIdx.y;
+  if (nz[b]) return;  // settled by the diagonal (or another workgroup)
   const float* Hb = H + b * CC;
   int any = 0;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < CC;
@@ -38,35 +53,41 @@ __global__ void nonzero_kernel(const float* __restrict__ H, int64_t CC, int* nz)
   if (any && (threadIdx.x & 63) == 0) atomicOr(&nz[b], 1);
 }
 
-__global__ void dead_kernel(const float* __restrict__ H, int64_t C, const int* nz, int* dead) {
+// dead[b][i] = H[b] nonzero and H[b][i][i] == 0; anydead[b] = any of them.
+__global__ void dead_kernel(const float* __restrict__ H, int64_t C, const int* nz, int* dead,
+                            int* anydead) {
   const int64_t b = blockIdx.y;
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= C) return;
-  dead[b * C + i] = nz[b] && (H[b * C * C + i * C + i] == 0.f);
+  const int d = nz[b] && (H[b * C * C + i * C + i] == 0.f);
+  dead[b * C + i] = d;
+  if (d) atomicOr(&anydead[b], 1);
 }
 
+// An all-zero H[b] becomes the identity; otherwise only dead diagonal entries
+// change (to 1), so only the diagonal is visited.
 __global__ void fix_h_kernel(float* H, int64_t C, const int* nz, const int* dead) {
   const int64_t b = blockIdx.y;
   const int64_t CC = C * C;
   float* Hb = H + b * CC;
-  const bool zero = !nz[b];
-  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < CC;
-       e += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t i = e / C, j = e % C;
-    if (zero)
-      Hb[e] = (i == j) ? 1.f : 0.f;
-    else if (i == j && dead[b * C + i])
-      Hb[e] = 1.f;
+  const int64_t t0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  if (!nz[b]) {
+    for (int64_t e = t0; e < CC; e += stride) Hb[e] = (e % (C + 1) == 0) ? 1.f : 0.f;
+  } else {
+    for (int64_t i = t0; i < C; i += stride)
+      if (dead[b * C + i]) Hb[i * C + i] = 1.f;
   }
 }
 
 // Zero dead columns of a (B, rows, C) matrix; optionally zero whole entries whose H was zero.
 __global__ void zero_cols_kernel(float* M, int64_t rows, int64_t C, const int* dead, const int* nz,
-                                 int zero_if_h_zero) {
+                                 const int* anydead, int zero_if_h_zero) {
   const int64_t b = blockIdx.y;
   const int64_t n = rows * C;
   float* Mb = M + b * n;
   const bool wipe = zero_if_h_zero && !nz[b];
+  if (!wipe && !anydead[b]) return;  // nothing to zero in this layer
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n;
        e += (int64_t)gridDim.x * blockDim.x) {
     if (wipe || dead[b * C + (e % C)]) Mb[e] = 0.f;
@@ -204,35 +225,39 @@ extern "C" int g2ptq_prepare_hessian(void* stream, float* H, int64_t B, int64_t 
                                      size_t ws_bytes) {
   G2PTQ_CHECK(H && W, "prepare_hessian: null pointer");
   G2PTQ_CHECK(B >= 1 && B < 65536 && C >= 1, "prepare_hessian: bad sizes");
-  const size_t need = al256((size_t)B * 4) + al256((size_t)B * C * 4);
+  const size_t need = al256((size_t)B * 8) + al256((size_t)B * C * 4);
   G2PTQ_CHECK(ws && ws_bytes >= need, "prepare_hessian: workspace %zu < %zu", ws_bytes, need);
   hipStream_t s = as_stream(stream);
-  int* nz = static_cast<int*>(ws);
-  int* dead = reinterpret_cast<int*>(static_cast<char*>(ws) + al256((size_t)B * 4));
-  // Counters start at zero: cleared by a kernel so the call can be graph-captured.
-  G2PTQ_TRY(fill_f32(s, reinterpret_cast<float*>(nz), B, 0.f));
+  int* nz = static_cast<int*>(ws);  // B flags, then B "any dead column" flags
+  int* anydead = nz + B;
+  int* dead = reinterpret_cast<int*>(static_cast<char*>(ws) + al256((size_t)B * 8));
+  // Flags start at zero: cleared by a kernel so the call can be graph-captured.
+  G2PTQ_TRY(fill_f32(s, reinterpret_cast<float*>(nz), 2 * B, 0.f));
   const int64_t CC = C * C;
+  hipLaunchKernelGGL(nonzero_diag_kernel, dim3((unsigned)std::min<int64_t>(cdiv(C, 256), 64), (unsigned)B),
+                     dim3(256), 0, s, H, C, nz);
+  G2PTQ_LAUNCHED();
   hipLaunchKernelGGL(nonzero_kernel, dim3(std::min<unsigned>(grid_for(CC), 1024), (unsigned)B),
                      dim3(256), 0, s, H, CC, nz);
   G2PTQ_LAUNCHED();
   hipLaunchKernelGGL(dead_kernel, dim3((unsigned)cdiv(C, 256), (unsigned)B), dim3(256), 0, s, H,
-                     C, nz, dead);
+                     C, nz, dead, anydead);
   G2PTQ_LAUNCHED();
   hipLaunchKernelGGL(fix_h_kernel, dim3(std::min<unsigned>(grid_for(CC), 4096), (unsigned)B),
                      dim3(256), 0, s, H, C, nz, dead);
   G2PTQ_LAUNCHED();
   hipLaunchKernelGGL(zero_cols_kernel, dim3(std::min<unsigned>(grid_for(R * C), 4096), (unsigned)B),
-                     dim3(256), 0, s, W, R, C, dead, nz, 0);
+                     dim3(256), 0, s, W, R, C, dead, nz, anydead, 0);
   G2PTQ_LAUNCHED();
   if (Dx) {
     hipLaunchKernelGGL(zero_cols_kernel, dim3(std::min<unsigned>(grid_for(CC), 4096), (unsigned)B),
-                       dim3(256), 0, s, Dx, C, C, dead, nz, 0);
+                       dim3(256), 0, s, Dx, C, C, dead, nz, anydead, 0);
     G2PTQ_LAUNCHED();
   }
   if (Grad) {
     hipLaunchKernelGGL(zero_cols_kernel,
                        dim3(std::min<unsigned>(grid_for(Rg * C), 4096), (unsigned)B), dim3(256), 0,
-                       s, Grad, Rg, C, dead, nz, 1);
+                       s, Grad, Rg, C, dead, nz, anydead, 1);
     G2PTQ_LAUNCHED();
   }
   return G2PTQ_OK;

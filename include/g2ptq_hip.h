@@ -171,7 +171,8 @@ int g2ptq_weighted_gram(void* stream, uint16_t* XT, int64_t ldt, int64_t K, int6
  * identity, a zero diagonal entry d becomes 1 and column d of W[b] (and of
  * Dx[b], nullable) is zeroed; where H[b] was all zero, Grad[b] (B × Rg × C,
  * nullable) is zeroed.  Replaces gptq_utils/gptq_utils.py:272-277,
- * gptaq_utils.py:302-308, g2ptq_utils.py:394-401. */
+ * gptaq_utils.py:302-308, g2ptq_utils.py:394-401.  ws: at least
+ * 256·⌈8B/256⌉ + 256·⌈4BC/256⌉ bytes. */
 int g2ptq_prepare_hessian(void* stream, float* H, int64_t B, int64_t C, float* W, int64_t R,
                           float* Dx, float* Grad, int64_t Rg, void* ws, size_t ws_bytes);
 
