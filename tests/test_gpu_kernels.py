@@ -390,9 +390,14 @@ def test_weighted_hessian_matches_oracle(dev):
     assert_close(act, st["act_square"][0], rtol=1e-5, atol=1e-6, what="act_square")
 
 
-@pytest.mark.parametrize("C,B", [(15, 2), (128, 1), (300, 2), (700, 1)])
+# 2600 and 3200: several 512-column panels (ragged last ones), so the
+# triangular inverse's block rows on their own stream read earlier block rows,
+# and at 3200 the trailing update beyond the next panel goes out in two
+# 2048-column launches.
+@pytest.mark.parametrize("C,B", [(15, 2), (128, 1), (300, 2), (700, 1), (2600, 2), (3200, 1)])
 def test_factor_matches_fp64(dev, C, B):
     from g2ptq_amd import _core
+    print(f"factor accuracy C={C} B={B}", flush=True)
     g = gen(C)
     X = torch.randn(4 * C, C, generator=g) * torch.exp(0.5 * torch.randn(C, generator=g))
     H = torch.stack([(2 / X.shape[0]) * (X.T @ X) * (1 + 0.1 * b) for b in range(B)])
@@ -428,6 +433,46 @@ def test_factor_damp_retry(dev):
     Uo, d_ref = ofactor.damp_chol_inv_upper(H2, 0.01)
     assert abs(d_ref - 0.016) < 1e-9
     assert abs(damps[0] - d_ref) < 1e-12, (damps[0], d_ref)
+
+
+def test_factor_damp_retry_batched_multipanel(dev):
+    """Two layers over three panels: layer 1 is indefinite at damp 0.01 (its
+    failure stops its later panels and inverse rows mid-way) and is refactored
+    alone at the reference's next damps; layer 0 keeps its first factor."""
+    from g2ptq_amd import _core
+    print("factor damp retry B=2 C=1100", flush=True)
+    C = 1100
+    g = gen(5)
+    Hs = []
+    for b in range(2):
+        X = torch.randn(4 * C, C, generator=g) * torch.exp(0.3 * torch.randn(C, generator=g))
+        Hs.append((X.T @ X) / X.shape[0])
+    H1 = Hs[1].double()
+    lam = torch.linalg.eigvalsh(H1)[0].item()
+    m = torch.mean(torch.diag(H1)).item()
+    m2 = (m - lam) / 1.0153  # as in test_factor_damp_retry: 0.01 … 0.0145 fail, 0.016 succeeds
+    Hs[1] = (H1 - (lam + 0.0153 * m2) * torch.eye(C, dtype=torch.float64)).float()
+    H = torch.stack(Hs)
+    U, damps = _core.factor(H.clone().to(dev), 0.01)
+    # the retry leaves no trace of the failed attempt: layer 1 equals a direct
+    # factor of both layers at the final damp, bit for bit
+    U16, _ = _core.factor(H.clone().to(dev), 0.016)
+    torch.cuda.synchronize()
+    U, U16 = U.cpu(), U16.cpu()
+    assert torch.equal(U[1], U16[1])
+    # Layer 1 succeeds at λ_min(A) = 0.0007·m2 (cond(A) ≈ 1.1e4), where the
+    # explicit inverses of the diagonal blocks lose more than LAPACK's
+    # substitution: within 10× of the reference chain there (≈ 5e-6 relative),
+    # within 2× for the well-conditioned layer 0.
+    for b, want, slack in ((0, 0.01, 2), (1, 0.016, 10)):
+        Uo, d_ref = ofactor.damp_chol_inv_upper(H[b], 0.01)
+        assert abs(d_ref - want) < 1e-9
+        assert abs(damps[b] - d_ref) < 1e-12, (b, damps[b], d_ref)
+        Ut, _ = ofactor.exact_inv_upper(H[b], d_ref)
+        assert torch.all(torch.tril(U[b], -1) == 0)
+        err_hip = ((U[b].double() - Ut).norm() / Ut.norm()).item()
+        err_ref = ((Uo.double() - Ut).norm() / Ut.norm()).item()
+        assert err_hip <= max(slack * err_ref, 1e-6), (b, err_hip, err_ref)
 
 
 @pytest.mark.parametrize("variant,groupsize", [(0, 128), (0, -1), (1, 128), (2, 128), (0, 96)])
