@@ -370,9 +370,10 @@ def run_step(acts, layers, w0, n_tokens, ev):
         e1.record(stream)
         e2, e3 = ev()
         e2.record(stream)
-        for gq, spec in insts:
-            gq.fasterquant(blocksize=128, percdamp=0.01, groupsize=GROUPSIZE, actorder=False,
-                           static_groups=False, backend="hip")
+        # every instance's fasterquant; instances that share the input (q and
+        # k/v) run as one compensation loop over all their rows
+        share.fasterquant(blocksize=128, percdamp=0.01, groupsize=GROUPSIZE, actorder=False,
+                          static_groups=False, backend="hip")
         e3.record(stream)
         torch.cuda.synchronize()
         hess_ms += e0.elapsed_time(e1)

@@ -316,3 +316,42 @@ def test_nan_hessian_exhausts_the_damp_retry(dev):
     gq.H = H.to(dev)
     with pytest.raises(ValueError, match="damp_percent"):
         gq.fasterquant(backend="hip")
+
+
+@pytest.mark.parametrize("rows_q,rows_kv,C,mse", [(96, 32, 640, False), (96, 32, 640, True),
+                                                   (4096, 1024, 1024, False)])
+def test_shared_input_joint_fasterquant_matches_per_instance(dev, rows_q, rows_kv, C, mse):
+    """SharedInputHessian.fasterquant (one compensation loop over q's and k/v's
+    rows) gives every member the weights and group parameters of its own
+    fasterquant, bit for bit."""
+    from g2ptq_amd import GPTQ, SharedInputHessian, WeightQuantizer, make_group_quantizers
+    print(f"joint fasterquant q={rows_q} kv={rows_kv} C={C} mse={mse}", flush=True)
+    X = _acts(2048, C, 77)
+
+    def setup():
+        lq = _layer(rows_q, C, 1).to(dev)
+        lk, lv = _layer(rows_kv, C, 2).to(dev), _layer(rows_kv, C, 3).to(dev)
+        insts = [GPTQ([lq]), GPTQ([lk, lv])]
+        for inst in insts:
+            q = WeightQuantizer()
+            q.configure(4, perchannel=True, sym=True, mse=mse)
+            inst.quantizer = make_group_quantizers(q, C, 128)
+        share = SharedInputHessian([(insts[0], 0), (insts[1], 0), (insts[1], 1)])
+        for i in range(0, 2048, 512):
+            share.add_batch(X[i:i + 512].reshape(1, 512, C).to(dev))
+        share.finalize()
+        return [lq, lk, lv], insts, share
+
+    kw = dict(blocksize=128, percdamp=0.01, groupsize=128, actorder=False, static_groups=False,
+              backend="hip")
+    la, ia, _ = setup()
+    for inst in ia:
+        inst.fasterquant(**kw)
+    lb, ib, share = setup()
+    share.fasterquant(**kw)
+    torch.cuda.synchronize()
+    for x, y in zip(la, lb):
+        assert torch.equal(x.weight, y.weight)
+    for xa, xb in zip(ia, ib):
+        for qa, qb in zip(xa.quantizer, xb.quantizer):
+            assert torch.equal(qa.scale, qb.scale) and torch.equal(qa.zero, qb.zero)
