@@ -80,14 +80,16 @@ __global__ void fix_h_kernel(float* H, int64_t C, const int* nz, const int* dead
   }
 }
 
-// Zero dead columns of a (B, rows, C) matrix; optionally zero whole entries whose H was zero.
+// wipe == 0: zero the dead columns of each (rows, C) slice of M (weights, GPTAQ's
+// cross term).  wipe == 1: zero the whole slice where H[b] was all zero and leave
+// every other slice alone, dead columns included (G2PTQ's gradients:
+// g2ptq_utils.py:394-401 clears them only together with an all-zero Hessian).
 __global__ void zero_cols_kernel(float* M, int64_t rows, int64_t C, const int* dead, const int* nz,
-                                 const int* anydead, int zero_if_h_zero) {
+                                 const int* anydead, int wipe) {
   const int64_t b = blockIdx.y;
   const int64_t n = rows * C;
   float* Mb = M + b * n;
-  const bool wipe = zero_if_h_zero && !nz[b];
-  if (!wipe && !anydead[b]) return;  // nothing to zero in this layer
+  if (wipe ? nz[b] != 0 : !anydead[b]) return;  // nothing to zero in this slice
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < n;
        e += (int64_t)gridDim.x * blockDim.x) {
     if (wipe || dead[b * C + (e % C)]) Mb[e] = 0.f;

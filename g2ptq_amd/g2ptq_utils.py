@@ -221,6 +221,9 @@ class G2PTQ:
             _lib.call("g2ptq_trust_region", _core.stream(), _lib.ptr(grads), _lib.ptr(Hinv),
                       _lib.ptr(Q_sub), _lib.ptr(W_sub), B * G, Rg, C, _core.f32(alpha), 1,
                       _lib.ptr(beta), _lib.ptr(Z), _lib.ptr(GH), _lib.ptr(ws), ws.numel())
+            # the per-row step of the last call, (B·G, R/G), for inspection (the
+            # reference keeps it local)
+            self._beta = beta.view(B * G, Rg)
             Q, W_int, Scale = _compensate(_lib.VARIANT_G2PTQ, self.quantizer, W_sub, Hinv,
                                           blocksize, groupsize, static_groups,
                                           perm if static_groups and actorder else None, flags,
@@ -228,6 +231,7 @@ class G2PTQ:
         else:
             # β = 0 ⇒ Z = GHinv = 0 and the G2PTQ sweep reduces, operation for
             # operation, to the GPTQ sweep.
+            self._beta = None
             Q, W_int, Scale = _compensate(_lib.VARIANT_GPTQ, self.quantizer, W_sub, Hinv,
                                           blocksize, groupsize, static_groups,
                                           perm if static_groups and actorder else None, flags,

@@ -13,11 +13,16 @@ from . import quant
 # Block operators (restating the torch backends of ``run_eager``)
 # ---------------------------------------------------------------------------
 
-def gptq_block(weight, hinv, scale, zero, int_weight, error, maxq):
-    """gptq_utils/gptq_utils.py:28-51 (in place on ``weight``/``int_weight``/``error``)."""
+def gptq_block(weight, hinv, scale, zero, int_weight, error, maxq, xq=None):
+    """gptq_utils/gptq_utils.py:28-51 (in place on ``weight``/``int_weight``/``error``).
+
+    ``xq`` (optional, the block's shape) receives each column's value at the
+    moment it is quantized, for the parity tests' rounding-tie checks."""
     columns = weight.shape[1]
     for column in range(columns):
         w = weight[:, column]
+        if xq is not None:
+            xq[:, column] = w
         qi, qs, qz = quant.asym_quant(w, scale[:, column], zero[:, column], maxq)
         q = quant.asym_dequant(qi, qs, qz)
         err = (w - q) / hinv[:, column, column].unsqueeze(1)
@@ -30,11 +35,13 @@ def gptq_block(weight, hinv, scale, zero, int_weight, error, maxq):
     return weight, int_weight, error
 
 
-def gptaq_block(weight, hinv, p, scale, zero, column_weight, int_weight, error, maxq):
+def gptaq_block(weight, hinv, p, scale, zero, column_weight, int_weight, error, maxq, xq=None):
     """gptq_utils/gptaq_utils.py:28-56."""
     columns = weight.shape[1]
     for column in range(columns):
         column_weight.copy_(weight[:, column])
+        if xq is not None:
+            xq[:, column] = column_weight
         qi, qs, qz = quant.asym_quant(column_weight, scale[:, column], zero[:, column], maxq)
         q = quant.asym_dequant(qi, qs, qz)
         err = (column_weight - q) / hinv[:, column, column].unsqueeze(1)
@@ -49,11 +56,13 @@ def gptaq_block(weight, hinv, p, scale, zero, column_weight, int_weight, error, 
     return weight, int_weight, error
 
 
-def g2ptq_block(weight, hinv, scale, zero, z, ghinv, int_weight, error, maxq):
+def g2ptq_block(weight, hinv, scale, zero, z, ghinv, int_weight, error, maxq, xq=None):
     """gptq_utils/g2ptq_utils.py:34-74 (``approx_beta == 0``)."""
     columns = weight.shape[1]
     for column in range(columns):
         w = weight[:, column]
+        if xq is not None:
+            xq[:, column] = w
         qi, qs, qz = quant.asym_quant(w, scale[:, column], zero[:, column], maxq)
         q = quant.asym_dequant(qi, qs, qz)
         err = w - q - ghinv[:, column]
@@ -101,10 +110,25 @@ def _maxq(quantizers):
     return quantizers[0].maxq
 
 
+def _recorder(record, W):
+    """``record`` (a dict or None) receives ``"X"``: every weight's value when it
+    was quantized, in the loop's column order (B, R, C)."""
+    if record is None:
+        return None
+    record["X"] = torch.zeros_like(W)
+    return record["X"]
+
+
+def _record_block(X, i1, i2, xt):
+    if X is not None:
+        X[:, :, i1:i2] = xt.transpose(1, 2)
+
+
 def gptq_compensation(W, Hinv, quantizers, blocksize=128, groupsize=-1, static_groups=False,
-                      qparam_perm=None, H_diag=None):
+                      qparam_perm=None, H_diag=None, record=None):
     """gptq_utils/gptq_utils.py:165-232 (torch backend, no graph). Mutates W."""
     B, R, C = W.shape
+    X = _recorder(record, W)
     Q = torch.zeros_like(W)
     W_int = torch.zeros_like(W)
     Scale = torch.zeros_like(W)
@@ -115,9 +139,10 @@ def gptq_compensation(W, Hinv, quantizers, blocksize=128, groupsize=-1, static_g
                                 H_diag)
         S1, Z1 = _stack_params(cq, W1.shape)
         wt = W1.transpose(1, 2).contiguous()
-        it, et = torch.empty_like(wt), torch.empty_like(wt)
+        it, et, xt = torch.empty_like(wt), torch.empty_like(wt), torch.empty_like(wt)
         gptq_block(wt, Hinv[:, i1:i2, i1:i2].contiguous(), S1.transpose(1, 2).contiguous(),
-                   Z1.transpose(1, 2).contiguous(), it, et, _maxq(quantizers))
+                   Z1.transpose(1, 2).contiguous(), it, et, _maxq(quantizers), xt)
+        _record_block(X, i1, i2, xt)
         Q1, I1, E1 = (t.transpose(1, 2).contiguous() for t in (wt, it, et))
         Q[:, :, i1:i2] = Q1
         W_int[:, :, i1:i2] = I1
@@ -127,9 +152,10 @@ def gptq_compensation(W, Hinv, quantizers, blocksize=128, groupsize=-1, static_g
 
 
 def gptaq_compensation(W, Hinv, P, quantizers, blocksize=128, groupsize=-1, static_groups=False,
-                       qparam_perm=None, H_diag=None):
+                       qparam_perm=None, H_diag=None, record=None):
     """gptq_utils/gptaq_utils.py:193-261. Mutates W."""
     B, R, C = W.shape
+    X = _recorder(record, W)
     Q = torch.zeros_like(W)
     W_int = torch.zeros_like(W)
     Scale = torch.zeros_like(W)
@@ -140,11 +166,12 @@ def gptaq_compensation(W, Hinv, P, quantizers, blocksize=128, groupsize=-1, stat
                                 H_diag)
         S1, Z1 = _stack_params(cq, W1.shape)
         wt = W1.transpose(1, 2).contiguous()
-        it, et = torch.empty_like(wt), torch.empty_like(wt)
+        it, et, xt = torch.empty_like(wt), torch.empty_like(wt), torch.empty_like(wt)
         cw = torch.empty(wt.shape[0], wt.shape[2])
         gptaq_block(wt, Hinv[:, i1:i2, i1:i2].contiguous(), P[:, i1:i2, i1:i2].contiguous(),
                     S1.transpose(1, 2).contiguous(), Z1.transpose(1, 2).contiguous(), cw, it, et,
-                    _maxq(quantizers))
+                    _maxq(quantizers), xt)
+        _record_block(X, i1, i2, xt)
         Q1, I1, E1 = (t.transpose(1, 2).contiguous() for t in (wt, it, et))
         Q[:, :, i1:i2] = Q1
         W_int[:, :, i1:i2] = I1
@@ -155,9 +182,10 @@ def gptaq_compensation(W, Hinv, P, quantizers, blocksize=128, groupsize=-1, stat
 
 
 def g2ptq_compensation(W, Hinv, Z, GHinv, quantizers, blocksize=128, groupsize=-1,
-                       static_groups=False, qparam_perm=None, H_diag=None):
+                       static_groups=False, qparam_perm=None, H_diag=None, record=None):
     """gptq_utils/g2ptq_utils.py:252-347 (``approx_grad_beta == 0``). Mutates W and GHinv."""
     B, R, C = W.shape
+    X = _recorder(record, W)
     Q = torch.zeros_like(W)
     W_int = torch.zeros_like(W)
     Scale = torch.zeros_like(W)
@@ -171,10 +199,11 @@ def g2ptq_compensation(W, Hinv, Z, GHinv, quantizers, blocksize=128, groupsize=-
                                 H_diag)
         S1, Zp1 = _stack_params(cq, W1.shape)
         wt = W1.transpose(1, 2).contiguous()
-        it, et = torch.empty_like(wt), torch.empty_like(wt)
+        it, et, xt = torch.empty_like(wt), torch.empty_like(wt), torch.empty_like(wt)
         g2ptq_block(wt, Hinv[:, i1:i2, i1:i2].contiguous(), S1.transpose(1, 2).contiguous(),
                     Zp1.transpose(1, 2).contiguous(), Z1.transpose(1, 2).contiguous(),
-                    GH1.transpose(1, 2).contiguous(), it, et, _maxq(quantizers))
+                    GH1.transpose(1, 2).contiguous(), it, et, _maxq(quantizers), xt)
+        _record_block(X, i1, i2, xt)
         Q1, I1, E1 = (t.transpose(1, 2).contiguous() for t in (wt, it, et))
         Q[:, :, i1:i2] = Q1
         W_int[:, :, i1:i2] = I1

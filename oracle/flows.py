@@ -32,6 +32,12 @@ def _static_params(quantizers, W_flat, groupsize, static_groups, H_diag=None):
                     qz.find_params(W_flat[:, sl], None if H_diag is None else H_diag[:, sl])
 
 
+def _loop_record(record, perm):
+    """The pre-quantization values of a compensation loop, in the loop's column
+    order, and the loop order itself (``perm`` maps loop column → column)."""
+    return {"X": record["X"], "perm": perm}
+
+
 def gptq_fasterquant(W, H, bits, sym, blocksize=128, percdamp=0.01, groupsize=-1, actorder=False,
                      static_groups=False, quantizers=None, mse=False, hclip=False):
     """gptq_utils/gptq_utils.py:234-353 (returns instead of writing layers)."""
@@ -56,13 +62,14 @@ def gptq_fasterquant(W, H, bits, sym, blocksize=128, percdamp=0.01, groupsize=-1
             H[b] = H[b][perm][:, perm]
         Hinv[b], d = factor.damp_chol_inv_upper(H[b], percdamp)
         damps.append(d)
+    rec = {}
     Q, W_int, Scale = compensate.gptq_compensation(
         W, Hinv, quantizers, blocksize, groupsize, static_groups,
-        perm if static_groups and actorder else None, H_diag)
+        perm if static_groups and actorder else None, H_diag, record=rec)
     if actorder:
         Q, W_int, Scale = Q[:, :, invperm], W_int[:, :, invperm], Scale[:, :, invperm]
     return {"Q": Q, "W_int": W_int, "Scale": Scale, "quantizers": quantizers, "Hinv": Hinv,
-            "damp": damps, "perm": perm}
+            "damp": damps, "perm": perm, "loop": _loop_record(rec, perm)}
 
 
 def gptaq_fasterquant(W, H, dXXT, bits, sym, blocksize=128, percdamp=0.01, groupsize=-1,
@@ -93,12 +100,14 @@ def gptaq_fasterquant(W, H, dXXT, bits, sym, blocksize=128, percdamp=0.01, group
             dXXT[b] = dXXT[b][perm][:, perm]
         Hinv[b], _ = factor.damp_chol_inv_upper(H[b], percdamp)
     P = compensate.gptaq_P(dXXT, Hinv, alpha)
+    rec = {}
     Q, W_int, Scale = compensate.gptaq_compensation(
         W, Hinv, P, quantizers, blocksize, groupsize, static_groups,
-        perm if static_groups and actorder else None, H_diag)
+        perm if static_groups and actorder else None, H_diag, record=rec)
     if actorder:
         Q, W_int, Scale = Q[:, :, invperm], W_int[:, :, invperm], Scale[:, :, invperm]
-    return {"Q": Q, "W_int": W_int, "Scale": Scale, "quantizers": quantizers, "Hinv": Hinv, "P": P}
+    return {"Q": Q, "W_int": W_int, "Scale": Scale, "quantizers": quantizers, "Hinv": Hinv, "P": P,
+            "perm": perm, "loop": _loop_record(rec, perm)}
 
 
 def g2ptq_trust_region(gradients_sub, Hinv_init, Hinv, Q_sub, W_sub, alpha, enabled):
@@ -166,13 +175,18 @@ def g2ptq_fasterquant(W, H, gradients, act_square, bits, sym, num_groups, blocks
         H_diag = H_diag[:, perm].contiguous()
     beta, Z, GHinv = g2ptq_trust_region(grads, Hinv_init, Hinv, Q_sub, W_sub, alpha,
                                         enable_gradient_update and alpha > 0)
+    GH0, W_tr = GHinv.clone(), W_sub.clone()
+    rec = {}
     Q, W_int, Scale = compensate.g2ptq_compensation(
         W_sub, Hinv, Z, GHinv, quantizers, blocksize, groupsize, static_groups,
-        perm if static_groups and actorder else None, H_diag)
+        perm if static_groups and actorder else None, H_diag, record=rec)
     if actorder:
         Q, W_int, Scale = Q[:, :, invperm], W_int[:, :, invperm], Scale[:, :, invperm]
+    rec["X"] = rec["X"].view(B, R, C)
     return {"Q": Q.view(B, R, C), "W_int": W_int.view(B, R, C), "Scale": Scale.view(B, R, C),
-            "quantizers": quantizers, "Hinv": Hinv, "beta": beta, "Z": Z, "GHinv0": None}
+            "quantizers": quantizers, "Hinv": Hinv, "beta": beta, "Z": Z, "GHinv0": GH0,
+            "Hinv_init": Hinv_init, "grads": grads, "Q0": Q_sub, "W_sub": W_tr,
+            "perm": perm, "loop": _loop_record(rec, perm)}
 
 
 def guided_fasterquant(W, H, act_square, bits, sym, num_groups, blocksize=128, percdamp=0.01,
@@ -207,13 +221,15 @@ def guided_fasterquant(W, H, act_square, bits, sym, num_groups, blocksize=128, p
             W_sub[b] = W_sub[b][:, perm]
             H_sub[b] = H_sub[b][perm][:, perm]
         Hinv[b], _ = factor.damp_chol_inv_upper(H_sub[b], percdamp)
+    rec = {}
     Q, W_int, Scale = compensate.gptq_compensation(
         W_sub, Hinv, quantizers, blocksize, groupsize, static_groups,
-        perm if static_groups and actorder else None, H_diag)
+        perm if static_groups and actorder else None, H_diag, record=rec)
     if actorder:
         Q, W_int, Scale = Q[:, :, invperm], W_int[:, :, invperm], Scale[:, :, invperm]
+    rec["X"] = rec["X"].view(B, R, C)
     return {"Q": Q.view(B, R, C), "W_int": W_int.view(B, R, C), "Scale": Scale.view(B, R, C),
-            "quantizers": quantizers, "Hinv": Hinv}
+            "quantizers": quantizers, "Hinv": Hinv, "perm": perm, "loop": _loop_record(rec, perm)}
 
 
 def rtn(W, bits, sym, groupsize):

@@ -135,6 +135,13 @@ class WeightQuantizer:
         s, z = find_params(xg, self.bits, self.sym, self.mse, self.norm, self.grid,
                            self.maxshrink, H_diag if self.hclip else None)
         self.scale, self.zero = s, z
+        # The zero point before its rounding (min/max asym fits only), for the
+        # parity tests' tie checks: a value within rounding noise of k + 1/2
+        # can round either way on another machine's arithmetic.
+        self.zraw = None
+        if not self.sym and not self.mse:
+            xmin, _ = minmax(xg)
+            self.zraw = (self.minq - xmin / s.unsqueeze(-1)).squeeze(-1)
         self._ready = True
 
     def ready(self):

@@ -103,6 +103,14 @@ def make_loops():
     return out
 
 
+def student_t3(shape, g):
+    """Student-t samples with ν = 3 from the seeded generator: N(0,1)/sqrt(χ²₃/3),
+    χ²₃ a sum of three squared normals."""
+    z = torch.randn(shape, generator=g)
+    chi2 = torch.randn((3,) + tuple(shape), generator=g).pow(2).sum(0)
+    return z / torch.sqrt(chi2 / 3)
+
+
 def flow_inputs():
     """Seeded inputs of the C=256 flow fixtures: LogNormal channel scales, bf16
     activations, bf16 weights ~N(0, 0.02), a perturbed full-precision input
@@ -115,7 +123,7 @@ def flow_inputs():
     W = (torch.randn(B, R, C, generator=g) * 0.02).bfloat16()
     G = 2
     sal = torch.rand(T, G, generator=g) * torch.exp(0.5 * torch.randn(T, 1, generator=g))
-    tau = torch.distributions.StudentT(3.0).sample((B, R, 1)).abs()
+    tau = student_t3((B, R, 1), g).abs()
     grad = 1e-3 * torch.randn(B, R, C, generator=g) * tau
     return dict(X=X, Xfp=Xfp, W=W, sal=sal, grad=grad, G=G)
 
@@ -166,6 +174,16 @@ def make_flows():
         out[f"{k}/q"] = r["Q"].numpy()
         if "beta" in r:
             out[f"{k}/beta"] = r["beta"].numpy()
+        # what the end-to-end parity protocol (oracle.parity) needs: the values
+        # at quantization time in loop order, the loop order, the fitted groups
+        out[f"{k}/x"] = r["loop"]["X"].numpy()
+        perm = r["perm"]
+        out[f"{k}/perm"] = (perm if perm is not None else torch.arange(W0.shape[2])).numpy()
+        qs = r["quantizers"]
+        out[f"{k}/qscale"] = torch.stack([q.scale.reshape(-1) for q in qs]).numpy()
+        out[f"{k}/qzero"] = torch.stack([q.zero.reshape(-1) for q in qs]).numpy()
+        if qs[0].zraw is not None:
+            out[f"{k}/qzraw"] = torch.stack([q.zraw.reshape(-1) for q in qs]).numpy()
     np.savez_compressed(FLOWS_FILE, **out)
     return out
 

@@ -120,3 +120,13 @@ def test_flow_gptq_matches_golden(flows):
     e1 = oflows.reconstruction_error(d["W"].float(), r["Q"], st["H"])
     e2 = oflows.reconstruction_error(d["W"].float(), _t(flows["gptq_asym/q"]), st["H"])
     assert abs(e1 - e2) <= 1e-4 * e2
+
+
+def test_flow_fixture_inputs_reproduce(flows):
+    """The seeded flow generator (every draw from one CPU generator) still
+    produces the stored flow inputs."""
+    d = mg.flow_inputs()
+    for k in ("X", "Xfp", "W"):
+        assert torch.equal(d[k].view(torch.int16), _t(flows[f"in_{k}"])), k
+    for k in ("sal", "grad"):
+        assert torch.equal(d[k], _t(flows[f"in_{k}"])), k

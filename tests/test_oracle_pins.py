@@ -551,6 +551,170 @@ def test_trust_region_beta_bounds_and_identities():
     assert torch.all(b0 == 0) and torch.all(Z0 == 0) and torch.all(G0 == 0)
 
 
+def _tr_slip_drop_ga2(grad, Ainv, U, Q, W, alpha):
+    """Planted mistake: c without its −GA²/diag(A⁻¹) term."""
+    GA = torch.bmm(grad, Ainv)
+    e = Q - W
+    d = torch.diagonal(Ainv, dim1=1, dim2=2).unsqueeze(1)
+    loss = ((e * GA + e ** 2 / 2) / d).abs()
+    c = (grad * GA).sum(2, keepdim=True).expand_as(GA)
+    c = c.clamp(min=2 * alpha * loss).clamp(min=torch.finfo(torch.float32).tiny)
+    return (1 - torch.sqrt(torch.clamp(1 - 2 * alpha * loss / c, min=0.0))).mean(-1)
+
+
+def _tr_slip_sign(grad, Ainv, U, Q, W, alpha):
+    """Planted mistake: E0 = W − Q instead of Q − W."""
+    return oflows.g2ptq_trust_region(grad, Ainv, U, W, Q, alpha, True)[0]
+
+
+def _tr_slip_diag_u(grad, Ainv, U, Q, W, alpha):
+    """Planted mistake: diag(U) used where diag(A⁻¹) belongs."""
+    Ad = Ainv.clone()
+    idx = torch.arange(Ainv.shape[-1])
+    Ad[:, idx, idx] = torch.diagonal(U, dim1=1, dim2=2)
+    GA = torch.bmm(grad, Ainv)
+    e = Q - W
+    d = torch.diagonal(Ad, dim1=1, dim2=2).unsqueeze(1)
+    loss = ((e * GA + e ** 2 / 2) / d).abs()
+    c = (grad * GA).sum(2, keepdim=True) - GA ** 2 / d
+    c = c.clamp(min=2 * alpha * loss).clamp(min=torch.finfo(torch.float32).tiny)
+    return (1 - torch.sqrt(torch.clamp(1 - 2 * alpha * loss / c, min=0.0))).mean(-1)
+
+
+def _beta_true(grad, Ainv, U, Q, W, alpha):
+    return oflows.g2ptq_trust_region(grad, Ainv, U, Q, W, alpha, True)[0]
+
+
+def _hand_case():
+    """One row, two columns, A = [[2, 1], [1, 2]]: A⁻¹ = [[2, −1], [−1, 2]]/3,
+    Grad = [1, 2], E0 = Q0 − W0 = [1/2, −1/4]."""
+    Ainv = torch.tensor([[[2.0, -1.0], [-1.0, 2.0]]], dtype=torch.float64) / 3
+    U = torch.linalg.cholesky(Ainv, upper=True)
+    grad = torch.tensor([[[1.0, 2.0]]], dtype=torch.float64)
+    W = torch.tensor([[[0.0, 0.0]]], dtype=torch.float64)
+    Q = torch.tensor([[[0.5, -0.25]]], dtype=torch.float64)
+    return grad, Ainv, U, Q, W
+
+
+def _hand_beta(alpha):
+    """Worked by hand.  GA = Grad·A⁻¹ = [0, 1]; diag(A⁻¹) = [2/3, 2/3];
+    loss = |(E0·GA + E0²/2)/diag| = [(1/8)·(3/2), |−1/4 + 1/32|·(3/2)]
+         = [3/16, 21/64];
+    c = Σ Grad⊙GA − GA²/diag = [2 − 0, 2 − 3/2] = [2, 1/2].
+    α = 0.1: 2α·loss = [3/80, 21/320] < c, so 1 − 2α·loss/c = [157/160, 139/160]
+    and β = 1 − (√(157/160) + √(139/160))/2.
+    α = 2: 2α·loss = [3/4, 21/16]; the second exceeds c = 1/2, c is clamped up
+    to it and its term is 1 − √0 = 1; the first is 1 − √(1 − 3/8):
+    β = (1 + 1 − √(5/8))/2."""
+    if alpha == 0.1:
+        return 1 - (math.sqrt(157 / 160) + math.sqrt(139 / 160)) / 2
+    if alpha == 2.0:
+        return (2 - math.sqrt(5 / 8)) / 2
+    raise ValueError(alpha)
+
+
+def _diag_case(seed):
+    """Diagonal Hessians, so A⁻¹ = diag(d): every term of the trust region
+    reduces to scalars.  Rows mix clamped and unclamped columns."""
+    g = gen(seed)
+    BG, Rg, C = 2, 4, 6
+    h = torch.rand(BG, C, generator=g, dtype=torch.float64) * 3 + 0.25
+    H = torch.diag_embed(h)
+    damp = 0.01 * h.mean(-1, keepdim=True)
+    d = 1 / (h + damp)
+    Ainv = torch.diag_embed(d)
+    U = torch.diag_embed(torch.sqrt(d))
+    grad = torch.randn(BG, Rg, C, generator=g, dtype=torch.float64)
+    grad[:, :, 0] *= 6  # one dominant gradient column: c_0 is small, its clamp engages
+    W = torch.randn(BG, Rg, C, generator=g, dtype=torch.float64)
+    Q = W + 0.8 * torch.randn(BG, Rg, C, generator=g, dtype=torch.float64)
+    return H, d, grad, Ainv, U, Q, W
+
+
+def _diag_beta(d, grad, Q, W, alpha):
+    """The diagonal closed form, entry by entry in Python floats:
+    loss_j = |e_j·g_j + e_j²/(2·d_j)|, c_j = Σ_k g_k²·d_k − g_j²·d_j clamped to
+    at least 2α·loss_j and the smallest normal float, β = mean_j(1 − √max(1 −
+    2α·loss_j/c_j, 0)).  Also returns how many terms the clamp decided."""
+    BG, Rg, C = grad.shape
+    beta = torch.zeros(BG, Rg, dtype=torch.float64)
+    clamped = 0
+    tiny = torch.finfo(torch.float32).tiny
+    for b in range(BG):
+        for r in range(Rg):
+            g = grad[b, r].tolist()
+            e = (Q[b, r] - W[b, r]).tolist()
+            dd = d[b].tolist()
+            total = sum(gk * gk * dk for gk, dk in zip(g, dd))
+            acc = 0.0
+            for j in range(C):
+                loss = abs(e[j] * g[j] + e[j] * e[j] / (2 * dd[j]))
+                c = total - g[j] * g[j] * dd[j]
+                if c < 2 * alpha * loss:
+                    clamped += 1
+                c = max(c, 2 * alpha * loss, tiny)
+                acc += 1 - math.sqrt(max(1 - 2 * alpha * loss / c, 0.0))
+            beta[b, r] = acc / C
+    return beta, clamped
+
+
+def test_trust_region_hand_computed_case():
+    """g2ptq_utils.py:459-476 on a 1×2 case worked by hand (_hand_beta), at an
+    α where no clamp engages and at one where a column's c is clamped."""
+    grad, Ainv, U, Q, W = _hand_case()
+    for alpha in (0.1, 2.0):
+        beta, Z, GH = oflows.g2ptq_trust_region(grad, Ainv, U, Q, W, alpha, True)
+        assert abs(float(beta) - _hand_beta(alpha)) < 1e-14
+        # GH = β·Grad·A⁻¹ = β·[0, 1]; Z = β·Grad·Uᵀ
+        assert torch.allclose(GH[0, 0], float(beta) * torch.tensor([0.0, 1.0], dtype=torch.float64),
+                              atol=1e-15)
+        assert torch.allclose(Z[0], float(beta) * grad[0] @ U[0].T, atol=1e-15)
+
+
+def test_trust_region_diagonal_closed_form():
+    """Diagonal Hessians, through the oracle's own factor: U = diag(√d) and
+    A⁻¹ = diag(d) with d = 1/(h + 0.01·mean h), and β, Z = β·g·√d,
+    GH = β·g·d equal the scalar closed form (_diag_beta), with the clamp
+    deciding some terms and not others."""
+    for seed in (31, 32):
+        H, d, grad, Ainv, U, Q, W = _diag_case(seed)
+        Uo, Ao = [], []
+        for h in H.float():
+            u, _, a = ofactor.damp_chol_inv_upper(h, 0.01, want_inverse=True)
+            Uo.append(u)
+            Ao.append(a)
+        Uo, Ao = torch.stack(Uo).double(), torch.stack(Ao).double()
+        assert torch.allclose(Uo, U, rtol=1e-6, atol=1e-7)
+        assert torch.allclose(Ao, Ainv, rtol=1e-6, atol=1e-7)
+        alpha = 0.5
+        beta, Z, GH = oflows.g2ptq_trust_region(grad, Ainv, U, Q, W, alpha, True)
+        ref, clamped = _diag_beta(d, grad, Q, W, alpha)
+        assert 0 < clamped < grad.numel(), clamped
+        assert torch.allclose(beta, ref, rtol=1e-12, atol=1e-14)
+        b = ref.unsqueeze(2)
+        assert torch.allclose(Z, b * grad * torch.sqrt(d).unsqueeze(1), rtol=1e-12, atol=1e-14)
+        assert torch.allclose(GH, b * grad * d.unsqueeze(1), rtol=1e-12, atol=1e-14)
+
+
+def test_trust_region_planted_mistakes_fail_the_pins():
+    """Each plausible slip — dropping −GA²/diag(A⁻¹) from c, flipping the sign
+    of E0, using diag(U) for diag(A⁻¹) — fails the hand-computed case or the
+    diagonal closed form, while the oracle passes both."""
+    grad, Ainv, U, Q, W = _hand_case()
+    H, d, dgrad, dAinv, dU, dQ, dW = _diag_case(31)
+    dref, _ = _diag_beta(d, dgrad, dQ, dW, 0.5)
+
+    def fails(fn):
+        hand = any(abs(float(fn(grad, Ainv, U, Q, W, a)) - _hand_beta(a)) > 1e-9
+                   for a in (0.1, 2.0))
+        diag = not torch.allclose(fn(dgrad, dAinv, dU, dQ, dW, 0.5), dref, rtol=1e-9, atol=1e-12)
+        return hand or diag
+
+    assert not fails(_beta_true)
+    for slip in (_tr_slip_drop_ga2, _tr_slip_sign, _tr_slip_diag_u):
+        assert fails(slip), slip.__doc__
+
+
 # ---------------------------------------------------------------------------
 # compressed-tensors packing (oracle/pack.py)
 # ---------------------------------------------------------------------------
