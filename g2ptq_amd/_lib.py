@@ -147,12 +147,14 @@ _WORKSPACES = {}
 def workspace(nbytes, device):
     """A cached uint8 device buffer of at least ``nbytes`` bytes.
 
-    Buffers are cached per device and reused across calls; callers enqueue on
-    the current stream, so stream order protects reuse.
+    Buffers are cached per (device, current stream) and reused across calls:
+    the calls that use one buffer are enqueued on that stream, so stream order
+    protects its reuse, and calls on different streams never share one.
     """
     nbytes = max(int(nbytes), 256)
     dev = torch.device(device)
-    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    index = dev.index if dev.index is not None else torch.cuda.current_device()
+    key = (index, torch._C._cuda_getCurrentRawStream(index))
     buf = _WORKSPACES.get(key)
     if buf is None or buf.numel() < nbytes:
         _WORKSPACES[key] = None

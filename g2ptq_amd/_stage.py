@@ -179,6 +179,10 @@ def staged_attr(name):
     def set(self, value):
         if value is None and getattr(self, private, None) is not None:
             self._flush_staged()
+        elif value is not None and getattr(self, private, None) is not None:
+            # a replaced Hessian is no longer the one a shared-input group's
+            # cached factor was computed from
+            self.__dict__.pop("_shared_factor", None)
         setattr(self, private, value)
         if value is None:
             for st in getattr(self, "_stagers", None) or ():

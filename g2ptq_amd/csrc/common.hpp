@@ -100,12 +100,13 @@ struct GemmF32 {
 
 int gemm_f32(hipStream_t stream, const GemmF32& g);
 
-// Two more streams (default priority) and events per device, created once
-// and kept, for the lookahead of the factor (the trailing updates on
-// `stream`, the triangular inverse's block rows on `stream2`) and of the
-// compensation loop (the far block tails on `stream`).  Calls that overlap
-// on one device would share them: the library's entry points are not meant
-// to run concurrently on one device.
+// Two more streams (default priority) and events per (device, caller stream),
+// created on first use and kept, for the lookahead of the factor (the
+// trailing updates on `stream`, the triangular inverse's block rows on
+// `stream2`) and of the compensation loop (the far block tails on `stream`).
+// Calls on different caller streams get different side streams and events, so
+// they can overlap; calls from several host threads on one caller stream
+// interleave their launches and must not overlap (nor share a workspace).
 struct SideStream {
   hipStream_t stream = nullptr;
   hipStream_t stream2 = nullptr;
@@ -115,7 +116,7 @@ struct SideStream {
   hipEvent_t swept = nullptr;                   // compensation: a super-block swept (main)
   hipEvent_t tailed = nullptr;                  // compensation: its far tail applied (side)
 };
-int side_stream(SideStream& out);
+int side_stream(hipStream_t caller, SideStream& out);
 
 // p[0..n) = v with a kernel (graph-capture safe, unlike hipMemsetAsync).
 int fill_f32(hipStream_t stream, float* p, int64_t n, float v);

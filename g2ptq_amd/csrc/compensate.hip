@@ -168,7 +168,7 @@ extern "C" int g2ptq_compensate(void* stream, int variant, int64_t B, int64_t R,
   G2PTQ_HIP(hipStreamIsCapturing(s, &capture));
   const bool overlap = ws_bytes >= 2 * need && capture == hipStreamCaptureStatusNone && SB < C;
   SideStream side;
-  if (overlap) G2PTQ_TRY(side_stream(side));
+  if (overlap) G2PTQ_TRY(side_stream(s, side));
   float* Ebuf[2] = {static_cast<float*>(ws),
                     overlap ? static_cast<float*>(ws) + need / 4 : static_cast<float*>(ws)};
   const int64_t RC = R * C, CC = C * C;

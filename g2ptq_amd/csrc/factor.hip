@@ -18,6 +18,7 @@
 //      by recursive doubling from the NB inverses, then the block row
 //      X[p, 0:p] = −X_pp·(L[p, 0:p]·X[0:p, 0:p]) as two GEMMs
 //   4. un-reverse into U (upper, zeros below) with the reference's NaN check.
+#include <map>
 #include <mutex>
 
 #include "common.hpp"
@@ -170,14 +171,13 @@ FactorWs factor_ws(int64_t B, int64_t C) {
 
 }  // namespace
 
-int side_stream(SideStream& out) {
+int side_stream(hipStream_t caller, SideStream& out) {
   static std::mutex mu;
-  static SideStream cache[64];
+  static std::map<std::pair<int, hipStream_t>, SideStream> cache;
   int dev = 0;
   G2PTQ_HIP(hipGetDevice(&dev));
-  G2PTQ_CHECK(dev >= 0 && dev < 64, "side stream: device index %d", dev);
   std::lock_guard<std::mutex> lock(mu);
-  SideStream& c = cache[dev];
+  SideStream& c = cache[{dev, caller}];
   if (c.stream == nullptr) {
     G2PTQ_HIP(hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking));
     G2PTQ_HIP(hipStreamCreateWithFlags(&c.stream2, hipStreamNonBlocking));
@@ -282,7 +282,7 @@ extern "C" int g2ptq_inv_chol_upper(void* stream, const float* H, int64_t B, int
   // the trailing updates that read the block row completed before the panel
   // was factored, and those of the panel itself read only the rows below it.
   SideStream side;
-  G2PTQ_TRY(side_stream(side));
+  G2PTQ_TRY(side_stream(s, side));
   bool inv_pending = false;  // inverse work queued on stream2
   auto factor_panel = [&](int64_t k, int64_t kb) -> int {
     bool fused = false;

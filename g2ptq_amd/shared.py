@@ -42,6 +42,7 @@ class SharedInputHessian:
     def finalize(self):
         owner, idx = self.members[0]
         owner.H  # reading H folds any staged calibration tokens into it
+        self._factors = {}  # factors of an earlier calibration are stale
         for inst, j in self.members[1:]:
             if inst is owner and j == idx:
                 continue
@@ -78,7 +79,8 @@ class SharedInputHessian:
                   export_compressed_tensors=export_compressed_tensors, backend=backend,
                   graph=graph)
         q0 = insts[0].quantizer[0]
-        cfg = lambda q: (q.bits, bool(q.sym), bool(q.mse), q.norm, q.grid, q.maxshrink)
+        cfg = lambda q: (q.bits, bool(q.sym), bool(q.mse), q.norm, q.grid, q.maxshrink,
+                         bool(getattr(q, "hclip", False)))
         joint = (len(insts) > 1 and groupsize > 0 and not static_groups and not actorder
                  and not graph and not getattr(q0, "hclip", False)
                  and all(type(i) is GPTQ and getattr(i, "_shared_factor", None) is self

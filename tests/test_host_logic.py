@@ -98,6 +98,21 @@ def test_shared_input_hessian_membership():
     assert not hasattr(c, "_shared_factor")             # not every slot is a member
 
 
+def test_shared_input_factor_cache_invalidation():
+    """A re-finalized group forgets the factors of its earlier calibration, and
+    a member whose Hessian is replaced stops using the group's cached factor."""
+    from g2ptq_amd import GPTQ
+    a = GPTQ([torch.nn.Linear(8, 4, bias=False)])
+    b = GPTQ([torch.nn.Linear(8, 4, bias=False)])
+    sh = SharedInputHessian([(a, 0), (b, 0)])
+    sh.store_factor((0.01, False), torch.eye(8), 0.01)
+    sh.finalize()
+    assert sh.cached_factor((0.01, False)) is None
+    assert a._shared_factor is sh and b._shared_factor is sh
+    a.H = torch.ones(1, 8, 8)
+    assert not hasattr(a, "_shared_factor") and b._shared_factor is sh
+
+
 def test_weight_quantizer_deepcopy_is_independent():
     """make_group_quantizers deep-copies one quantizer per group: the copies are
     independent modules with the same configuration and buffers."""
