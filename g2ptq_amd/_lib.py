@@ -52,6 +52,9 @@ SIGNATURES = {
     "g2ptq_compensate_workspace": [_i32, _i64, _i64, _i64, _i64, _szp],
     "g2ptq_compensate": [_p, _i32, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _i32, _i32, _i64, _i32,
                          _i32, _f32, _f32, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _sz],
+    "g2ptq_compensate_noalloc": [_p, _i32, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _i32,
+                                 _i32, _i64, _i32, _i32, _f32, _f32, _p, _i64, _p, _p, _p, _p, _p,
+                                 _p, _p],
     "g2ptq_gptaq_p": [_p, _p, _p, _i64, _i64, _f32, _p, _p, _sz],
     "g2ptq_trust_region": [_p, _p, _p, _p, _p, _i64, _i64, _i64, _f32, _i32, _p, _p, _p, _p, _sz],
     "g2ptq_trust_region_workspace": [_i64, _i64, _i64, _szp],

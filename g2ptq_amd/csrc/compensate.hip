@@ -6,6 +6,7 @@
 // are fitted by the sweep itself) → fused sweep (one launch for every row of
 // every layer in the batch) → block-tail update of the remaining columns as
 // fp32 MFMA GEMMs.
+#include <mutex>
 #include <numeric>
 
 #include "sweep.hpp"
@@ -134,14 +135,17 @@ extern "C" int g2ptq_compensate_workspace(int variant, int64_t B, int64_t R, int
   return G2PTQ_OK;
 }
 
-extern "C" int g2ptq_compensate(void* stream, int variant, int64_t B, int64_t R, int64_t C,
-                                int64_t bs, float* W, const float* U, const float* P,
-                                const float* Z, float* GH, int bits, int sym, int64_t groupsize,
-                                int static_groups, int mse_grid, float mse_norm,
-                                float mse_maxshrink, const float* hdiag, int64_t hblocks,
-                                const int* colgroup,
-                                float* scale_tab, float* zero_tab, float* Q, float* Wint,
-                                float* Scale, int* flags, void* ws, size_t ws_bytes) {
+// The lazy-batch loop behind g2ptq_compensate and g2ptq_compensate_noalloc.
+// ws holds the error columns of one super-block (two with overlap allowed);
+// every column of it is written by a sweep before a tail reads it, so it
+// needs no clearing.
+static int compensate_impl(hipStream_t s, int variant, int64_t B, int64_t R, int64_t C,
+                           int64_t bs, float* W, const float* U, const float* P, const float* Z,
+                           float* GH, int bits, int sym, int64_t groupsize, int static_groups,
+                           int mse_grid, float mse_norm, float mse_maxshrink, const float* hdiag,
+                           int64_t hblocks, const int* colgroup, float* scale_tab,
+                           float* zero_tab, float* Q, float* Wint, float* Scale, int* flags,
+                           void* ws, size_t ws_bytes, bool allow_overlap) {
   G2PTQ_CHECK(W && U && scale_tab && zero_tab && Q, "compensate: null pointer");
   G2PTQ_CHECK(bits >= 2 && bits <= 16, "compensate: bits=%d unsupported", bits);
   G2PTQ_CHECK(bs >= 1 && bs <= kMaxBlock, "compensate: blocksize %lld not in [1, %d]",
@@ -150,7 +154,6 @@ extern "C" int g2ptq_compensate(void* stream, int variant, int64_t B, int64_t R,
   G2PTQ_CHECK(variant != G2PTQ_VARIANT_GPTAQ || P, "compensate: GPTAQ needs P");
   G2PTQ_CHECK(variant != G2PTQ_VARIANT_G2PTQ || (Z && GH), "compensate: G2PTQ needs Z and GH");
   G2PTQ_CHECK(B >= 1 && B < 65536 && R >= 1 && C >= 1, "compensate: bad sizes");
-  hipStream_t s = as_stream(stream);
   const int maxq = (1 << (bits - 1)) - 1;
   const bool dynamic = groupsize > 0 && !static_groups;
   int64_t SB = std::min(super_block(variant, bs, groupsize, static_groups),
@@ -166,7 +169,8 @@ extern "C" int g2ptq_compensate(void* stream, int variant, int64_t B, int64_t R,
   // "far" tail) runs on the side stream while the next super-block is swept.
   hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
   G2PTQ_HIP(hipStreamIsCapturing(s, &capture));
-  const bool overlap = ws_bytes >= 2 * need && capture == hipStreamCaptureStatusNone && SB < C;
+  const bool overlap = allow_overlap && ws_bytes >= 2 * need &&
+                       capture == hipStreamCaptureStatusNone && SB < C;
   SideStream side;
   if (overlap) G2PTQ_TRY(side_stream(s, side));
   float* Ebuf[2] = {static_cast<float*>(ws),
@@ -290,6 +294,67 @@ extern "C" int g2ptq_compensate(void* stream, int variant, int64_t B, int64_t R,
   }
   if (far_pending) G2PTQ_HIP(hipStreamWaitEvent(s, side.tailed, 0));
   return G2PTQ_OK;
+}
+
+extern "C" int g2ptq_compensate(void* stream, int variant, int64_t B, int64_t R, int64_t C,
+                                int64_t bs, float* W, const float* U, const float* P,
+                                const float* Z, float* GH, int bits, int sym, int64_t groupsize,
+                                int static_groups, int mse_grid, float mse_norm,
+                                float mse_maxshrink, const float* hdiag, int64_t hblocks,
+                                const int* colgroup,
+                                float* scale_tab, float* zero_tab, float* Q, float* Wint,
+                                float* Scale, int* flags, void* ws, size_t ws_bytes) {
+  return compensate_impl(as_stream(stream), variant, B, R, C, bs, W, U, P, Z, GH, bits, sym,
+                         groupsize, static_groups, mse_grid, mse_norm, mse_maxshrink, hdiag,
+                         hblocks, colgroup, scale_tab, zero_tab, Q, Wint, Scale, flags, ws,
+                         ws_bytes, true);
+}
+
+// Scratch memory of g2ptq_compensate_noalloc: the error columns of the loop,
+// in a file-scope device array instead of a caller workspace.  Each device
+// that runs the entry point holds its own copy until the process ends, and
+// every call on a device shares it.  In host code `scratch` is only a symbol
+// handle: its device address comes from hipGetSymbolAddress, once per device.
+static constexpr size_t kScratchBytes = size_t(32) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+static int scratch_address(void** out) {
+  static std::mutex mu;
+  static void* addr[64] = {};
+  int dev = 0;
+  G2PTQ_HIP(hipGetDevice(&dev));
+  G2PTQ_CHECK(dev >= 0 && dev < 64, "compensate_noalloc: device index %d", dev);
+  std::lock_guard<std::mutex> lock(mu);
+  if (addr[dev] == nullptr) {
+    void* p = nullptr;
+    G2PTQ_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    G2PTQ_CHECK(p != nullptr, "compensate_noalloc: no device address for the scratch array");
+    addr[dev] = p;
+  }
+  *out = addr[dev];
+  return G2PTQ_OK;
+}
+
+extern "C" int g2ptq_compensate_noalloc(void* stream, int variant, int64_t B, int64_t R,
+                                        int64_t C, int64_t bs, float* W, const float* U,
+                                        const float* P, const float* Z, float* GH, int bits,
+                                        int sym, int64_t groupsize, int static_groups,
+                                        int mse_grid, float mse_norm, float mse_maxshrink,
+                                        const float* hdiag, int64_t hblocks, const int* colgroup,
+                                        float* scale_tab, float* zero_tab, float* Q, float* Wint,
+                                        float* Scale, int* flags) {
+  G2PTQ_CHECK(B >= 1 && R >= 1 && bs >= 1 && bs <= kMaxBlock, "compensate_noalloc: bad sizes");
+  const size_t need = al256((size_t)B * R * bs * 4);
+  G2PTQ_CHECK(need <= kScratchBytes,
+              "compensate_noalloc: B*R*blocksize*4 = %zu bytes exceeds the %zu-byte scratch "
+              "array (at most %lld rows at blocksize %lld); use g2ptq_compensate",
+              need, kScratchBytes, (long long)(kScratchBytes / (4 * (size_t)bs)), (long long)bs);
+  void* ws = nullptr;
+  G2PTQ_TRY(scratch_address(&ws));
+  return compensate_impl(as_stream(stream), variant, B, R, C, bs, W, U, P, Z, GH, bits, sym,
+                         groupsize, static_groups, mse_grid, mse_norm, mse_maxshrink, hdiag,
+                         hblocks, colgroup, scale_tab, zero_tab, Q, Wint, Scale, flags, ws,
+                         kScratchBytes, false);
 }
 
 extern "C" int g2ptq_gptaq_p(void* stream, const float* Dx, const float* U, int64_t B, int64_t C,

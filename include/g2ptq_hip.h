@@ -230,6 +230,27 @@ int g2ptq_compensate(void* stream, int variant, int64_t B, int64_t R, int64_t C,
                      int64_t hblocks, const int* colgroup, float* scale_tab, float* zero_tab, float* Q,
                      float* Wint, float* Scale, int* flags, void* ws, size_t ws_bytes);
 
+/* g2ptq_compensate without a workspace argument, for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  No counterpart in the reference: it exists only for
+ * those callers.  The loop's error columns live in a file-scope device array
+ * of 32 MiB (33554432 bytes), one per device, held until the process ends;
+ * B·R·blocksize·4 must not exceed it (at blocksize 128, B·R ≤ 65536 rows),
+ * else the call fails with G2PTQ_ERR_ARG before touching the device.  With
+ * B·R·512·4 within it (B·R ≤ 16384) the loop runs as g2ptq_compensate does
+ * with a one-buffer workspace; beyond that it applies every 128-column block's
+ * tail separately.  It never overlaps tails on a side stream.  All calls on one
+ * device share the array: calls that overlap in time on one device (two
+ * streams or two host threads) race on it.  Everything else is as for
+ * g2ptq_compensate; nothing is allocated. */
+int g2ptq_compensate_noalloc(void* stream, int variant, int64_t B, int64_t R, int64_t C,
+                             int64_t blocksize, float* W, const float* U, const float* P,
+                             const float* Z, float* GH, int bits, int sym, int64_t groupsize,
+                             int static_groups, int mse_grid, float mse_norm,
+                             float mse_maxshrink, const float* hdiag, int64_t hblocks,
+                             const int* colgroup, float* scale_tab, float* zero_tab, float* Q,
+                             float* Wint, float* Scale, int* flags);
+
 /* GPTAQ P = alpha·triu(Dx·Uᵀ, 1)·U for B layers (gptq_utils/gptaq_utils.py:349-352). */
 int g2ptq_gptaq_p(void* stream, const float* Dx, const float* U, int64_t B, int64_t C, float alpha,
                   float* P, void* ws, size_t ws_bytes);
