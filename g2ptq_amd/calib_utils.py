@@ -1,21 +1,32 @@
 """Calibration capture feeding ``add_batch``.
 
-Drop-ins for the caches the reference's drivers hook into a block's forward
-and backward passes:
+The reference's drivers hook three caches into a block's forward and backward
+passes; these are drop-ins with the same constructors, hook methods and the
+attributes the drivers read (``fp_cache``, ``saliency_cache``,
+``gradients_cache``):
 
 - ``FPInputsCache`` (gptq_utils/gptaq_utils.py:442-555): the full-precision
-  input of every quantizable linear, the X_fp stream of ``GPTAQ.add_batch``;
-  linears that receive the identical tensor share one host buffer when
-  offloaded.  Kept on the device (the 288 GB of HBM hold the inputs of a
-  block at the benchmark sizes) unless ``offload_inps``.
-- ``SaliencyCache`` (gptq_utils/g2ptq_utils.py:586-681): per batch, the mean
-  of grad² over G channel groups of each linear's output gradient, the
-  saliency of ``G2PTQ`` / ``GPTQGuided``; ``g2ptq_group_mean_square``.
-- ``GradientCache`` (:684-766): the per-token running mean of each linear's
-  weight gradient, ``G2PTQ``'s gradients; ``g2ptq_running_mean_update``.
+  input of every quantizable linear, the X_fp stream of ``GPTAQ.add_batch``.
+- ``SaliencyCache`` (gptq_utils/g2ptq_utils.py:586-681): per batch and loss,
+  the mean of grad² over G consecutive channel groups of each linear's output
+  gradient — the saliencies of ``G2PTQ`` / ``GPTQGuided``.
+- ``GradientCache`` (gptq_utils/g2ptq_utils.py:684-766): per loss, the
+  per-token running mean of each linear's weight gradient — ``G2PTQ``'s
+  gradients.
 
-Hook wiring, autograd and the loss-weighted summaries stay in torch; the
-per-batch reductions run in the HIP library.
+How they are built here:
+
+- The inputs of a block stay in HBM (288 GB holds a block's calibration
+  inputs at the benchmark sizes) unless ``offload_inps``; then each
+  shared-input group owns one page-locked host slab that the group's batches
+  fill in arrival order through a copy stream, and a member's k-th batch is the
+  slab's k-th batch (the member that fires first for a batch copies it, the
+  others take the same rows after checking it is the same tensor).
+- The per-batch reductions are HIP kernels: ``g2ptq_group_mean_square`` for a
+  saliency batch, ``g2ptq_running_mean_update`` (in place) for a gradient.
+- Per-loss results live in ``_LossTable`` objects; summarizing folds them with
+  the loss weights in the weights' order (w₁·t₁ + w₂·t₂ + …, each product and
+  sum rounded once in fp32, as the reference's Python ``sum`` does).
 """
 import contextlib
 import functools
@@ -29,8 +40,9 @@ from . import _lib
 _DTYPE_CODE = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 
 
-def _cleanup():
-    """utils/memory_utils.cleanup_memory: collect garbage and return cached blocks."""
+def _release_memory():
+    """Drop unreachable tensors and return the allocator's cached blocks
+    (what utils/memory_utils.cleanup_memory does for the reference)."""
     gc.collect()
     if torch.cuda.is_available():
         torch.cuda.empty_cache()
@@ -43,108 +55,197 @@ def _dtype_code(t):
     return code
 
 
-def _module(full, name):
-    return full.get(name, full.get(name + ".module", None))
+def _lookup(modules, name):
+    """A linear by name; wrapped linears register as ``<name>.module``."""
+    m = modules.get(name)
+    return m if m is not None else modules.get(name + ".module")
+
+
+class _Hooks:
+    """Handles of registered hooks, removed together."""
+
+    def __init__(self):
+        self.handles = []
+
+    def forward(self, modules, names, fn):
+        for name in names:
+            self.handles.append(_lookup(modules, name).register_forward_hook(
+                functools.partial(fn, name=name)))
+
+    def remove(self):
+        while self.handles:
+            self.handles.pop().remove()
+
+
+# ---------------------------------------------------------------------------
+# Full-precision inputs (GPTAQ's X_fp)
+# ---------------------------------------------------------------------------
+
+class _Slab:
+    """Token rows of one shared-input group, batch after batch, in a host buffer.
+
+    ``take(k, x, name)`` returns the rows of the group's k-th batch: a member
+    asking for a batch nobody has stored yet stores ``x`` (k must be the next
+    batch); a member asking for a stored batch gets its rows after a check that
+    it received the very tensor the first member did."""
+
+    def __init__(self, members, rows, features, dtype):
+        self.members = members
+        self.buffer = torch.zeros(rows, features, dtype=dtype,
+                                  pin_memory=torch.cuda.is_available())
+        self.filled = 0
+        self.batches = []      # row views of the buffer, one per batch
+        self.origins = []      # (address, shape) of the tensor each batch came from
+        self._stream = None
+        self._pending = None   # event of the last device→host copy
+
+    def take(self, k, x, name):
+        origin = (x.data_ptr(), tuple(x.shape))
+        if k < len(self.batches):
+            if self.origins[k] != origin:
+                raise AssertionError(
+                    f"shared-input group {self.members} member {name!r} received a different "
+                    f"tensor {origin} than the member that fired first {self.origins[k]}; the "
+                    "group was declared as sharing one input tensor")
+            return self.batches[k]
+        n = x.shape[0]
+        if self.filled + n > self.buffer.shape[0]:
+            raise AssertionError(f"FP input buffer for group {self.members} overflowed "
+                                 f"({self.filled + n} > {self.buffer.shape[0]})")
+        rows = self.buffer[self.filled:self.filled + n]
+        self._store(rows, x)
+        self.filled += n
+        self.batches.append(rows)
+        self.origins.append(origin)
+        return rows
+
+    def _store(self, rows, x):
+        if not x.is_cuda:
+            rows.copy_(x)
+            return
+        # The copy runs on a stream of its own, after the work that produced x,
+        # so the forward pass is not held up by the device→host transfer.
+        if self._stream is None:
+            self._stream = torch.cuda.Stream(device=x.device)
+        self._stream.wait_stream(torch.cuda.current_stream(x.device))
+        with torch.cuda.stream(self._stream):
+            rows.copy_(x, non_blocking=True)
+            x.record_stream(self._stream)
+            self._pending = torch.cuda.Event()
+            self._pending.record(self._stream)
+
+    def settle(self):
+        """Wait until every stored batch has reached the host buffer."""
+        if self._pending is not None:
+            self._pending.synchronize()
+            self._pending = None
 
 
 class FPInputsCache:
-    """gptq_utils/gptaq_utils.py:442-555."""
+    """gptq_utils/gptaq_utils.py:442-555: ``fp_cache[name]`` lists the 2-D
+    full-precision inputs of linear ``name``, one per calibration batch.
+    Kept in HBM as the forward pass produced them, or, with ``offload_inps``,
+    copied into host slabs of ``nsamples·seqlen`` rows shared by each
+    ``shared_input_groups`` group (tuples of names; names outside this cache
+    are ignored, a name in no group forms its own)."""
 
     def __init__(self, sequential, modules, nsamples, seqlen, dtype, offload_inps=False,
                  shared_input_groups=None):
-        self.fp_cache = {}
-        self.fp_buffers = {}
-        self.cursor = {}
-        self.names = []
-        for names in sequential:
-            self.names += names
-        self.handles = []
+        self.names = [n for stage in sequential for n in stage]
         self.offload_inps = offload_inps
-        # group_key -> [remaining members, destination slice, source identity]
-        self._pending = {}
-        for name in self.names:
-            self.fp_cache[name] = []
-        self.groups, self.group_of = self._build_shared_input_groups(shared_input_groups)
-        if not self.offload_inps:
+        self.fp_cache = {n: [] for n in self.names}
+        self._hooks = _Hooks()
+        self.slabs = {}        # first member's name -> _Slab
+        self._slab_of = {}     # name -> its group's _Slab
+        if not offload_inps:
             return
-        total_tokens = nsamples * seqlen
-        pin = torch.cuda.is_available()
-        for group_key, group in self.groups.items():
-            in_features = {_module(modules, n).weight.shape[1] for n in group}
-            assert len(in_features) == 1, (
-                f"shared-input group {group} disagrees on in_features {in_features}; "
-                f"get_shared_input_groups grouped modules that cannot share an input tensor")
-            # page-locked, so the write-back below is a DMA at link speed
-            self.fp_buffers[group_key] = torch.zeros(total_tokens, in_features.pop(), dtype=dtype,
-                                                     pin_memory=pin)
-            self.cursor[group_key] = 0
+        known = set(self.names)
+        groups = [tuple(n for n in g if n in known) for g in (shared_input_groups or ())]
+        grouped = {n for g in groups for n in g}
+        groups = [g for g in groups if g] + [(n,) for n in self.names if n not in grouped]
+        for members in groups:
+            widths = {_lookup(modules, n).weight.shape[1] for n in members}
+            if len(widths) != 1:
+                raise AssertionError(
+                    f"shared-input group {members} disagrees on in_features {widths}; "
+                    "linears of different input widths cannot share an input tensor")
+            slab = _Slab(members, nsamples * seqlen, widths.pop(), dtype)
+            self.slabs[members[0]] = slab
+            for n in members:
+                self._slab_of[n] = slab
 
-    def _build_shared_input_groups(self, shared_input_groups):
-        """gptaq_utils.py:481-493: the layer's groups restricted to this cache's names."""
-        in_cache = set(self.names)
-        groups, group_of = {}, {}
-        for group in (shared_input_groups or ()):
-            members = tuple(n for n in group if n in in_cache)
-            if not members:
-                continue
-            groups[members[0]] = members
-            for name in members:
-                group_of[name] = members[0]
-        return groups, group_of
+    @property
+    def handles(self):
+        return self._hooks.handles
 
     def cache_fp_input(self, m, inp, out, name):
-        """gptaq_utils.py:495-532 (forward hook)."""
-        inp = inp[0].detach()
-        if len(inp.shape) == 3:
-            inp = inp.reshape((-1, inp.shape[-1]))
-        if not self.offload_inps:
-            self.fp_cache[name].append(inp)
-            return
-        group_key = self.group_of[name]
-        group = self.groups[group_key]
-        pending = self._pending.get(group_key)
-        identity = (inp.data_ptr(), tuple(inp.shape))
-        if pending is not None:
-            dst = pending[1]
-            assert pending[2] == identity, (
-                f"shared-input group {group} member {name!r} received a different tensor "
-                f"{identity} than the member that fired first {pending[2]}; "
-                f"get_shared_input_groups declared them as sharing an input but they do not")
-            pending[0] -= 1
-        else:
-            n = inp.shape[0]
-            cursor = self.cursor[group_key]
-            buffer = self.fp_buffers[group_key]
-            assert cursor + n <= buffer.shape[0], (
-                f"FP input buffer for group {group} overflowed ({cursor + n} > {buffer.shape[0]})")
-            dst = buffer[cursor:cursor + n]
-            dst.copy_(inp.contiguous())
-            self.cursor[group_key] = cursor + n
-            pending = self._pending[group_key] = [len(group) - 1, dst, identity]
-        self.fp_cache[name].append(dst)
-        if pending[0] <= 0:
-            del self._pending[group_key]
+        """Forward hook of linear ``name``: record this batch's input."""
+        x = inp[0].detach()
+        x = x.reshape(-1, x.shape[-1])
+        batches = self.fp_cache[name]
+        if self.offload_inps:
+            x = self._slab_of[name].take(len(batches), x, name)
+        batches.append(x)
 
     def add_hook(self, full):
-        for name in self.names:
-            self.handles.append(_module(full, name).register_forward_hook(
-                functools.partial(self.cache_fp_input, name=name)))
+        self._hooks.forward(full, self.names, self.cache_fp_input)
 
     def clear_hook(self):
-        for h in self.handles:
-            h.remove()
-        self.handles = []
+        """Remove the hooks; the offloaded batches are on the host afterwards."""
+        self._hooks.remove()
+        for slab in self.slabs.values():
+            slab.settle()
 
     def clear_cache(self):
+        for slab in self.slabs.values():
+            slab.settle()
         self.fp_cache = {}
-        self.fp_buffers = {}
-        self.cursor = {}
-        self._pending = {}
-        _cleanup()
+        self.slabs = {}
+        self._slab_of = {}
+        _release_memory()
 
+
+# ---------------------------------------------------------------------------
+# Per-loss tables and the loss-weighted fold
+# ---------------------------------------------------------------------------
+
+class _LossTable:
+    """One linear's results per loss type, in the order the losses first appear."""
+
+    def __init__(self):
+        self.by_loss = {}
+
+    def __contains__(self, loss):
+        return loss in self.by_loss
+
+    def get(self, loss, default=None):
+        return self.by_loss.get(loss, default)
+
+    def put(self, loss, value):
+        self.by_loss[loss] = value
+
+    def weighted(self, loss_weights):
+        """(weight, value) for every loss of ``loss_weights`` present, in its order."""
+        return [(w, self.by_loss[l]) for l, w in loss_weights.items() if l in self.by_loss]
+
+
+def _fold(pairs):
+    """w₁·t₁ + w₂·t₂ + … with every product and sum rounded once (no fused
+    multiply-add), the arithmetic of the reference's ``sum(w * t ...)``."""
+    (w, t), rest = pairs[0], pairs[1:]
+    acc = t * w
+    for w, t in rest:
+        acc = acc + t * w
+    return acc
+
+
+# ---------------------------------------------------------------------------
+# Output-gradient saliencies (G2PTQ / GuidedQuant)
+# ---------------------------------------------------------------------------
 
 def group_mean_square(grad, num_groups):
-    """``grad.float().pow(2).view(n, G, -1).mean(-1)`` of a (…, hidden) GPU tensor."""
+    """``grad.float().pow(2).view(n, G, -1).mean(-1)`` of a (…, hidden) GPU
+    tensor, in one HIP reduction (n = tokens, G consecutive channel groups)."""
     if not grad.is_cuda:
         raise RuntimeError("group_mean_square: the gradient must be a GPU tensor")
     g = grad.reshape(-1, grad.shape[-1])
@@ -163,76 +264,84 @@ def group_mean_square(grad, num_groups):
 
 
 class SaliencyCache:
-    """gptq_utils/g2ptq_utils.py:586-681."""
+    """gptq_utils/g2ptq_utils.py:586-681.  ``saliency_cache[name]`` maps a loss
+    type to the list of per-batch (tokens, G) saliencies; after
+    ``summarize_saliency`` it is the list of loss-weighted per-batch tensors."""
 
     def __init__(self, names, num_groups):
-        self.num_groups = num_groups
-        self.saliency_cache = {}
-        self.outs = {}
         self.names = names
-        for name in self.names:
-            self.saliency_cache[name] = {}   # loss -> list of per-batch saliency tensors
-            self.outs[name] = 0
-        self.handles = []
+        self.num_groups = num_groups
+        self.outs = {n: 0 for n in names}
+        self._tables = {n: _LossTable() for n in names}
+        self.saliency_cache = {n: self._tables[n].by_loss for n in names}
+        self._hooks = _Hooks()
         self.hooks_enabled = False
 
+    @property
+    def handles(self):
+        return self._hooks.handles
+
     def cache_saliency(self, module, inp, out, name):
+        """Forward hook: keep the linear's output for the backward pass."""
         self.outs[name] = out
 
     def grad_hook(self, grad, name, loss_type):
-        """:604-618: (n_tokens, G) mean of grad² per channel group."""
+        """One batch's output gradient → its (tokens, G) mean of squares."""
         if not self.hooks_enabled:
             return
-        self.saliency_cache[name].setdefault(loss_type, []).append(
-            group_mean_square(grad, self.num_groups))
-
-    def summarize_saliency(self, loss_weights):
-        """:620-640: one list of per-batch tensors, the loss-weighted sum."""
-        for name in self.names:
-            per_loss = self.saliency_cache[name]
-            present = [(l, w) for l, w in loss_weights.items() if l in per_loss]
-            if not present:
-                self.saliency_cache[name] = []
-                continue
-            lengths = [len(per_loss[l]) for l, _ in present]
-            assert len(set(lengths)) == 1, (
-                f"Saliency for '{name}' has mismatched per-loss batch counts: "
-                f"{ {l: len(per_loss[l]) for l, _ in present} }")
-            self.saliency_cache[name] = [sum(w * per_loss[l][i] for l, w in present)
-                                         for i in range(lengths[0])]
-
-    def set_forward_hook(self, full):
-        for name in self.names:
-            self.handles.append(_module(full, name).register_forward_hook(
-                functools.partial(self.cache_saliency, name=name)))
+        table = self._tables[name]
+        batches = table.get(loss_type)
+        if batches is None:
+            batches = []
+            table.put(loss_type, batches)
+        batches.append(group_mean_square(grad, self.num_groups))
 
     def backward(self, loss_tensor, loss_type="block", retain_graph=True):
-        """:654-672: gradients of the loss w.r.t. the cached outputs."""
-        names = [name for name in self.names if isinstance(self.outs[name], torch.Tensor)]
-        if not names:
+        """Differentiate ``loss_tensor`` w.r.t. every kept output and record
+        the saliencies under ``loss_type``."""
+        kept = [(n, self.outs[n]) for n in self.names if torch.is_tensor(self.outs[n])]
+        if not kept:
             return
         self.hooks_enabled = True
         try:
-            grads = torch.autograd.grad(loss_tensor, [self.outs[name] for name in names],
+            grads = torch.autograd.grad(loss_tensor, [o for _, o in kept],
                                         retain_graph=retain_graph, allow_unused=True)
-            for name, grad in zip(names, grads):
+            for (name, _), grad in zip(kept, grads):
                 if grad is not None:
                     self.grad_hook(grad, name=name, loss_type=loss_type)
         finally:
             self.hooks_enabled = False
 
+    def summarize_saliency(self, loss_weights):
+        """Fold the losses of ``loss_weights`` ({loss: weight}) batch by batch."""
+        for name in self.names:
+            table = self._tables[name]
+            pairs = table.weighted(loss_weights)
+            counts = {l: len(table.get(l)) for l in loss_weights if l in table}
+            if len(set(counts.values())) > 1:
+                raise AssertionError(
+                    f"Saliency for '{name}' has mismatched per-loss batch counts: {counts}")
+            n = len(pairs[0][1]) if pairs else 0
+            self.saliency_cache[name] = [_fold([(w, batches[i]) for w, batches in pairs])
+                                         for i in range(n)]
+
+    def set_forward_hook(self, full):
+        self._hooks.forward(full, self.names, self.cache_saliency)
+
     def clear_hook(self):
-        for h in self.handles:
-            h.remove()
-        self.handles = []
+        self._hooks.remove()
         self.hooks_enabled = False
 
     def clear_cache(self):
-        for name in self.names:
-            self.saliency_cache[name] = {}
-            self.outs[name] = 0
-        _cleanup()
+        self._tables = {n: _LossTable() for n in self.names}
+        self.saliency_cache = {n: self._tables[n].by_loss for n in self.names}
+        self.outs = {n: 0 for n in self.names}
+        _release_memory()
 
+
+# ---------------------------------------------------------------------------
+# Weight gradients (G2PTQ)
+# ---------------------------------------------------------------------------
 
 def running_mean_update(cache, grad, n_tokens, index):
     """``cache·(index/(index+1)) + grad.float()/(n_tokens·(index+1))`` in place
@@ -254,73 +363,84 @@ def running_mean_update(cache, grad, n_tokens, index):
     return cache
 
 
+class _RunningMean:
+    """Σ_k grad_k / (n_k · K) over K batches, updated in place on the device."""
+
+    def __init__(self):
+        self.value = None
+        self.count = 0
+
+    def update(self, grad, n_tokens):
+        self.value = running_mean_update(self.value, grad, n_tokens, self.count)
+        self.count += 1
+
+
 class GradientCache:
-    """gptq_utils/g2ptq_utils.py:684-766."""
+    """gptq_utils/g2ptq_utils.py:684-766.  ``gradients_cache[name]`` maps a
+    loss type to the running per-token mean of the linear's weight gradient;
+    after ``summarize_gradients`` it is their loss-weighted sum (0 when none)."""
 
     def __init__(self, names, num_groups):
-        self.num_groups = num_groups
-        self.gradients_cache = {}
-        self.index = {}
-        self.current_batch_tokens = {}
         self.names = names
-        for name in self.names:
-            self.gradients_cache[name] = {}   # loss -> running-mean gradient tensor
-            self.index[name] = {}             # loss -> accumulation count
-        self.handles = []
+        self.num_groups = num_groups
+        self.current_batch_tokens = {}
+        self._means = {n: {} for n in names}      # name -> loss -> _RunningMean
+        self.gradients_cache = {n: {} for n in names}
+        self._hooks = _Hooks()
         self.hooks_enabled = False
 
+    @property
+    def handles(self):
+        return self._hooks.handles
+
+    @property
+    def index(self):
+        """Batches accumulated per name and loss."""
+        return {n: {l: m.count for l, m in per.items()} for n, per in self._means.items()}
+
     def forward_hook(self, module, inp, out, name):
+        """Forward hook: the batch's token count (rows of the flattened input)."""
         x = inp[0]
         self.current_batch_tokens[name] = x.numel() // x.shape[-1]
 
     def cache_gradient(self, grad, name, loss_type):
-        """:704-714 (weight-gradient hook)."""
+        """Weight-gradient hook: fold this batch into the loss's running mean."""
         if not self.hooks_enabled:
             return
-        n_tokens = self.current_batch_tokens[name]
-        index = self.index[name].get(loss_type, 0)
-        cache = self.gradients_cache[name].get(loss_type)
-        if cache is not None and not isinstance(cache, torch.Tensor):
-            cache = None
-        self.gradients_cache[name][loss_type] = running_mean_update(cache, grad, n_tokens, index)
-        self.index[name][loss_type] = index + 1
+        mean = self._means[name].get(loss_type)
+        if mean is None:
+            mean = self._means[name][loss_type] = _RunningMean()
+        mean.update(grad, self.current_batch_tokens[name])
+        self.gradients_cache[name][loss_type] = mean.value
 
     def summarize_gradients(self, loss_weights):
-        """:716-724: one tensor per name, the loss-weighted sum (0 when none)."""
         for name in self.names:
-            per_loss = self.gradients_cache[name]
-            present = [(l, w) for l, w in loss_weights.items() if l in per_loss]
-            self.gradients_cache[name] = (sum(w * per_loss[l] for l, w in present)
-                                          if present else 0)
+            pairs = [(w, self._means[name][l].value) for l, w in loss_weights.items()
+                     if l in self._means[name]]
+            self.gradients_cache[name] = _fold(pairs) if pairs else 0
 
     def set_forward_hook(self, full):
-        for name in self.names:
-            self.handles.append(_module(full, name).register_forward_hook(
-                functools.partial(self.forward_hook, name=name)))
+        self._hooks.forward(full, self.names, self.forward_hook)
 
     @contextlib.contextmanager
     def set_backward_hook(self, full, loss_type="block"):
-        """:736-755: weight-gradient hooks for the duration of one backward."""
+        """Weight-gradient hooks on every linear for the duration of one backward."""
+        hooks = [_lookup(full, n).weight.register_hook(
+            functools.partial(self.cache_gradient, name=n, loss_type=loss_type))
+            for n in self.names]
         self.hooks_enabled = True
-        handles = []
-        for name in self.names:
-            handles.append(_module(full, name).weight.register_hook(
-                functools.partial(self.cache_gradient, name=name, loss_type=loss_type)))
         try:
             yield
         finally:
-            for h in handles:
-                h.remove()
             self.hooks_enabled = False
+            for h in hooks:
+                h.remove()
 
     def clear_hook(self):
-        for h in self.handles:
-            h.remove()
-        self.handles = []
+        self._hooks.remove()
         self.hooks_enabled = False
 
     def clear_cache(self):
-        for name in self.names:
-            self.gradients_cache[name] = {}
-            self.index[name] = {}
-        _cleanup()
+        self._means = {n: {} for n in self.names}
+        self.gradients_cache = {n: {} for n in self.names}
+        _release_memory()

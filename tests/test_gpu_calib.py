@@ -115,3 +115,40 @@ def test_saliency_and_gradient_caches_end_to_end(dev):
     sal.clear_cache()
     grd.clear_cache()
     assert sal.saliency_cache["up"] == {} and grd.gradients_cache["down"] == {}
+
+
+def test_fp_inputs_cache_offload_from_gpu(dev):
+    """gptaq_utils.py:442-555 with device activations: offloaded batches go to
+    page-locked host slabs through a copy stream and are complete once the hooks
+    are cleared; shared-input members get the same host rows; GPTAQ consumes
+    the FIFO exactly as it would the device tensors."""
+    from g2ptq_amd import GPTAQ
+    from g2ptq_amd.calib_utils import FPInputsCache
+    torch.manual_seed(11)
+    full = {n: nn.Linear(256, 64, bias=False).to(dev).to(torch.bfloat16) for n in ("q", "k")}
+    cache = FPInputsCache([["q", "k"]], full, nsamples=3, seqlen=128, dtype=torch.bfloat16,
+                          offload_inps=True, shared_input_groups=[("q", "k")])
+    cache.add_hook(full)
+    xs = [torch.randn(1, 128, 256, device=dev).bfloat16() for _ in range(3)]
+    for x in xs:
+        for n in ("q", "k"):
+            full[n](x)
+        x.mul_(0)  # overwrite the device tensor: the copy must have been ordered before
+    cache.clear_hook()
+    for n in ("q", "k"):
+        assert len(cache.fp_cache[n]) == 3
+        assert not cache.fp_cache[n][0].is_cuda and cache.fp_cache[n][0].is_pinned()
+    assert cache.fp_cache["k"][2].data_ptr() == cache.fp_cache["q"][2].data_ptr()
+    torch.manual_seed(11)
+    ref = [torch.randn(1, 128, 256, device=dev).bfloat16() for _ in range(3)]
+    for got, x in zip(cache.fp_cache["q"], ref):
+        assert torch.equal(got, x.reshape(128, 256).cpu())
+    # the FIFO feeds GPTAQ.add_batch like device tensors would
+    a, b = GPTAQ([full["q"]]), GPTAQ([full["q"]])
+    a.fp_inp[0] = list(cache.fp_cache["q"])
+    b.fp_inp[0] = [x.reshape(128, 256) for x in ref]
+    for x in ref:
+        a.add_batch(0, x, None)
+        b.add_batch(0, x, None)
+    assert torch.equal(a.dXXT, b.dXXT) and torch.equal(a.H, b.H)
+    cache.clear_cache()

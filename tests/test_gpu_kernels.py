@@ -542,3 +542,26 @@ def test_gemm_f32_accuracy_against_fp64(dev, K, b_trans):
     bound = A.double().abs() @ Bm.double().abs() + Cm.double().abs()
     err = ((D.cpu().double() - ref).abs() / bound).max().item()
     assert err <= 4e-7, err
+
+
+@pytest.mark.parametrize("sym,groupsize,C", [(True, 128, 384), (False, 128, 300), (False, -1, 96),
+                                             (True, 64, 200)])
+def test_fake_quantize_grouped_matches_oracle(dev, sym, groupsize, C):
+    """common_utils.py:33-44 in one launch: bit-exact against the oracle's group
+    by group fake quantization, ragged last group included."""
+    from g2ptq_amd import WeightQuantizer, fake_quantize_grouped, make_group_quantizers
+    from oracle import quant as oq
+    g = gen(1300 + C)
+    W = torch.randn(2, 48, C, generator=g) * 0.02
+    q = WeightQuantizer()
+    q.configure(3, perchannel=True, sym=sym)
+    hq = make_group_quantizers(q, C, groupsize)
+    oqs = oq.make_group_quantizers(oq.WeightQuantizer().configure(3, sym=sym), C, groupsize)
+    Wd = W.to(dev)
+    width = C if groupsize == -1 else groupsize
+    for k, (a, b) in enumerate(zip(hq, oqs)):
+        a.find_params(Wd[:, :, k * width:(k + 1) * width].reshape(96, -1))
+        b.find_params(W[:, :, k * width:(k + 1) * width].reshape(96, -1))
+    got = fake_quantize_grouped(hq, Wd, groupsize)
+    exp = oq.fake_quantize_grouped(oqs, W, groupsize)
+    assert_bitexact(got, exp, "fake_quantize_grouped")

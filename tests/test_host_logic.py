@@ -164,10 +164,11 @@ def test_fp_inputs_cache_shared_groups(offload):
         for got, x in zip(cache.fp_cache[n], xs):
             assert torch.equal(got, x.reshape(5, 16))
     if offload:
-        assert set(cache.fp_buffers) == {"q", "o"}
-        assert cache.cursor == {"q": 15, "o": 15}
+        assert set(cache.slabs) == {"q", "o"}
+        assert cache.slabs["q"].members == ("q", "k", "v")
+        assert cache.slabs["q"].filled == 15 and cache.slabs["o"].filled == 15
         assert cache.fp_cache["k"][1].data_ptr() == cache.fp_cache["q"][1].data_ptr()
-        assert torch.equal(cache.fp_buffers["q"][5:10], xs[1].reshape(5, 16))
+        assert torch.equal(cache.slabs["q"].buffer[5:10], xs[1].reshape(5, 16))
         # a member receiving another tensor than its group-mate is a spec error
         cache.add_hook(full)
         full["q"](xs[0])
@@ -175,7 +176,30 @@ def test_fp_inputs_cache_shared_groups(offload):
             full["k"](torch.randn(1, 5, 16))
         cache.clear_hook()
     cache.clear_cache()
-    assert cache.fp_cache == {} and cache.fp_buffers == {}
+    assert cache.fp_cache == {} and cache.slabs == {}
+
+
+def test_fp_inputs_cache_members_firing_out_of_order():
+    """A member's k-th batch is its group's k-th batch whatever order the
+    members fire in: q twice, then k twice, then v, all see the right rows."""
+    from g2ptq_amd.calib_utils import FPInputsCache
+    m = _fp_cache_model()
+    full = dict(m.items())
+    cache = FPInputsCache([["q", "k", "v"]], full, nsamples=2, seqlen=5, dtype=torch.float32,
+                          offload_inps=True, shared_input_groups=[("q", "k", "v")])
+    cache.add_hook(full)
+    xs = [torch.randn(1, 5, 16) for _ in range(2)]
+    for n in ("q", "k"):
+        for x in xs:
+            full[n](x)
+    full["v"](xs[0])
+    cache.clear_hook()
+    assert cache.slabs["q"].filled == 10
+    for n, k in (("q", 2), ("k", 2), ("v", 1)):
+        assert len(cache.fp_cache[n]) == k
+        for got, x in zip(cache.fp_cache[n], xs):
+            assert torch.equal(got, x.reshape(5, 16))
+        assert cache.fp_cache[n][0].data_ptr() == cache.slabs["q"].buffer.data_ptr()
 
 
 def test_fp_inputs_cache_overflow():
