@@ -99,3 +99,60 @@ def test_stack_cat_ragged_and_unaligned(dev):
         stack_cat([(a[0].to(dev),), (a[1].to(dev),)])
     with pytest.raises(RuntimeError):
         stack_cat([(a[0].to(dev), big[0].to(dev))])
+
+
+def test_grouped_experts_with_routed_inputs_match_oracle(dev):
+    """Config 4's structure at reduced size: 64 same-shape expert linears
+    quantized as ONE layer batch (common_utils.py:60-85), each with its own
+    routed 2-D calibration inputs (one sample per call, gptq_utils.py:115-126):
+    Zipf-uneven token counts, experts called with empty batches (a sample with
+    no tokens), one expert never called (no calibration: RTN).  GPTQ W4 sym
+    g128 against the oracle under the end-to-end parity protocol."""
+    from g2ptq_amd import GPTQ, WeightQuantizer, make_group_quantizers
+    from oracle import flows as oflows
+    from oracle import hessian as ohess
+    from tests._util import assert_flow_parity
+    E, R, C, batches, tb = 64, 64, 256, 8, 1024
+    g = gen(640)
+    sig = torch.exp(torch.randn(C, generator=g))
+    p = torch.arange(1, E + 1, dtype=torch.float64) ** -1.1
+    p[E - 1] = 0.0                                      # never routed, never called
+    p[E - 2] = 0.0                                      # called with empty batches only
+    lins = []
+    for e in range(E):
+        lin = nn.Linear(C, R, bias=False)
+        with torch.no_grad():
+            lin.weight.copy_(torch.randn(R, C, generator=g) * 0.02)
+        lins.append(lin.to(dev).to(torch.bfloat16))
+    W0 = torch.stack([l.weight.detach().float().cpu() for l in lins])
+    gq = GPTQ(lins)
+    q = WeightQuantizer()
+    q.configure(4, perchannel=True, sym=True)
+    gq.quantizer = make_group_quantizers(q, C, 128)
+    st = ohess.gptq_state(E, C)
+    counts = torch.zeros(E, dtype=torch.int64)
+    empties = 0
+    for _ in range(batches):
+        x = (torch.randn(tb, C, generator=g) * sig).bfloat16()
+        top = torch.multinomial(p.expand(tb, E), 2, replacement=False, generator=g)
+        for e in range(E - 1):
+            xe = x[(top == e).any(1)]
+            if xe.shape[0] == 0 and e != E - 2 and e % 3:
+                continue                                # most idle experts are not called
+            empties += xe.shape[0] == 0
+            counts[e] += xe.shape[0]
+            gq.add_batch(e, xe.to(dev), None)
+            ohess.gptq_add_batch(st, e, xe)
+    assert empties > 0 and counts[E - 2] == 0 and counts[:8].min() > counts[32:E - 2].max()
+    print(f"routed tokens per expert: {counts.tolist()}", flush=True)
+    assert torch.equal(gq.nsamples.cpu(), torch.tensor(st["nsamples"]))
+    H = st["H"].clone()
+    gq.fasterquant(blocksize=128, percdamp=0.01, groupsize=128, backend="hip",
+                   export_compressed_tensors=True)
+    torch.cuda.synchronize()
+    ref = oflows.gptq_fasterquant(W0, H, 4, True, groupsize=128)
+    He = H.clone()
+    idle = torch.tensor([bool((h == 0).all()) for h in He])
+    He[idle] = torch.eye(C)                             # the Hessian RTN minimizes
+    assert idle[E - 1] and idle[E - 2]
+    assert_flow_parity("64 routed experts", lins, gq.quantizer, ref, W0, He, 4, 128, False)
