@@ -1,10 +1,13 @@
 """GPU: the G2PTQ α autotune pattern (g2ptq_utils.py:1481-1577) — fasterquant re-run
 for several α with the weights and Hessians restored in between — reuses one
-factor per Hessian and gives bit-identical weights to a fresh instance per α."""
+factor per Hessian, gives bit-identical weights to a fresh instance per α, and
+matches the oracle at every α (trust-region β, end-to-end parity protocol)."""
 import pytest
 import torch
 
-from tests._util import gen
+from oracle import flows as oflows
+from oracle import hessian as ohess
+from tests._util import assert_beta_close, assert_flow_parity, gen
 
 pytestmark = pytest.mark.gpu
 
@@ -28,10 +31,14 @@ def _setup(dev, seed=900):
     q = WeightQuantizer()
     q.configure(3, perchannel=True, sym=True)
     gq.quantizer = make_group_quantizers(q, C, 128)
+    st = ohess.g2ptq_state(B, G, C)
     for i in range(0, T, ch):
-        xb = X[i:i + ch].reshape(1, ch, C).to(dev)
+        xb = X[i:i + ch].reshape(1, ch, C)
+        xd = xb.to(dev)
         for b in range(B):
-            gq.add_batch(b, xb, None)
+            gq.add_batch(b, xd, None)
+            ohess.g2ptq_add_batch(st, b, xb, sal[i:i + ch])
+    gq._oracle = (st, grad)
     return gq, layers, W
 
 
@@ -49,11 +56,18 @@ def test_alpha_sweep_reuses_factor_and_matches_fresh(dev, monkeypatch):
     saved_H = gq.H.cpu().clone()
     q0 = gq.quantizer[0]
     results = {}
+    st, grad = gq._oracle
     for alpha in (0.05, 0.1, 0.2):
         gq.quantizer = make_group_quantizers(q0, 256, 128)
-        gq.fasterquant(blocksize=128, percdamp=0.01, groupsize=128, alpha=alpha, backend="hip")
+        gq.fasterquant(blocksize=128, percdamp=0.01, groupsize=128, alpha=alpha, backend="hip",
+                       export_compressed_tensors=True)
         torch.cuda.synchronize()
         results[alpha] = torch.stack([l.weight.detach().cpu().clone() for l in layers])
+        ref = oflows.g2ptq_fasterquant(W0.float(), st["H"].clone(), grad, st["act_square"], 3,
+                                       True, 2, groupsize=128, alpha=alpha)
+        assert_beta_close(gq._beta.cpu(), ref["beta"], f"autotune alpha={alpha}")
+        assert_flow_parity(f"autotune alpha={alpha}", layers, gq.quantizer, ref, W0.float(),
+                           st["H"].reshape(-1, 256, 256), 3, 128, False)
         with torch.no_grad():
             for b, l in enumerate(layers):
                 l.weight.copy_(W0[b].to(dev))
