@@ -50,6 +50,10 @@ def parse():
     p.add_argument("--steps", type=int, default=3)
     p.add_argument("--warmup", type=int, default=1)
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-kernel-rates", action="store_true",
+                   help="skip the standalone factor / sweep / tail-product timings")
+    p.add_argument("--no-g2ptq", action="store_true",
+                   help="skip the config-3 G2PTQ block reported beside the benchmark line")
     p.add_argument("--tokens", type=int, default=N_TOKENS)
     p.add_argument("--calibrate-copy", action="store_true",
                    help="run one 1 GiB device copy first (the known-size reference kernel "
@@ -127,6 +131,8 @@ def workload_cfg3(dev, steps, warmup):
     lins = {name: _linear(R, C, torch.bfloat16, g, dev) for name, (R, C, _) in LINEARS.items()}
     w0 = {k: v.weight.detach().clone() for k, v in lins.items()}
     grads, sals = {}, {}
+    # the Student-t and χ² draws use the device's default generator: seed it
+    torch.cuda.manual_seed(42 + 2)
     t_dist = torch.distributions.StudentT(torch.tensor(3.0, device=dev))
     for name, (R, C, key) in LINEARS.items():
         tau = t_dist.sample((R,)).abs()
@@ -381,11 +387,13 @@ def run_step(acts, layers, w0, n_tokens, ev):
     return hess_ms, quant_ms
 
 
-def cpu_baseline():
+def cpu_baseline(acts, w0):
     """The oracle (torch-CPU restatement of the reference arithmetic) on a bounded
-    sample, scaled to one block: Hessians on token slices (cost ∝ N), the factor
-    chain at C=4096 (×6 linears) and C=14336 extrapolated by C³ from C=4096 when
-    too slow, compensation on row slices scaled by rows (rows are independent)."""
+    sample of the benchmark's own inputs (slices of the GPU-generated
+    activations and weights, copied to the host), scaled to one block:
+    Hessians on token slices (cost ∝ N), the factor chain on the C=4096
+    slice Hessian (×6 linears; C=14336 extrapolated by C³), compensation of
+    weight-row slices with that factor (rows are independent: scaled by rows)."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from oracle import compensate as ocomp
     from oracle import factor as ofactor
@@ -394,12 +402,12 @@ def cpu_baseline():
     cores = len(os.sched_getaffinity(0))
     cores = min(cores, int(os.environ.get("OMP_NUM_THREADS", cores)))
     torch.set_num_threads(cores)
-    g = torch.Generator().manual_seed(SEED)
     t_total = 0.0
     parts = {}
-    # Hessians: the reference accumulates one per linear (7), C=4096 ×6, C=14336 ×1.
-    for C, slice_tok, count in ((4096, 8192, 6), (14336, 2048, 1)):
-        x = (torch.randn(1, slice_tok, C, generator=g) * torch.exp(torch.randn(C, generator=g))).bfloat16()
+    # Hessians: the reference accumulates one per linear (7): C=4096 ×6, C=14336 ×1.
+    for key, slice_tok, count in (("qkv", 8192, 6), ("down", 2048, 1)):
+        x = acts[key][:slice_tok].cpu().unsqueeze(0)
+        C = x.shape[-1]
         st = ohess.gptq_state(1, C)
         t = time.perf_counter()
         ohess.gptq_add_batch(st, 0, x)
@@ -408,23 +416,23 @@ def cpu_baseline():
         t_total += dt
         if C == 4096:
             H4096 = st["H"][0]
-    # Factor chain at C=4096 (6 linears), C=14336 by C³ scaling (estimate).
+    # Factor chain (damp, cholesky, cholesky_inverse, cholesky) at C=4096 (6
+    # linears); C=14336 by C³ scaling (estimate).
     t = time.perf_counter()
-    ofactor.damp_chol_inv_upper(H4096 + 1e-3 * torch.eye(4096), 0.01)
+    U, _ = ofactor.damp_chol_inv_upper(H4096, 0.01)
     dt = time.perf_counter() - t
     parts["factor_C4096"] = dt * 6
     parts["factor_C14336_est"] = dt * (14336 / 4096) ** 3
     t_total += parts["factor_C4096"] + parts["factor_C14336_est"]
-    U = torch.linalg.cholesky(torch.linalg.inv(H4096.double() + 0.05 * torch.eye(4096, dtype=torch.float64)), upper=True).float()
-    # Compensation: rows are independent; time a row slice and scale by rows.
+    # Compensation of the real weight rows; rows are independent, so a row
+    # slice scales by rows.  C=14336 reuses the C=4096 factor block-diagonally
+    # (the sweep's cost does not depend on U's values).
     rows_c4096 = 4096 + 2048 + 4096 + 2 * 14336
-    for C, rslice, rows_total in ((4096, 256, rows_c4096), (14336, 64, 4096)):
-        W = torch.randn(1, rslice, C, generator=g) * 0.02
+    for name, rslice, rows_total in (("q_proj", 256, rows_c4096), ("down_proj", 64, 4096)):
+        W = w0[name][:rslice].float().cpu().unsqueeze(0)
+        C = W.shape[-1]
         Uc = U if C == 4096 else torch.block_diag(*([U] * 4))[:C, :C].contiguous()
-        qs = []
-        for _ in range(C // GROUPSIZE):
-            q = oquant.WeightQuantizer().configure(BITS, sym=SYM)
-            qs.append(q)
+        qs = [oquant.WeightQuantizer().configure(BITS, sym=SYM) for _ in range(C // GROUPSIZE)]
         t = time.perf_counter()
         ocomp.gptq_compensation(W, Uc.unsqueeze(0), qs, 128, GROUPSIZE, False, None)
         dt = (time.perf_counter() - t) * rows_total / rslice
@@ -432,11 +440,106 @@ def cpu_baseline():
         t_total += dt
     return {"value": t_total, "unit": "s", "cores": cores, "kind": "port",
             "cpu": _cpu_model(),
-            "sample": ("oracle (torch-CPU, reference op order): Hessian on 8192/2048-token slices "
-                       "scaled by N (7 per-linear Hessians as the reference computes them); "
-                       "damp+chol+cholesky_inverse+chol at C=4096 x6, C=14336 extrapolated by C^3; "
-                       "compensation on 256/64-row slices scaled by rows"),
+            "sample": ("oracle (torch-CPU, reference op order) on slices of this run's own "
+                       "inputs: Hessian on 8192 (C=4096) / 2048 (C=14336) tokens scaled by N, "
+                       "7 per-linear Hessians as the reference computes them; "
+                       "damp+chol+cholesky_inverse+chol of the C=4096 slice Hessian x6, "
+                       "C=14336 extrapolated by C^3; compensation of 256/64 weight rows "
+                       "scaled by rows"),
             "parts_s": {k: round(v, 3) for k, v in parts.items()}}
+
+
+def kernel_rates(dev, acts, reps=10):
+    """Standalone launches of the path's other kernels at the step's shapes,
+    timed with HIP events on the launching stream (mean of ``reps``): the
+    factor (2·C³/3 algorithmic flop), the compensation sweep of one 128-column
+    block (20 bytes per weight: W read; Q, codes, scales and errors written),
+    and the compensation's trailing tail product (2·R·N·K flop)."""
+    from g2ptq_amd import GPTQ, _core, _lib
+    stream = torch.cuda.current_stream()
+    out = {}
+
+    def timed(fn):
+        fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    for key, C in (("qkv", 4096), ("down", 14336)):
+        lin = torch.nn.Linear(C, 64, bias=False, device=dev, dtype=torch.bfloat16)
+        gq = GPTQ([lin])
+        for t0 in range(0, 65536, 8192):
+            gq.add_batch(0, acts[key][t0:t0 + 8192].view(-1, SEQ, C), None)
+        H = gq.H.clone()
+        _core.prepare_hessian(H, torch.zeros(1, 64, C, device=dev))
+        U = torch.empty_like(H)
+        info = torch.zeros(1, dtype=torch.int32, device=dev)
+        ws = _lib.workspace(_lib.query_size("g2ptq_factor_workspace", 1, C), dev)
+        ms = timed(lambda: _lib.call("g2ptq_inv_chol_upper", _core.stream(), _lib.ptr(H), 1, C,
+                                     0.01, None, _lib.ptr(U), _lib.ptr(info), _lib.ptr(ws),
+                                     ws.numel()))
+        out[f"factor_C{C}"] = {"ms": round(ms, 3),
+                               "tflops": round(2 * C ** 3 / 3 / (ms / 1e3) / 1e12, 1)}
+        R = 4096
+        W = torch.randn(1, R, C, device=dev) * 0.02
+        # one 128-column block in the reference's transposed block layout
+        wt = W[:, :, :128].transpose(1, 2).contiguous()
+        hinv = U[:, :128, :128].contiguous()
+        sc = torch.full_like(wt, 0.01)
+        zr = torch.zeros_like(wt)
+        it, et = torch.empty_like(wt), torch.empty_like(wt)
+        w_keep = wt.clone()
+
+        def sweep():
+            wt.copy_(w_keep)
+            _lib.call("g2ptq_block_sweep", _core.stream(), 0, 1, 128, R, 7, _lib.ptr(wt),
+                      _lib.ptr(hinv), None, _lib.ptr(sc), _lib.ptr(zr), None, None, None,
+                      _lib.ptr(it), _lib.ptr(et), None)
+        copy_ms = timed(lambda: wt.copy_(w_keep))
+        ms = timed(sweep) - copy_ms
+        nbytes = R * 128 * 20
+        out[f"sweep_R{R}_C{C}"] = {"us_per_block": round(ms * 1e3, 1),
+                                   "GBps": round(nbytes / (ms / 1e3) / 1e9, 1),
+                                   "frac_hbm": round(nbytes / (ms / 1e3) / 8e12, 4)}
+        K, N = 512, C - 512
+        E = torch.randn(1, R, K, device=dev) * 1e-3
+        Wt = torch.randn(1, R, C, device=dev)
+        ms = timed(lambda: _lib.call(
+            "g2ptq_gemm_f32", _core.stream(), R, N, K, 1, _lib.ptr(E), K, R * K,
+            _lib.ptr(U[0, :K, K:]), C, C * C, 0, _lib.ptr(Wt[0, :, K:]), C, R * C,
+            _lib.ptr(Wt[0, :, K:]), C, R * C, -1.0, 1.0))
+        out[f"tail_gemm_R{R}_N{N}_K{K}"] = {"ms": round(ms, 3),
+                                            "tflops": round(2 * R * N * K / (ms / 1e3) / 1e12, 1)}
+        del gq, H, U, W, Wt
+    torch.cuda.empty_cache()
+    return out
+
+
+def g2ptq_block(dev, steps=2, warmup=1):
+    """Config 3 (the north-star workload with G2PTQ compensation) in the default
+    run: seconds per block and per stage over ``steps`` timed steps."""
+    step, desc = workload_cfg3(dev, steps, warmup)
+
+    def ev():
+        return [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+
+    for _ in range(warmup):
+        step(ev)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    recs = [step(ev) for _ in range(steps)]
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps
+    h = sum(e[0].elapsed_time(e[1]) for e, _ in recs) / steps
+    qz = sum(e[2].elapsed_time(e[3]) for e, _ in recs) / steps
+    return {"workload": desc, "sec_per_block": round(wall, 4), "steps": steps, "warmup": warmup,
+            "stages_ms": {"hessian": round(h, 2), "factor_and_compensation": round(qz, 2)},
+            "hessian_tflops": round(recs[0][1] / (h / 1e3) / 1e12, 1),
+            "hessian_flop_convention": "2*N*C^2 per (linear, row group) weighted Hessian"}
 
 
 def traffic_per_launch():
@@ -548,8 +651,14 @@ def main():
                                   for k, v in sorted(shapes.items())}},
         "cpu_baseline": None,
     }
+    if not args.no_kernel_rates:
+        out["kernels"] = kernel_rates(dev, acts)
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline()
+        out["cpu_baseline"] = cpu_baseline(acts, w0)
+    if not args.no_g2ptq:
+        del acts, layers, w0
+        torch.cuda.empty_cache()
+        out["g2ptq_block"] = g2ptq_block(dev)
     print(json.dumps(out), flush=True)
 
 
