@@ -9,7 +9,12 @@
 // 2⁻²³·|a·b|: six bf16 MFMAs per 16 k instead of eight fp32 ones, each a
 // quarter of the cycles (8192³: 158–165 TFLOP/s against 125 on fp32 MFMAs).
 // Its error is below the fp32 MFMA path's (measured max |err| / (|A|·|B|)
-// 2.8e-7 vs 3.6e-7 at K = 1536, both against fp64).
+// 2.8e-7 vs 3.6e-7 at K = 1536, both against fp64).  With B given N×K both
+// operands are k-contiguous and each element is split once per workgroup, as
+// its 16-k slab is stored to LDS as three bf16 planes; with B given K×N the
+// fp32 slab is staged and each wave splits the fragments it reads (a split at
+// store time would have to transpose B into 2-byte LDS writes).  Both orders
+// sum the same six products in the same order, so the results are identical.
 //
 // A is M×K row-major; B is K×N row-major, or N×K row-major (b_kcontig).  The
 // same kernel serves every fp32 product of the path: block-tail updates of the
@@ -51,6 +56,15 @@ __device__ __forceinline__ void split3_2(f32x2 f, bf16x2& h, bf16x2& m, bf16x2& 
   const f32x2 r2 = r1 - __builtin_convertvector(m, f32x2);
   l = __builtin_convertvector(r2, bf16x2);
 }
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void split4(float4 u, bf16x4& h, bf16x4& m, bf16x4& l) {
+  bf16x2 h0, h1, m0, m1, l0, l1;
+  split3_2(f32x2{u.x, u.y}, h0, m0, l0);
+  split3_2(f32x2{u.z, u.w}, h1, m1, l1);
+  h = __builtin_shufflevector(h0, h1, 0, 1, 2, 3);
+  m = __builtin_shufflevector(m0, m1, 0, 1, 2, 3);
+  l = __builtin_shufflevector(l0, l1, 0, 1, 2, 3);
+}
 __device__ __forceinline__ void split3(float4 u0, float4 u1, bf16x8& h, bf16x8& m, bf16x8& l) {
   bf16x2 h0, h1, h2, h3, m0, m1, m2, m3, l0, l1, l2, l3;
   split3_2(f32x2{u0.x, u0.y}, h0, m0, l0);
@@ -67,6 +81,12 @@ __device__ __forceinline__ void split3(float4 u0, float4 u1, bf16x8& h, bf16x8& 
 
 constexpr int BK = 32;
 constexpr int PK = 36;   // [row][k] pitch (floats)
+// Split path: 16-k slabs, each operand staged in LDS as three bf16 planes
+// (h, m, l) split once per workgroup as the slab is stored.  A plane is
+// [row][k] (B's [n][k]) with a 24-element (48-byte) pitch: the 16-byte reads
+// of 8 consecutive rows start 12 banks apart and hit distinct bank quads.
+constexpr int SK = 16;
+constexpr int SP = 24;
 constexpr int GH = 8;    // tile-rows per group of the tile order
 
 // Tile id → (tm, tn): groups of GH tile-rows walked column by column.
@@ -249,6 +269,7 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmF32 g, int64_t tm,
       }                                                                                        \
     }                                                                                          \
   } while (0)
+
   // Split products: per 16-k step each lane's 8 consecutive k of a row (A) or
   // column (B) are split into three bf16 fragments, and the six products
   // whose pieces sum to at most 2⁻¹⁶ relative go through the bf16 matrix
@@ -289,32 +310,160 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmF32 g, int64_t tm,
     }                                                                                          \
   } while (0)
 
-  // Slabs are processed in pairs; a trailing odd slab and the prefetches past
-  // the end load zeros (k >= K is masked), which add nothing.
-  const int nk = K > klo ? (int)cdiv(K - klo, (int64_t)BK) : 0;
-  const int nk2 = (nk + 1) & ~1;
-  if (nk2 > 0) {
-    GF_LOAD(xa, xb, 0);
-    GF_STORE(xa, xb, 0);
-    GF_LOAD(xa, xb, 1);
-    GF_LOAD(ya, yb, 2);
-  }
-  __syncthreads();
-  for (int kt = 0; kt < nk2; kt += 2) {
-    __builtin_amdgcn_sched_barrier(0);
-    if (SPLIT) GF_MMA_SPLIT(0); else GF_MMA(0);  // slab kt
-    GF_STORE(xa, xb, 1);    // slab kt+1
-    GF_LOAD(xa, xb, kt + 3);
-    __builtin_amdgcn_sched_barrier(0);
+  if constexpr (SPLIT && B_KCONTIG) {
+    // 16-k slabs through three bf16 planes per operand, four slabs of global
+    // loads in flight (register sets s0..s3 hold the slabs ≡ 0..3 mod 4).
+    constexpr int PL = TILE * SP;                          // bf16 per plane
+    static_assert(2 * 3 * PL * 2 <= (int)sizeof(As) && 2 * 3 * PL * 2 <= (int)sizeof(Bs),
+                  "split planes exceed the operand buffers");
+    __bf16* const Ap = reinterpret_cast<__bf16*>(&As[0][0]);  // [buf][plane][row][SP]
+    __bf16* const Bp = reinterpret_cast<__bf16*>(&Bs[0][0]);
+    constexpr int RS = TILE / 64;                          // float4 per thread ([row][k])
+    constexpr int KPT = SK * TILE / 256;                   // B as K×N: k per thread (8 or 4)
+    const int sa_row = tid >> 2, sa_kq = (tid & 3) * 4;
+    const int sb_n = tid % TILE, sb_k = (tid / TILE) * KPT;
+    const uint32_t b_off = B_KCONTIG ? 0u : (uint32_t)(sb_k * g.ldb + sb_n);
+    float4 ra0[RS], ra1[RS], ra2[RS], ra3[RS];
+    float4 rb0[RS], rb1[RS], rb2[RS], rb3[RS];
+    float bs0[KPT], bs1[KPT], bs2[KPT], bs3[KPT];
+#define GS_LOAD(RA_, RB_, BS_, slab)                                                           \
+  do {                                                                                         \
+    const int64_t k0_ = klo + (int64_t)(slab) * SK;                                            \
+    _Pragma("unroll") for (int i_ = 0; i_ < RS; ++i_)                                          \
+      RA_[i_] = ld4(A, g.lda, m0 + sa_row + 64 * i_, k0_ + sa_kq, M, K);                       \
+    if (B_KCONTIG) {                                                                           \
+      _Pragma("unroll") for (int i_ = 0; i_ < RS; ++i_)                                        \
+        RB_[i_] = ld4(B, g.ldb, n0 + sa_row + 64 * i_, k0_ + sa_kq, N, K);                     \
+    } else {                                                                                   \
+      /* uniform row base + a 32-bit per-thread offset */                                      \
+      const bool n_ok_ = n0 + sb_n < N;                                                        \
+      _Pragma("unroll") for (int c_ = 0; c_ < KPT; ++c_) {                                     \
+        const float* row_ = B + (k0_ + c_) * g.ldb + n0;                                       \
+        BS_[c_] = (n_ok_ && k0_ + sb_k + c_ < K) ? row_[b_off] : 0.f;                          \
+      }                                                                                        \
+    }                                                                                          \
+  } while (0)
+#define GS_STORE(RA_, RB_, BS_, buf)                                                           \
+  do {                                                                                         \
+    _Pragma("unroll") for (int i_ = 0; i_ < RS; ++i_) {                                        \
+      bf16x4 h_, m_, l_;                                                                       \
+      split4(RA_[i_], h_, m_, l_);                                                             \
+      __bf16* p_ = Ap + (buf) * 3 * PL + (sa_row + 64 * i_) * SP + sa_kq;                      \
+      *reinterpret_cast<bf16x4*>(p_) = h_;                                                     \
+      *reinterpret_cast<bf16x4*>(p_ + PL) = m_;                                                \
+      *reinterpret_cast<bf16x4*>(p_ + 2 * PL) = l_;                                            \
+    }                                                                                          \
+    if (B_KCONTIG) {                                                                           \
+      _Pragma("unroll") for (int i_ = 0; i_ < RS; ++i_) {                                      \
+        bf16x4 h_, m_, l_;                                                                     \
+        split4(RB_[i_], h_, m_, l_);                                                           \
+        __bf16* p_ = Bp + (buf) * 3 * PL + (sa_row + 64 * i_) * SP + sa_kq;                    \
+        *reinterpret_cast<bf16x4*>(p_) = h_;                                                   \
+        *reinterpret_cast<bf16x4*>(p_ + PL) = m_;                                              \
+        *reinterpret_cast<bf16x4*>(p_ + 2 * PL) = l_;                                          \
+      }                                                                                        \
+    } else {                                                                                   \
+      _Pragma("unroll") for (int q_ = 0; q_ < KPT / 4; ++q_) {                                 \
+        bf16x4 h_, m_, l_;                                                                     \
+        split4(make_float4(BS_[4 * q_], BS_[4 * q_ + 1], BS_[4 * q_ + 2], BS_[4 * q_ + 3]),    \
+               h_, m_, l_);                                                                    \
+        __bf16* p_ = Bp + (buf) * 3 * PL + sb_n * SP + sb_k + 4 * q_;                          \
+        *reinterpret_cast<bf16x4*>(p_) = h_;                                                   \
+        *reinterpret_cast<bf16x4*>(p_ + PL) = m_;                                              \
+        *reinterpret_cast<bf16x4*>(p_ + 2 * PL) = l_;                                          \
+      }                                                                                        \
+    }                                                                                          \
+  } while (0)
+    // The six cross products whose pieces sum to at most 2⁻¹⁶ relative (the
+    // three dropped ones are below 2⁻²³ of |a·b|), smallest first.
+#define GS_MMA(buf)                                                                            \
+  do {                                                                                         \
+    const __bf16* a_ = Ap + (buf) * 3 * PL;                                                    \
+    const __bf16* b_ = Bp + (buf) * 3 * PL;                                                    \
+    bf16x8 ah[NBLK], am[NBLK], al[NBLK], bh[NBLK], bm[NBLK], bl[NBLK];                         \
+    _Pragma("unroll") for (int i = 0; i < NBLK; ++i) {                                         \
+      const int o_ = (wm * WT + i * 32 + lr) * SP + lh * 8;                                    \
+      ah[i] = *reinterpret_cast<const bf16x8*>(a_ + o_);                                       \
+      am[i] = *reinterpret_cast<const bf16x8*>(a_ + PL + o_);                                  \
+      al[i] = *reinterpret_cast<const bf16x8*>(a_ + 2 * PL + o_);                              \
+    }                                                                                          \
+    _Pragma("unroll") for (int j = 0; j < NBLK; ++j) {                                         \
+      const int o_ = (wn * WT + j * 32 + lr) * SP + lh * 8;                                    \
+      bh[j] = *reinterpret_cast<const bf16x8*>(b_ + o_);                                       \
+      bm[j] = *reinterpret_cast<const bf16x8*>(b_ + PL + o_);                                  \
+      bl[j] = *reinterpret_cast<const bf16x8*>(b_ + 2 * PL + o_);                              \
+    }                                                                                          \
+    _Pragma("unroll") for (int i = 0; i < NBLK; ++i)                                           \
+    _Pragma("unroll") for (int j = 0; j < NBLK; ++j) {                                         \
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[i], bh[j], acc[i][j], 0, 0, 0);   \
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bl[j], acc[i][j], 0, 0, 0);   \
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am[i], bm[j], acc[i][j], 0, 0, 0);   \
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am[i], bh[j], acc[i][j], 0, 0, 0);   \
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bm[j], acc[i][j], 0, 0, 0);   \
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[i], bh[j], acc[i][j], 0, 0, 0);   \
+    }                                                                                          \
+  } while (0)
+    // Step t: the MMAs of slab t (buffer t % 2), then slab t+1 goes from its
+    // register set into the other buffer and that set loads slab t+5.  Slabs
+    // past the end load zeros and skip their MMAs.
+#define GS_STEP(t, RA_, RB_, BS_)                                                              \
+  do {                                                                                         \
+    __builtin_amdgcn_sched_barrier(0);                                                         \
+    if ((t) < nk) GS_MMA((t) & 1);                                                             \
+    GS_STORE(RA_, RB_, BS_, ((t) + 1) & 1);                                                    \
+    GS_LOAD(RA_, RB_, BS_, (t) + 5);                                                           \
+    __builtin_amdgcn_sched_barrier(0);                                                         \
+    __syncthreads();                                                                           \
+  } while (0)
+    const int nk = K > klo ? (int)cdiv(K - klo, (int64_t)SK) : 0;
+    if (nk > 0) {
+      GS_LOAD(ra0, rb0, bs0, 0);
+      GS_STORE(ra0, rb0, bs0, 0);
+      GS_LOAD(ra1, rb1, bs1, 1);
+      GS_LOAD(ra2, rb2, bs2, 2);
+      GS_LOAD(ra3, rb3, bs3, 3);
+      GS_LOAD(ra0, rb0, bs0, 4);
+    }
     __syncthreads();
+    for (int kt = 0; kt < nk; kt += 4) {
+      GS_STEP(kt, ra1, rb1, bs1);
+      GS_STEP(kt + 1, ra2, rb2, bs2);
+      GS_STEP(kt + 2, ra3, rb3, bs3);
+      GS_STEP(kt + 3, ra0, rb0, bs0);
+    }
     __builtin_amdgcn_sched_barrier(0);
-    if (SPLIT) GF_MMA_SPLIT(1); else GF_MMA(1);  // slab kt+1
-    GF_STORE(ya, yb, 0);    // slab kt+2
-    GF_LOAD(ya, yb, kt + 4);
-    __builtin_amdgcn_sched_barrier(0);
+#undef GS_LOAD
+#undef GS_STORE
+#undef GS_MMA
+#undef GS_STEP
+  } else {
+    // Slabs are processed in pairs; a trailing odd slab and the prefetches
+    // past the end load zeros (k >= K is masked), which add nothing.
+    const int nk = K > klo ? (int)cdiv(K - klo, (int64_t)BK) : 0;
+    const int nk2 = (nk + 1) & ~1;
+    if (nk2 > 0) {
+      GF_LOAD(xa, xb, 0);
+      GF_STORE(xa, xb, 0);
+      GF_LOAD(xa, xb, 1);
+      GF_LOAD(ya, yb, 2);
+    }
     __syncthreads();
+    for (int kt = 0; kt < nk2; kt += 2) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (SPLIT) GF_MMA_SPLIT(0); else GF_MMA(0);  // slab kt
+      GF_STORE(xa, xb, 1);    // slab kt+1
+      GF_LOAD(xa, xb, kt + 3);
+      __builtin_amdgcn_sched_barrier(0);
+      __syncthreads();
+      __builtin_amdgcn_sched_barrier(0);
+      if (SPLIT) GF_MMA_SPLIT(1); else GF_MMA(1);  // slab kt+1
+      GF_STORE(ya, yb, 0);    // slab kt+2
+      GF_LOAD(ya, yb, kt + 4);
+      __builtin_amdgcn_sched_barrier(0);
+      __syncthreads();
+    }
+    __builtin_amdgcn_sched_barrier(0);
   }
-  __builtin_amdgcn_sched_barrier(0);
 #undef GF_LOAD
 #undef GF_STORE
 #undef GF_MMA
@@ -460,6 +609,9 @@ int gemm_f32(hipStream_t stream, const GemmF32& g) {
   // (about 1.3x the fp32 MFMA rate, and no less accurate); the short-K updates
   // of the factor's panels are latency-bound and keep the fp32 MFMAs.
   const bool split = g.pot_nb == 0 && g.K >= 128;
+  G2PTQ_CHECK(!split || g.b_kcontig || g.ldb < (1ll << 27),
+              "gemm_f32: ldb %lld too large for the split path's 32-bit row offsets",
+              (long long)g.ldb);
   if (t128 * nz >= 512) launch_gemm<128>(stream, g, vec, nz, split);
   else launch_gemm<64>(stream, g, vec, nz, split);
   G2PTQ_LAUNCHED();
