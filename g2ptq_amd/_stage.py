@@ -17,9 +17,20 @@ long K runs.
 Planes per kind: 0 (GPTQ) Xᵀ; 1 (GPTAQ) Xᵀ and the bf16 hi/lo parts of
 (X_fp − X)ᵀ; 2 (weighted, G groups) Xᵀ and the hi/lo parts of (x·s[t,g])ᵀ.
 
-The buffer grows ×4 at flush points (it is empty then, so nothing is copied),
-up to ``budget_bytes`` (default 8 GiB, env ``G2PTQ_STAGE_BYTES``): MI355X's
-288 GB of HBM holds a whole decoder block's calibration set staged.
+The first buffer holds 32 batches of the first batch's size (at least 65536
+tokens): a calibration run is typically 32 or more batches, so its whole set
+is usually one flush.  Later buffers grow ×4 at flush points (the buffer is
+empty then, so nothing is copied), all up to ``budget_bytes`` (default a
+quarter of the device's memory, at most 64 GiB; env ``G2PTQ_STAGE_BYTES``):
+MI355X's 288 GB of HBM holds a whole decoder block's calibration set staged.
+A read of the Hessian (the calibration is complete, or the caller looks at
+it) flushes and frees the buffer; a later ``add_batch`` allocates a new one.
+
+The buffer's row pitch is a multiple of 2048 tokens plus 1024 (an odd
+multiple of 2 KiB): power-of-two-like pitches alias the rows of a Gram panel
+onto few memory channels (measured on MI355X, C = 14336, K = 204800: a
+528384-byte pitch, 512 KiB + 4 KiB, made the Gram 20 % slower than 518 to
+560 KiB pitches).
 """
 import os
 
@@ -27,7 +38,13 @@ import torch
 
 from . import _lib
 
-DEFAULT_BUDGET = int(os.environ.get("G2PTQ_STAGE_BYTES", str(8 << 30)))
+# Staging budget in bytes per stager; None: a quarter of the device's memory,
+# at most 64 GiB.
+DEFAULT_BUDGET = (int(os.environ["G2PTQ_STAGE_BYTES"]) if os.environ.get("G2PTQ_STAGE_BYTES")
+                  else None)
+_MAX_BUDGET = 64 << 30
+_FIRST_BATCHES = 32   # batches of the first batch's size that the first buffer holds
+_PITCH_SKEW = 1024    # tokens added to every buffer's pitch (see above)
 
 # Optional launch timing: when a list, every Gram flush appends
 # (start event, end event, algorithmic flops, K, C), events recorded on the
@@ -54,7 +71,10 @@ class GramStager:
         self.G = groups
         self.planes = {KIND_GPTQ: 1, KIND_GPTAQ: 3, KIND_WEIGHTED: 1 + 2 * groups}[kind]
         self.rows = _lib.query_size_i64("g2ptq_hessian_stage_rows", columns)
-        budget = DEFAULT_BUDGET if budget_bytes is None else budget_bytes
+        budget = budget_bytes if budget_bytes is not None else DEFAULT_BUDGET
+        if budget is None:
+            total = torch.cuda.get_device_properties(torch.device(device)).total_memory
+            budget = min(_MAX_BUDGET, total // 4)
         per_token = self.planes * self.rows * 2
         self.max_tokens = max(_GRAM_PAD * 2, budget // per_token // _GRAM_PAD * _GRAM_PAD)
         self.buf = None
@@ -70,12 +90,15 @@ class GramStager:
 
     def reserve(self, T):
         """With the buffer empty (just flushed because T more tokens did not fit,
-        or never allocated): allocate the first buffer, or one 4× larger, up to
-        the budget."""
+        or never allocated): allocate the first buffer (room for 32 batches of T
+        tokens, at least 65536), or one 4× larger, up to the budget."""
         assert self.k == 0
         need = _ceil(T, 64) + _GRAM_PAD
-        cap = max(_FIRST_TOKENS, need) if self.buf is None else max(need, self.cap * 4)
-        cap = _ceil(max(need, min(cap, self.max_tokens)), _GRAM_PAD)
+        if self.buf is None:
+            cap = max(_FIRST_TOKENS, need, _FIRST_BATCHES * _ceil(T, 64) + _GRAM_PAD)
+        else:
+            cap = max(need, self.cap * 4)
+        cap = _ceil(max(need, min(cap, self.max_tokens)), _GRAM_PAD) + _PITCH_SKEW
         if self.buf is not None and cap <= self.cap:
             return
         self.buf = None
@@ -168,12 +191,15 @@ def bump(owner, name, idx, amount):
 
 def staged_attr(name):
     """A Hessian attribute whose reads first fold every staged token into it
-    (the owner's ``_flush_staged``), and whose deletion (``= None``) folds them
-    in and then drops the staging buffers."""
+    (the owner's ``_flush_staged``) and free the staging buffers, and whose
+    deletion (``= None``) folds them in and then drops the buffers."""
     private = "_" + name
 
     def get(self):
         self._flush_staged()
+        for st in getattr(self, "_stagers", None) or ():
+            if st is not None and st.buf is not None:
+                st.release()
         return getattr(self, private, None)
 
     def set(self, value):
