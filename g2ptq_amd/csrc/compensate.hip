@@ -30,18 +30,33 @@ __global__ void triu1_kernel(float* t, int64_t C) {
   }
 }
 
-// diag(A⁻¹)[c] = Σ_i U[i][c]² (A⁻¹ = UᵀU), one thread per column.
-__global__ void inv_diag_kernel(const float* __restrict__ U, int64_t C, float* dA) {
+// diag(A⁻¹)[c] = Σ_i U[i][c]² (A⁻¹ = UᵀU): a workgroup per 64 columns,
+// four row phases per column (rows i ≡ p mod 4, four loads in flight per
+// thread), the phases summed in a fixed order.
+__global__ __launch_bounds__(256) void inv_diag_kernel(const float* __restrict__ U, int64_t C,
+                                                       float* dA) {
+  __shared__ float part[4][64];
   const int64_t b = blockIdx.y;
-  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (c >= C) return;
+  const int cl = threadIdx.x & 63, ph = threadIdx.x >> 6;
+  const int64_t c = (int64_t)blockIdx.x * 64 + cl;
   const float* Ub = U + b * C * C;
-  float s = 0.f;
-  for (int64_t i = 0; i <= c; ++i) {
-    const float u = Ub[i * C + c];
-    s += u * u;
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+  if (c < C) {
+    int64_t i = ph;
+    for (; i + 12 <= c; i += 16) {
+      const float u0 = Ub[i * C + c], u1 = Ub[(i + 4) * C + c];
+      const float u2 = Ub[(i + 8) * C + c], u3 = Ub[(i + 12) * C + c];
+      s0 += u0 * u0; s1 += u1 * u1; s2 += u2 * u2; s3 += u3 * u3;
+    }
+    for (; i <= c; i += 4) {
+      const float u = Ub[i * C + c];
+      s0 += u * u;
+    }
   }
-  dA[b * C + c] = s;
+  part[ph][cl] = (s0 + s1) + (s2 + s3);
+  __syncthreads();
+  if (ph == 0 && c < C)
+    dA[b * C + c] = (part[0][cl] + part[1][cl]) + (part[2][cl] + part[3][cl]);
 }
 
 __device__ float block_sum(float v, float* red) {
@@ -420,14 +435,16 @@ extern "C" int g2ptq_trust_region(void* stream, const float* Grad, const float* 
   a.A = Grad; a.lda = C; a.sA = RC;
   a.B = U; a.ldb = C; a.sB = CC; a.b_kcontig = 1;
   a.D = Z; a.ldd = C; a.sD = RC;
+  a.tri = 2;  // B(k, n) = U[n][k] is zero for k < n
   G2PTQ_TRY(gemm_f32(s, a));
   GemmF32 b;  // GH ← GA = T1 · U = Grad · A⁻¹
   b.M = Rg; b.N = C; b.K = C; b.batch = BG;
   b.A = Z; b.lda = C; b.sA = RC;
   b.B = U; b.ldb = C; b.sB = CC;
   b.D = GH; b.ldd = C; b.sD = RC;
+  b.tri = 8;  // B = U is zero below the diagonal
   G2PTQ_TRY(gemm_f32(s, b));
-  hipLaunchKernelGGL(inv_diag_kernel, dim3((unsigned)cdiv(C, 256), (unsigned)BG), dim3(256), 0, s,
+  hipLaunchKernelGGL(inv_diag_kernel, dim3((unsigned)cdiv(C, 64), (unsigned)BG), dim3(256), 0, s,
                      U, C, dA);
   G2PTQ_LAUNCHED();
   hipLaunchKernelGGL(trust_row_kernel, dim3((unsigned)(BG * Rg)), dim3(256), 0, s, Grad, Q0, W0,
