@@ -127,10 +127,17 @@ using namespace g2ptq;
 // every earlier block's error term before it is quantized, and a dynamic
 // group never straddles a super-block boundary (the width is a multiple of
 // the group size), so find_params sees the same, fully updated columns.
-// G2PTQ's tail subtracts bs·GH with a GH that changes every block, so it
-// keeps one block per super-block.
+// G2PTQ's block tail also subtracts bs·GH with a GH that every block's own
+// tail updates (GH −= Z_b·U_b).  Summed over the m blocks of a super-block,
+// the columns after it receive
+//   m·bs·GH₀ + Σ_b (E2_b − bs·(m−1−b)·Z_b)·U_b   and   GH −= Σ_b Z_b·U_b,
+// with GH₀ their GH at the super-block's start (the blocks' own tails touch
+// only the super-block's columns) and E2_b = err − z·(bs−1−j) the block
+// operand of g2ptq_utils.py:329-346: so the sweep also writes
+// E3_b = err − z·(bs−1−j + bs·(m−1−b)), and the far tail is one K = m·bs
+// product with γ = −m·bs, like the other variants'.
 static int64_t super_block(int variant, int64_t bs, int64_t groupsize, int static_groups) {
-  if (variant == G2PTQ_VARIANT_G2PTQ) return bs;
+  (void)variant;
   int64_t unit = bs;
   if (groupsize > 0 && !static_groups) unit = bs / std::gcd(bs, groupsize) * groupsize;
   return unit >= 512 ? unit : unit * (512 / unit);
@@ -144,9 +151,11 @@ extern "C" int g2ptq_compensate_workspace(int variant, int64_t B, int64_t R, int
   // (a dynamic group size that is coprime to the block size is bounded by C),
   // twice: the error columns of consecutive super-blocks alternate between
   // two buffers so that one's far tail can run while the next is swept.
+  // G2PTQ adds one block's near-tail operand (E2, below).
   const int64_t bs = std::max<int64_t>(blocksize, 1);
-  const int64_t widest = variant == G2PTQ_VARIANT_G2PTQ ? bs : std::max<int64_t>(512, bs);
-  *bytes = 2 * al256((size_t)B * R * widest * 4);
+  const int64_t widest = std::max<int64_t>(512, bs);
+  *bytes = 2 * al256((size_t)B * R * widest * 4) +
+           (variant == G2PTQ_VARIANT_G2PTQ ? al256((size_t)B * R * bs * 4) : 0);
   return G2PTQ_OK;
 }
 
@@ -173,23 +182,30 @@ static int compensate_impl(hipStream_t s, int variant, int64_t B, int64_t R, int
   const bool dynamic = groupsize > 0 && !static_groups;
   int64_t SB = std::min(super_block(variant, bs, groupsize, static_groups),
                         cdiv(C, bs) * bs);
+  // G2PTQ with super-blocks: the near tails read each block's E2 from a
+  // buffer of its own; the super-block buffer holds the far-tail E3.
+  const bool g2 = variant == G2PTQ_VARIANT_G2PTQ;
   size_t need = al256((size_t)B * R * SB * 4);
-  if (ws_bytes < need && SB > bs) {  // a smaller workspace: fall back to per-block tails
+  size_t need2 = (g2 && SB > bs) ? al256((size_t)B * R * bs * 4) : 0;
+  if (ws_bytes < need + need2 && SB > bs) {  // a smaller workspace: per-block tails
     SB = bs;
     need = al256((size_t)B * R * SB * 4);
+    need2 = 0;
   }
-  G2PTQ_CHECK(ws && ws_bytes >= need, "compensate: workspace %zu < %zu", ws_bytes, need);
+  G2PTQ_CHECK(ws && ws_bytes >= need + need2, "compensate: workspace %zu < %zu", ws_bytes,
+              need + need2);
   // Lookahead: with room for two error buffers, and outside graph capture,
   // the tail of a super-block beyond the next super-block's columns (the
   // "far" tail) runs on the side stream while the next super-block is swept.
   hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
   G2PTQ_HIP(hipStreamIsCapturing(s, &capture));
-  const bool overlap = allow_overlap && ws_bytes >= 2 * need &&
+  const bool overlap = allow_overlap && ws_bytes >= 2 * need + need2 &&
                        capture == hipStreamCaptureStatusNone && SB < C;
   SideStream side;
   if (overlap) G2PTQ_TRY(side_stream(s, side));
   float* Ebuf[2] = {static_cast<float*>(ws),
                     overlap ? static_cast<float*>(ws) + need / 4 : static_cast<float*>(ws)};
+  float* E2buf = need2 ? static_cast<float*>(ws) + (overlap ? 2 : 1) * need / 4 : nullptr;
   const int64_t RC = R * C, CC = C * C;
 
   // W[:, :, c0:c1] -= Ecols · U[k0:k1, c0:c1]  (+ GPTAQ: += Q[:, :, k0:k1] · P[k0:k1, c0:c1]),
@@ -204,8 +220,9 @@ static int compensate_impl(hipStream_t s, int variant, int64_t B, int64_t R, int
     t.D = W + c0; t.ldd = C; t.sD = RC;
     t.alpha = -1.f; t.beta = 1.f;
     if (variant == G2PTQ_VARIANT_G2PTQ) {
-      // W -= bs·GH[:, c0:] + (E − Z·D)·U_slab, with E2 = E − Z·D from the sweep.
-      t.X = GH + c0; t.ldx = C; t.sX = RC; t.gamma = -(float)bs;
+      // W -= (k1 − k0)·GH[:, c0:] + E·U_slab: a block's tail with E = E2
+      // (k1 − k0 = bs), a super-block's with E = E3.
+      t.X = GH + c0; t.ldx = C; t.sX = RC; t.gamma = -(float)(k1 - k0);
     }
     G2PTQ_TRY(gemm_f32(q, t));
     if (variant == G2PTQ_VARIANT_GPTAQ) {
@@ -278,8 +295,14 @@ static int compensate_impl(hipStream_t s, int variant, int64_t B, int64_t R, int
       a.CW = nullptr;
       if (variant == G2PTQ_VARIANT_G2PTQ) {
         a.E = nullptr;
-        a.E2 = Eb; a.e2b = R * SB; a.e2r = SB; a.e2c = 1;
         a.dist0 = bs - 1;
+        if (E2buf) {
+          a.E2 = E2buf; a.e2b = R * bs; a.e2r = bs; a.e2c = 1;
+          a.E3 = Eb; a.e3b = R * SB; a.e3r = SB;
+          a.dist3 = bs - 1 + (s1 - i2);
+        } else {
+          a.E2 = Eb; a.e2b = R * SB; a.e2r = SB; a.e2c = 1;
+        }
       } else {
         a.E = Eb; a.eb = R * SB; a.er = SB; a.ec = 1;
         a.E2 = nullptr;
@@ -287,7 +310,7 @@ static int compensate_impl(hipStream_t s, int variant, int64_t B, int64_t R, int
       a.flags = flags;
       G2PTQ_TRY(launch_sweep(s, variant, a, B));
       // The block's tail inside the super-block.
-      if (i2 < s1) G2PTQ_TRY(tail(Eb, SB, i1, i2, i2, s1));
+      if (i2 < s1) G2PTQ_TRY(E2buf ? tail(E2buf, bs, i1, i2, i2, s1) : tail(Eb, SB, i1, i2, i2, s1));
     }
     // The super-block's errors applied to every later column at once.
     if (s1 < C) {

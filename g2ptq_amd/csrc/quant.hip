@@ -291,6 +291,7 @@ __global__ __launch_bounds__(64) void sweep_kernel(SweepArgs a) {
   float* Eo = a.E ? a.E + b * a.eb + r * a.er : nullptr;
   float* So = a.Sc ? a.Sc + b * a.cb + r * a.cr : nullptr;
   float* E2 = (V == 2 && a.E2) ? a.E2 + b * a.e2b + r * a.e2r : nullptr;
+  float* E3 = (V == 2 && a.E3) ? a.E3 + b * a.e3b + r * a.e3r : nullptr;
 
   int bad = 0;
   float last_x = 0.f;
@@ -420,6 +421,13 @@ __global__ __launch_bounds__(64) void sweep_kernel(SweepArgs a) {
                 e2[q] = __fsub_rn(ev[q], __fmul_rn(zg[kk + q], (float)(a.dist0 - (c + q))));
               *reinterpret_cast<float4*>(E2 + c) = make_float4(e2[0], e2[1], e2[2], e2[3]);
             }
+            if (V == 2 && E3) {
+              float e3[4];
+#pragma unroll
+              for (int q = 0; q < 4; ++q)
+                e3[q] = __fsub_rn(ev[q], __fmul_rn(zg[kk + q], (float)(a.dist3 - (c + q))));
+              *reinterpret_cast<float4*>(E3 + c) = make_float4(e3[0], e3[1], e3[2], e3[3]);
+            }
           }
         }
       } else {
@@ -434,6 +442,8 @@ __global__ __launch_bounds__(64) void sweep_kernel(SweepArgs a) {
             if (So) So[(int64_t)j * a.cc] = sv[jj];
             if (V == 2 && E2)
               E2[(int64_t)j * a.e2c] = __fsub_rn(ev, __fmul_rn(zg[jj], (float)(a.dist0 - j)));
+            if (V == 2 && E3)
+              E3[(int64_t)j * a.e2c] = __fsub_rn(ev, __fmul_rn(zg[jj], (float)(a.dist3 - j)));
             if (V == 2 && GHo) GHo[(int64_t)j * a.gc] = gb[jj];
           }
         }
@@ -622,6 +632,7 @@ __global__ __launch_bounds__(256) void sweep4_kernel(SweepArgs a) {
   float* Eo = a.E ? a.E + b * a.eb + r * a.er : nullptr;
   float* So = a.Sc ? a.Sc + b * a.cb + r * a.cr : nullptr;
   float* E2 = (V == 2 && a.E2) ? a.E2 + b * a.e2b + r * a.e2r : nullptr;
+  float* E3 = (V == 2 && a.E3) ? a.E3 + b * a.e3b + r * a.e3r : nullptr;
 
   int bad = 0;
   float last_x = 0.f;
@@ -808,6 +819,7 @@ __global__ __launch_bounds__(256) void sweep4_kernel(SweepArgs a) {
         if (Eo) Eo[(int64_t)j * a.ec] = eb[s];
         if (So) So[(int64_t)j * a.cc] = sv[s];
         if (V == 2 && E2) E2[(int64_t)j * a.e2c] = __fsub_rn(eb[s], __fmul_rn(zg[s], (float)(a.dist0 - j)));
+        if (V == 2 && E3) E3[(int64_t)j * a.e2c] = __fsub_rn(eb[s], __fmul_rn(zg[s], (float)(a.dist3 - j)));
         if (V == 2 && GHo) GHo[(int64_t)j * a.gc] = gb[s];
       }
     }
@@ -826,7 +838,8 @@ bool sweep_vec_ok(const SweepArgs& a) {
   };
   return ok(a.W, a.wb, a.wr, a.wc) && ok(a.Q, a.qb, a.qr, a.qc) && ok(a.I, a.ib, a.ir, a.ic) &&
          ok(a.E, a.eb, a.er, a.ec) && ok(a.Sc, a.cb, a.cr, a.cc) &&
-         ok(a.E2, a.e2b, a.e2r, a.e2c) && ok(a.GH, a.gb, a.gr, a.gc) && a.GHout == nullptr;
+         ok(a.E2, a.e2b, a.e2r, a.e2c) && ok(a.E3, a.e3b, a.e3r, a.e2c) &&
+         ok(a.GH, a.gb, a.gr, a.gc) && a.GHout == nullptr;
 }
 
 template <int V>

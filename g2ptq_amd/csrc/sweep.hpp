@@ -36,6 +36,9 @@ struct SweepArgs {
   float* CW; int64_t cwb, cwr;                 // GPTAQ last pre-quant column (nullable)
   float* E2; int64_t e2b, e2r, e2c;            // G2PTQ: err - z*(dist0 - j) (nullable)
   int64_t dist0;                               // G2PTQ: blocksize - 1
+  // G2PTQ, super-block far tail: err - z*(dist3 - j) (nullable; same strides
+  // as E2); dist3 = dist0 + the columns of the super-block after this block.
+  float* E3; int64_t e3b, e3r; int64_t dist3;
   int* flags;
 };
 

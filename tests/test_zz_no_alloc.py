@@ -80,12 +80,13 @@ def test_noalloc_matches_compensate_twice(dev, case):
     for i, (B, R, C) in enumerate((first, second)):
         print(f"noalloc case v{variant} w{bits} g{gs} call {i} B={B} R={R} C={C}", flush=True)
         inputs = _inputs(B, R, C, 900 + 10 * i + variant)
-        # the super-block width the scratch allows, one buffer (no side-stream lookahead)
-        sb = 128 if variant == 2 else 512
-        if B * R * sb * 4 > SCRATCH:
-            sb = BS
+        # the super-block width the scratch allows, one buffer (no side-stream
+        # lookahead); G2PTQ also holds one block's near-tail operand
+        sb, extra = 512, (_al256(B * R * BS * 4) if variant == 2 else 0)
+        if _al256(B * R * sb * 4) + extra > SCRATCH:
+            sb, extra = BS, 0
         ref = _run("g2ptq_compensate", variant, inputs, bits, sym, gs,
-                   ws_bytes=_al256(B * R * sb * 4))
+                   ws_bytes=_al256(B * R * sb * 4) + extra)
         got = _run("g2ptq_compensate_noalloc", variant, inputs, bits, sym, gs)
         for k in ref:
             assert_bitexact(got[k], ref[k], f"call {i} {k}")
