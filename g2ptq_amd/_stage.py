@@ -45,6 +45,7 @@ DEFAULT_BUDGET = (int(os.environ["G2PTQ_STAGE_BYTES"]) if os.environ.get("G2PTQ_
 _MAX_BUDGET = 64 << 30
 _FIRST_BATCHES = 32   # batches of the first batch's size that the first buffer holds
 _PITCH_SKEW = 1024    # tokens added to every buffer's pitch (see above)
+_FREE_MARGIN = 4 << 30  # device memory a new buffer leaves free
 
 # Optional launch timing: when a list, every Gram flush appends
 # (start event, end event, algorithmic flops, K, C), events recorded on the
@@ -102,6 +103,15 @@ class GramStager:
         if self.buf is not None and cap <= self.cap:
             return
         self.buf = None
+        # Stay within what the device has free (other stagers of the same layer
+        # group, the caller's tensors): shrink a large buffer rather than fail.
+        per_token = self.planes * self.rows * 2
+        free, _ = torch.cuda.mem_get_info(self.device)
+        cached = torch.cuda.memory_reserved(self.device) - torch.cuda.memory_allocated(self.device)
+        avail = free + cached - _FREE_MARGIN
+        if cap * per_token > avail:
+            cap = _ceil(max(need, avail // per_token - _PITCH_SKEW - _GRAM_PAD),
+                        _GRAM_PAD) + _PITCH_SKEW
         self.buf = torch.empty(self.planes, self.rows, cap, dtype=torch.bfloat16,
                                device=self.device)
         self.cap = cap

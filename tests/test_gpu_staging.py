@@ -183,3 +183,32 @@ def test_staged_guided_across_flushes(dev, monkeypatch):
     _weighted_close(gq.H[0], st["H"][0], "guided")
     act = gq.act_square[0].cpu()
     assert (act - st["act_square"][0]).abs().max() <= 1e-5 * st["act_square"][0].abs().max()
+
+
+def test_staging_buffer_shrinks_to_free_memory(dev, monkeypatch):
+    """With little device memory free, the first buffer is cut to what fits
+    (at least one batch), and the Hessian still equals the oracle's."""
+    import torch as _t
+    from g2ptq_amd import GPTQ, _lib, _stage
+    C = 384
+    rows = _lib.query_size_i64("g2ptq_hessian_stage_rows", C)
+    real = _t.cuda.mem_get_info
+
+    def tight(device=None):
+        free, total = real(device)
+        # room for about 12000 tokens beyond the margin, whatever torch has cached
+        cached = _t.cuda.memory_reserved(device) - _t.cuda.memory_allocated(device)
+        return _stage._FREE_MARGIN + rows * 2 * 12000 - cached, total
+
+    monkeypatch.setattr(_t.cuda, "mem_get_info", tight)
+    gq = GPTQ(_layers(1, 64, C, dev))
+    st = ohess.gptq_state(1, C)
+    g = gen(81)
+    for _ in range(6):
+        x = torch.randn(1, 3000, C, generator=g).bfloat16()
+        gq.add_batch(0, x.to(dev), None)
+        ohess.gptq_add_batch(st, 0, x)
+    cap = gq._stagers[0].cap
+    assert 3000 <= cap < 32 * 3000, cap
+    torch.cuda.synchronize()
+    _close(gq.H[0], st["H"][0], "shrunk staging")
