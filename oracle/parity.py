@@ -79,10 +79,12 @@ def stage_b(codes_hip, codes_ref, x_ref, scale_hip, scale_ref, zero_hip, zero_re
     first[rows] = diff[rows].to(torch.int8).argmax(1)
     reasons = []
     ties = {"rounding": 0, "zero_point": 0}
+    dist = []
     for r in rows.nonzero().flatten().tolist():
         j = int(first[r])
         t = float(x[r, j] / sr[r, j])
-        if abs(t - float(torch.floor(torch.tensor(t))) - 0.5) < tol:
+        dist.append(abs(t - float(torch.floor(torch.tensor(t))) - 0.5))
+        if dist[-1] < tol:
             ties["rounding"] += 1
             continue
         if zraw_ref is not None and zh[r, j] != zr[r, j]:
@@ -114,6 +116,7 @@ def stage_b(codes_hip, codes_ref, x_ref, scale_hip, scale_ref, zero_hip, zero_re
         "rows_diverged": n_first, "first_divergence_frac": first_frac,
         "mismatch_frac": float(diff.double().mean()), "ties": ties,
         "scale_rel_err": s_err, "dequant_rel_err": q_err,
+        "max_tie_distance": max(dist) if dist else 0.0,
     }
 
 
@@ -132,6 +135,7 @@ def summary(report):
     return (f"{report['rows_diverged']}/{report['rows']} rows diverge "
             f"(first divergences {100 * report['first_divergence_frac']:.4f} % of "
             f"{report['entries']} entries; ties {report['ties']}), "
+            f"farthest from a tie {report.get('max_tie_distance', 0.0):.2g}, "
             f"{100 * report['mismatch_frac']:.3f} % codes differ in all, "
             f"scale err {report['scale_rel_err']:.2g}, dequant err {report['dequant_rel_err']:.2g}")
 
@@ -149,7 +153,7 @@ def exported_codes(layers, bits, cols):
 
 
 def check_flow(label, layers, quantizers, ref, W0, H, bits, groupsize, static_groups,
-               max_first=1e-4, recon_rtol=0.005, check=True):
+               max_first=1e-4, recon_rtol=0.005, check=True, tie_tol=1e-4):
     """The whole bar for a ``fasterquant`` run with
     ``export_compressed_tensors=True`` on ``layers`` (fitted ``quantizers``)
     against an oracle flow ``ref`` on the same inputs: the stage-B report,
@@ -169,7 +173,7 @@ def check_flow(label, layers, quantizers, ref, W0, H, bits, groupsize, static_gr
     sr, zr, zraw = element_params(ref["quantizers"], N, C, groupsize, static_groups, perm,
                                   attr="zraw")
     qr = loop_order(ref["Q"].reshape(N, C), perm)
-    rep = stage_b(ch, cr, x, sh, sr, zh, zr, qr, zraw_ref=zraw)
+    rep = stage_b(ch, cr, x, sh, sr, zh, zr, qr, zraw_ref=zraw, tol=tie_tol)
     inv = None if perm is None else torch.argsort(perm)
     qh = loop_order(sh * (ch - zh).float(), inv).reshape(B, R, C)
     Qd = torch.stack([l.weight.detach().float().cpu() for l in layers])
