@@ -251,6 +251,14 @@ static int compensate_impl(hipStream_t s, int variant, int64_t B, int64_t R, int
   for (int64_t s0 = 0, sbi = 0; s0 < C; s0 += SB, ++sbi) {
     const int64_t s1 = std::min(s0 + SB, C);
     float* E = Ebuf[sbi & 1];
+    // GPTQ with full 128-column blocks, 16 lanes per row and groups fitted in
+    // the sweep (or static): one launch sweeps the whole super-block and
+    // applies its near tails itself.
+    const bool sb_groups = !dynamic || (mse_grid == 0 && groupsize % 32 == 0 &&
+                                        bs % groupsize == 0);
+    const int nblk = (variant == G2PTQ_VARIANT_GPTQ && bs == kMaxBlock && sb_groups &&
+                      (s1 - s0) % bs == 0 && s1 - s0 > bs)
+                         ? (int)((s1 - s0) / bs) : 1;
     for (int64_t i1 = s0; i1 < s1; i1 += bs) {
       const int64_t i2 = std::min(i1 + bs, C), n = i2 - i1;
       // Min/max groups that tile the block in 32-column multiples are fitted
@@ -308,6 +316,12 @@ static int compensate_impl(hipStream_t s, int variant, int64_t B, int64_t R, int
         a.E2 = nullptr;
       }
       a.flags = flags;
+      if (nblk > 1 && i1 == s0 && sweep_superblock_ok(a, B)) {
+        a.nblk = nblk;
+        a.Wsb = W + i1;
+        G2PTQ_TRY(launch_sweep(s, variant, a, B));
+        break;  // the launch swept every block of the super-block
+      }
       G2PTQ_TRY(launch_sweep(s, variant, a, B));
       // The block's tail inside the super-block.
       if (i2 < s1) G2PTQ_TRY(E2buf ? tail(E2buf, bs, i1, i2, i2, s1) : tail(Eb, SB, i1, i2, i2, s1));

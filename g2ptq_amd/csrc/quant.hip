@@ -509,13 +509,13 @@ __device__ __forceinline__ float group_bcast(float v, int o) {
   }
 }
 
-template <int V, int L, bool F>
+template <int V, int L, bool F, bool SBM = false>
 __global__ __launch_bounds__(256) void sweep4_kernel(SweepArgs a) {
   constexpr int PW = 32, RW = 256 / L;  // panel width, rows per workgroup
   constexpr int NS = PW / L;            // panel columns per lane
   // The triangles plus one spare word per lane (the full-block staging's
   // sink for entries left of the diagonal).
-  __shared__ float Us[kTri + 64];
+  __shared__ __attribute__((aligned(16))) float Us[kTri + 64];
   __shared__ float Ps[(V == 1) ? kTri + 64 : 1];
   __shared__ float e_s[kMaxBlock * RW];
   __shared__ float t_s[(V == 1) ? kMaxBlock * RW : 1];
@@ -523,19 +523,33 @@ __global__ __launch_bounds__(256) void sweep4_kernel(SweepArgs a) {
   __shared__ __attribute__((aligned(16))) float rdiag[kMaxBlock];  // RN(1 / U_jj)
   __shared__ __attribute__((aligned(16))) float dg[kMaxBlock];     // U_jj
 
-  const int tid = threadIdx.x, rr = tid / L, sub = tid % L;
   const int64_t b = blockIdx.y;
+  const float minq = (float)(-(a.maxq + 1)), fmaxq = (float)a.maxq;
+
+  int bad = 0;
+  float last_x = 0.f;
+  const int nblk = SBM ? a.nblk : 1;
+#pragma clang loop unroll(disable)
+  for (int bi = 0; bi < nblk; ++bi) {
+  const int64_t cofs = (int64_t)bi * kMaxBlock;  // the block's first column in the super-block
+  // In a super-block launch the thread index and block width are re-read
+  // opaquely per block, so the compiler cannot hoist the block's many
+  // derived addresses out of the block loop (which would cost a wave
+  // occupancy in registers).
+  int tid = threadIdx.x, n = a.n;
+  if (SBM) {
+    asm volatile("" : "+v"(tid));
+    asm volatile("" : "+s"(n));
+  }
+  const int rr = tid / L, sub = tid % L;
   const int64_t r0 = (int64_t)blockIdx.x * RW + rr;
   const bool act = r0 < a.R;
   const int64_t r = act ? r0 : 0;
-  const int n = a.n;
-  const float minq = (float)(-(a.maxq + 1)), fmaxq = (float)a.maxq;
-
   {
     // Stage the block's upper triangle (shared by the four waves): rows of U
     // as 16-byte chunks, all of a thread's loads in flight before its stores.
-    const float* U = a.U + b * a.ub;
-    const float* P = (V == 1) ? a.P + b * a.ub : nullptr;
+    const float* U = a.U + b * a.ub + cofs * a.uj + cofs;
+    const float* P = (V == 1) ? a.P + b * a.ub + cofs * a.uj + cofs : nullptr;
     const int nc = (n + 3) >> 2;              // 4-column chunks per row
     const int total = n * nc;
     const bool vec = ((a.uj & 3) == 0) && ((reinterpret_cast<uintptr_t>(U) & 15) == 0) &&
@@ -621,21 +635,21 @@ __global__ __launch_bounds__(256) void sweep4_kernel(SweepArgs a) {
   }
   __syncthreads();
 
-  const float* Win = a.W + b * a.wb + r * a.wr;
+  const float* Win = a.W + b * a.wb + r * a.wr + cofs * a.wc;
   const float* Sp = a.S + b * a.sb + r * a.sr;
   const float* Zp = a.Z0 + b * a.sb + r * a.sr;
-  const float* Zg = (V == 2) ? a.Zg + b * a.zb + r * a.zr : nullptr;
-  const float* GH = (V == 2) ? a.GH + b * a.gb + r * a.gr : nullptr;
-  float* GHo = (V == 2 && a.GHout) ? a.GHout + b * a.gb + r * a.gr : nullptr;
-  float* Qo = a.Q + b * a.qb + r * a.qr;
-  float* Io = a.I ? a.I + b * a.ib + r * a.ir : nullptr;
-  float* Eo = a.E ? a.E + b * a.eb + r * a.er : nullptr;
-  float* So = a.Sc ? a.Sc + b * a.cb + r * a.cr : nullptr;
-  float* E2 = (V == 2 && a.E2) ? a.E2 + b * a.e2b + r * a.e2r : nullptr;
-  float* E3 = (V == 2 && a.E3) ? a.E3 + b * a.e3b + r * a.e3r : nullptr;
+  const float* Zg = (V == 2) ? a.Zg + b * a.zb + r * a.zr + cofs * a.zc : nullptr;
+  const float* GH = (V == 2) ? a.GH + b * a.gb + r * a.gr + cofs * a.gc : nullptr;
+  float* GHo = (V == 2 && a.GHout) ? a.GHout + b * a.gb + r * a.gr + cofs * a.gc : nullptr;
+  float* Qo = a.Q + b * a.qb + r * a.qr + cofs * a.qc;
+  float* Io = a.I ? a.I + b * a.ib + r * a.ir + cofs * a.ic : nullptr;
+  float* Eo = a.E ? a.E + b * a.eb + r * a.er + cofs * a.ec : nullptr;
+  float* So = a.Sc ? a.Sc + b * a.cb + r * a.cr + cofs * a.cc : nullptr;
+  float* E2 = (V == 2 && a.E2) ? a.E2 + b * a.e2b + r * a.e2r + cofs * a.e2c : nullptr;
+  float* E3 = (V == 2 && a.E3) ? a.E3 + b * a.e3b + r * a.e3r + cofs * a.e2c : nullptr;
+  const int* colgroup = a.colgroup ? a.colgroup + cofs : nullptr;
+  const int64_t col0 = a.col0 + cofs;
 
-  int bad = 0;
-  float last_x = 0.f;
   float fs = 0.f, fz = 0.f;  // fused group parameters of the current group
 
   for (int p0 = 0; p0 < n; p0 += PW) {
@@ -660,7 +674,7 @@ __global__ __launch_bounds__(256) void sweep4_kernel(SweepArgs a) {
       }
       params_from_minmax(mn, mx, nan != 0, a.maxq, a.sym, fs, fz);
       if (act && sub == 0) {
-        const int64_t gidx = (a.col0 + p0) / a.gsize;
+        const int64_t gidx = (col0 + p0) / a.gsize;
         a.FS[b * a.sb + r * a.sr + gidx * a.sg] = fs;
         a.FZ[b * a.sb + r * a.sr + gidx * a.sg] = fz;
       }
@@ -675,8 +689,8 @@ __global__ __launch_bounds__(256) void sweep4_kernel(SweepArgs a) {
         zv[s] = fz;
       } else {
         int gidx = 0;
-        if (a.colgroup) gidx = a.colgroup[j];
-        else if (a.gsize > 0) gidx = (int)((int)a.col0 + j) / (int)a.gsize;
+        if (colgroup) gidx = colgroup[j];
+        else if (a.gsize > 0) gidx = (int)((int)col0 + j) / (int)a.gsize;
         sv[s] = Sp[(int64_t)gidx * a.sg];
         zv[s] = Zp[(int64_t)gidx * a.sg];
       }
@@ -824,7 +838,49 @@ __global__ __launch_bounds__(256) void sweep4_kernel(SweepArgs a) {
       }
     }
   }
-  if (V == 1 && a.CW && act && sub == 0) a.CW[b * a.cwb + r * a.cwr] = last_x;
+    if (SBM && bi + 1 < nblk) {
+      // Near tail of the super-block: W[row, c] −= Σ_k e_k·U[cofs + k, c] for
+      // the columns c of the later blocks, 64 at a time (the triangle's LDS
+      // holds the U slab, k-major), four consecutive columns per lane.
+      float* Wr = a.Wsb + b * a.wb + r * a.wr;
+      const float* Ub = a.U + b * a.ub + cofs * a.uj;
+      for (int c0 = (int)cofs + kMaxBlock; c0 < nblk * kMaxBlock; c0 += 64) {
+        __syncthreads();  // the sweep's (or the previous slab's) LDS reads are done
+        for (int q = tid; q < kMaxBlock * 16; q += 256) {
+          const int k = q >> 4, c4 = (q & 15) * 4;
+          *reinterpret_cast<float4*>(&Us[k * 64 + c4]) =
+              *reinterpret_cast<const float4*>(Ub + (int64_t)k * a.uj + c0 + c4);
+        }
+        __syncthreads();
+        if (act) {
+          float4 w = *reinterpret_cast<const float4*>(Wr + c0 + 4 * sub);
+          float t[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll 4
+          for (int k = 0; k < kMaxBlock; k += 2) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              const float e = e_s[(k + h) * RW + rr];
+              const float4 u = *reinterpret_cast<const float4*>(&Us[(k + h) * 64 + 4 * sub]);
+              t[h][0] = __builtin_fmaf(e, u.x, t[h][0]);
+              t[h][1] = __builtin_fmaf(e, u.y, t[h][1]);
+              t[h][2] = __builtin_fmaf(e, u.z, t[h][2]);
+              t[h][3] = __builtin_fmaf(e, u.w, t[h][3]);
+            }
+          }
+          w.x = __fsub_rn(w.x, __fadd_rn(t[0][0], t[1][0]));
+          w.y = __fsub_rn(w.y, __fadd_rn(t[0][1], t[1][1]));
+          w.z = __fsub_rn(w.z, __fadd_rn(t[0][2], t[1][2]));
+          w.w = __fsub_rn(w.w, __fadd_rn(t[0][3], t[1][3]));
+          *reinterpret_cast<float4*>(Wr + c0 + 4 * sub) = w;
+        }
+      }
+    }
+    if (SBM) __syncthreads();  // the next block's staging overwrites the LDS
+  }  // block bi of the super-block
+  const int rr = threadIdx.x / L, sub = threadIdx.x % L;
+  const int64_t r0 = (int64_t)blockIdx.x * RW + rr;
+  const bool act = r0 < a.R;
+  if (V == 1 && a.CW && act && sub == 0) a.CW[b * a.cwb + r0 * a.cwr] = last_x;
   if (bad && act && a.flags) atomicOr(a.flags, FLAG_BAD_SCALE);
 }
 
@@ -842,14 +898,26 @@ bool sweep_vec_ok(const SweepArgs& a) {
          ok(a.GH, a.gb, a.gr, a.gc) && a.GHout == nullptr;
 }
 
+// 16 lanes per row while the launch's rows fit in about two waves per SIMD.
+bool lanes16(int64_t B, int64_t R) { return B * R <= 8192; }
+
 template <int V>
 void launch_variant(hipStream_t stream, const SweepArgs& a, dim3 grid, bool vec) {
   const bool full = (a.n % 32) == 0;
   if (full) {
     // 16 lanes per row while that keeps the block within about two waves per
     // SIMD (1024 SIMDs), else a quad per row.
-    if ((int64_t)grid.y * a.R <= 8192) {
+    if (lanes16(grid.y, a.R)) {
       dim3 g16((unsigned)cdiv(a.R, (int64_t)16), grid.y);
+      if constexpr (V == 0) {
+        if (a.nblk > 1) {
+          if (a.fuse > 0)
+            hipLaunchKernelGGL((sweep4_kernel<V, 16, true, true>), g16, dim3(256), 0, stream, a);
+          else
+            hipLaunchKernelGGL((sweep4_kernel<V, 16, false, true>), g16, dim3(256), 0, stream, a);
+          return;
+        }
+      }
       if (a.fuse > 0)
         hipLaunchKernelGGL((sweep4_kernel<V, 16, true>), g16, dim3(256), 0, stream, a);
       else
@@ -873,6 +941,11 @@ void launch_variant(hipStream_t stream, const SweepArgs& a, dim3 grid, bool vec)
 
 }  // namespace
 
+bool sweep_superblock_ok(const SweepArgs& a, int64_t B) {
+  return a.n == kMaxBlock && lanes16(B, a.R) && sweep_vec_ok(a) && a.uj % 4 == 0 &&
+         aligned16(a.U) && a.P == nullptr && a.Zg == nullptr;
+}
+
 int launch_sweep(hipStream_t stream, int variant, const SweepArgs& a, int64_t B) {
   G2PTQ_CHECK(a.n >= 1 && a.n <= kMaxBlock, "block sweep: block width %d not in [1, %d]", a.n,
               kMaxBlock);
@@ -883,6 +956,9 @@ int launch_sweep(hipStream_t stream, int variant, const SweepArgs& a, int64_t B)
               "block sweep: fused group parameters need 32-column panels and aligned groups");
   dim3 grid((unsigned)cdiv(a.R, 64), (unsigned)B);
   const bool vec = sweep_vec_ok(a);
+  G2PTQ_CHECK(a.nblk <= 1 || (variant == G2PTQ_VARIANT_GPTQ && sweep_superblock_ok(a, B) &&
+                              a.Wsb == a.W && a.nblk * kMaxBlock <= 1 << 20),
+              "block sweep: a super-block launch needs GPTQ, full blocks and 16 lanes per row");
   switch (variant) {
     case G2PTQ_VARIANT_GPTQ:
       launch_variant<0>(stream, a, grid, vec);

@@ -39,10 +39,20 @@ struct SweepArgs {
   // G2PTQ, super-block far tail: err - z*(dist3 - j) (nullable; same strides
   // as E2); dist3 = dist0 + the columns of the super-block after this block.
   float* E3; int64_t e3b, e3r; int64_t dist3;
+  // Super-block mode (GPTQ, 16 lanes per row, full 128-column blocks,
+  // column-contiguous rows; nblk > 1): the launch sweeps nblk consecutive
+  // blocks, W, U and the outputs pointing at the first, and applies each
+  // block's errors to its rows' columns of the later blocks in Wsb (the
+  // writable W the block inputs come from) before sweeping the next.
+  int nblk;
+  float* Wsb;
   int* flags;
 };
 
 int launch_sweep(hipStream_t stream, int variant, const SweepArgs& a, int64_t B);
+// Whether a GPTQ block (a.nblk unset) can run as the first of a super-block
+// launch: 16 lanes per row, a full 128-column block, 16-byte aligned rows.
+bool sweep_superblock_ok(const SweepArgs& a, int64_t B);
 int launch_find_params(hipStream_t stream, const float* x, int64_t rows, int64_t cols,
                        int64_t ldx, int maxq, int sym, float* scale, float* zero, int64_t ldp,
                        int* flags);
