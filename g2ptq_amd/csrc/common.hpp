@@ -86,16 +86,6 @@ struct GemmF32 {
   // (B[k][n] = 0 for k > n).
   int tri = 0;
   const int* skip = nullptr;  // optional per-b1 flag: nonzero => skip that entry
-  // Fused diagonal-block factor (the factor's panel update produces the next
-  // diagonal block): when pot_nb > 0, the workgroup of output tile (0, 0) of
-  // each batch entry b1 factors and inverts the top-left pot_nb×pot_nb block
-  // of its result (potrf.hpp) and stores X = L⁻¹ there (lower, zeros above)
-  // instead of the block; a failing pivot p sets pot_info[b1] = pot_k + p and
-  // pot_st[b1] = 1 (the block is then left as it was).
-  int pot_nb = 0;
-  int64_t pot_k = 0;
-  int* pot_st = nullptr;
-  int* pot_info = nullptr;
 };
 
 int gemm_f32(hipStream_t stream, const GemmF32& g);

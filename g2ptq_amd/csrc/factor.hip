@@ -10,9 +10,10 @@
 //   2. blocked right-looking Cholesky of Â in panels of NBO = 512 columns,
 //      each factored NB = 64 columns at a time: potrf of the diagonal block
 //      in one workgroup (registers), which also inverts it in place;  TRSM
-//      as a GEMM with that inverse;  update of the panel's remaining
-//      columns;  then one SYRK trailing update per panel (K = 512) as a
-//      lower-triangular fp32 MFMA GEMM
+//      with that inverse and update of the panel's remaining columns in one
+//      launch (panel_step_kernel, whose first tile factors the next diagonal
+//      block);  then one SYRK trailing update per panel (K = 512) as a
+//      lower-triangular fp32 GEMM
 //   3. the triangular inverse X = L̂⁻¹ panel by panel, as soon as each is
 //      factored, on a third stream beside the Cholesky: the diagonal block
 //      by recursive doubling from the NB inverses, then the block row
@@ -79,37 +80,36 @@ __global__ void reverse_damp_kernel(const float* __restrict__ H, int64_t C, floa
 // Cholesky + in-place inverse of the nbk×nbk (nbk <= 64) diagonal block at
 // (k, k) of each layer: load, potrf_core (potrf.hpp), store X = L⁻¹ (lower,
 // zeros above) or record the failing pivot.
-__global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1))) void potrf_diag_kernel(
-    float* WA, int64_t C, int64_t k, int nbk, int* st, int* info) {
+__global__ __launch_bounds__(256) void potrf_diag_kernel(float* WA, int64_t C, int64_t k, int nbk,
+                                                        int* st, int* info) {
   const int64_t b = blockIdx.x;
   __shared__ __attribute__((aligned(16))) float Xs[POT_NB * XP];
-  __shared__ __attribute__((aligned(16))) float colL[2][POT_NB];
-  __shared__ float rdl[2];
+  __shared__ __attribute__((aligned(16))) float Lm[POT_NB * LP];
+  __shared__ __attribute__((aligned(16))) float rdv[POT_NB];
   __shared__ int fail_s;
   float* Wb = WA + b * C * C + k * C + k;
   const int i = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int skip = st[b];
-  // Lower triangle of the block: row r through lane i of wave r & 1
+  // Lower triangle of the block: row r through lane i of wave r & 3
   // (coalesced; addresses clamped into the block so the loads need no
-  // branches), all 32 rows of a wave in flight together, transposed through
-  // LDS so that lane i of wave 0 holds row i.
+  // branches), all 16 rows of a wave in flight together.
   {
     const int ci = i < nbk ? i : nbk - 1;
-    float x[POT_NB / 2];
+    float x[POT_NB / 4];
 #pragma unroll
-    for (int h = 0; h < POT_NB / 2; ++h) {
-      const int r = 2 * h + w;
+    for (int h = 0; h < POT_NB / 4; ++h) {
+      const int r = 4 * h + w;
       const int rr = r < nbk ? r : nbk - 1;
       x[h] = Wb[(int64_t)rr * C + ci];
     }
 #pragma unroll
-    for (int h = 0; h < POT_NB / 2; ++h) {
-      const int r = 2 * h + w;
+    for (int h = 0; h < POT_NB / 4; ++h) {
+      const int r = 4 * h + w;
       Xs[r * XP + i] = (r < nbk && i < nbk) ? (i <= r ? x[h] : 0.f) : (r == i ? 1.f : 0.f);
     }
   }
   __syncthreads();
-  const int fail = potrf_core(Xs, colL, rdl, &fail_s);
+  const int fail = potrf_core(Xs, Lm, rdv, &fail_s);
   // Layers already done (a damp retry) run the steps on whatever the block
   // holds and store nothing: testing the flag only here lets its load overlap
   // the block loads instead of preceding them.
@@ -123,7 +123,242 @@ __global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   }
   if (i < nbk) {
 #pragma unroll 4
-    for (int r = w; r < nbk; r += 2) Wb[(int64_t)r * C + i] = (i <= r) ? Xs[r * XP + i] : 0.f;
+    for (int r = w; r < nbk; r += 4) Wb[(int64_t)r * C + i] = (i <= r) ? Xs[r * XP + i] : 0.f;
+  }
+}
+
+// ---- Panel steps: TRSM, remainder update and the next diagonal block in one launch ----
+//
+// Column block [j, j + nbk) of the panel [k, pe), its diagonal block already
+// inverted in place (X_jj = L_jj⁻¹, lower):
+//   L[r, j:j+nbk] = Â[r, j:j+nbk]·X_jjᵀ           rows r >= r0 = j + nbk
+//   Â[r, c]      −= Σ_t L[r, j+t]·L[c, j+t]        r0 <= c < pe, c <= r
+// and the workgroup of tile (r0, r0) factors and inverts the next diagonal
+// block.  A workgroup owns one 64×64 tile (i, n) of the update and forms the
+// two L blocks it multiplies (rows of tile-row i and of tile-column n) itself
+// from the raw column block, so the TRSM needs no launch of its own.  The raw
+// column block is therefore read while the step runs, and L cannot go back in
+// place: workgroups of tile-column 0 write their L rows to a panel buffer
+// (Lp, rows × NBO), and the panel's last step (panel_finish_kernel) copies it
+// into Â.
+//
+// The products use v_mfma_f32_32x32x2_f32 in the order of gemm_f32's fp32
+// path (32-k slabs; k-octet o, lane half h holding k = 8o + 4h + c in the c-th
+// of four MFMAs), and its epilogue arithmetic (alpha·acc + beta·C with
+// alpha = 1, beta = 0 for L and alpha = −1, beta = 1 for the update), so the
+// factor is bit-identical to a TRSM launch followed by an update launch of
+// gemm_f32 (the scheme this replaced: measured on MI355X, same bits for
+// C = 64 … 14336).
+constexpr int SLP = 68;  // LDS row pitch (floats) of the 64-wide k tiles
+static_assert(SLP >= LP, "the panel step's tiles hold the potrf scratch");
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// A 64×64 block of Â (rows row0.., columns col0.., only rows < nrows and
+// columns < ncols nonzero) into LDS [row][SLP].
+__device__ __forceinline__ void panel_load(float* Ls, const float* Wb, int64_t C, int64_t row0,
+                                           int64_t col0, int64_t nrows, int ncols, bool vec) {
+  const int t = threadIdx.x;
+  const int c4 = (t & 15) * 4;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int r = (t >> 4) + 16 * q;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (r < nrows) {
+      const float* p = Wb + (row0 + r) * C + col0 + c4;
+      if (vec && c4 + 3 < ncols) {
+        v = *reinterpret_cast<const float4*>(p);
+      } else {
+        if (c4 < ncols) v.x = p[0];
+        if (c4 + 1 < ncols) v.y = p[1];
+        if (c4 + 2 < ncols) v.z = p[2];
+        if (c4 + 3 < ncols) v.w = p[3];
+      }
+    }
+    *reinterpret_cast<float4*>(&Ls[r * SLP + c4]) = v;
+  }
+}
+
+// One wave's 32×32 block of Σ_k Ap[ar + ·][k]·Bp[br + ·][k] over 64 k.
+__device__ __forceinline__ f32x16 panel_mma(const float* Ap, const float* Bp, int ar, int br) {
+  const int lane = threadIdx.x & 63, lr = lane & 31, lh = lane >> 5;
+  f32x16 acc;
+#pragma unroll
+  for (int v = 0; v < 16; ++v) acc[v] = 0.f;
+#pragma unroll
+  for (int o = 0; o < 8; ++o) {
+    const float4 a = *reinterpret_cast<const float4*>(Ap + (ar + lr) * SLP + o * 8 + lh * 4);
+    const float4 b = *reinterpret_cast<const float4*>(Bp + (br + lr) * SLP + o * 8 + lh * 4);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, b.x, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, b.y, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, b.z, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, b.w, acc, 0, 0, 0);
+  }
+  return acc;
+}
+
+// The wave's block of L = (raw)·Xᵀ as gemm_f32 stores it (1·acc + 0), into
+// LDS over the raw rows (columns at or past nbk zero).
+__device__ __forceinline__ void panel_put_l(float* Ls, const f32x16& acc, int wm, int wn, int nbk) {
+  const int lane = threadIdx.x & 63, lr = lane & 31, lh = lane >> 5;
+  const int col = wn * 32 + lr;
+#pragma unroll
+  for (int v = 0; v < 16; ++v) {
+    const int row = wm * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+    Ls[row * SLP + col] = col < nbk ? __builtin_fmaf(1.f, acc[v], 0.f) : 0.f;
+  }
+}
+
+struct PanelArgs {
+  float* WA;         // Â (B × C × C), updated in place
+  float* Lp;         // panel buffer (B × C × NBO): L of the panel's column blocks
+  int64_t C;
+  int64_t k, pe;     // panel [k, pe)
+  int64_t j;         // column block [j, j + nbk)
+  int nbk;
+  int pot_nb;        // next diagonal block's width (0: none)
+  int ncb;           // tile-columns of the remainder, cdiv(pe − r0, 64)
+  int nrb;           // tile-rows, cdiv(C − r0, 64)
+  int* st;
+  int* info;
+};
+
+__global__ __launch_bounds__(256) void panel_step_kernel(PanelArgs p) {
+  __shared__ __attribute__((aligned(16))) float Xj[64 * SLP];
+  __shared__ __attribute__((aligned(16))) float Ai[64 * SLP];
+  __shared__ __attribute__((aligned(16))) float An[64 * SLP];
+  __shared__ int fail_s;
+  const int64_t b = blockIdx.y;
+  if (p.st[b]) return;
+  const int64_t C = p.C, r0 = p.j + p.nbk;
+  // Tile id → (i, n): the triangle of tile-rows inside the panel first
+  // (id 0 = the diagonal tile that factors the next block), then the
+  // rectangle below the panel.
+  const int64_t id = blockIdx.x, tri = (int64_t)p.ncb * (p.ncb + 1) / 2;
+  int64_t i, n;
+  if (id < tri) {
+    i = (int64_t)((sqrtf(8.f * (float)id + 1.f) - 1.f) * 0.5f);
+    while (i * (i + 1) / 2 > id) --i;
+    while ((i + 1) * (i + 2) / 2 <= id) ++i;
+    n = id - i * (i + 1) / 2;
+  } else {
+    i = p.ncb + (id - tri) / p.ncb;
+    n = (id - tri) % p.ncb;
+  }
+  float* Wb = p.WA + b * C * C;
+  const bool vec = (C & 3) == 0;
+  const int64_t ri = r0 + 64 * i, rn = r0 + 64 * n;  // first row of each L block
+  panel_load(Xj, Wb, C, p.j, p.j, p.nbk, p.nbk, vec);
+  panel_load(Ai, Wb, C, ri, p.j, C - ri, p.nbk, vec);
+  if (n != i) panel_load(An, Wb, C, rn, p.j, C - rn, p.nbk, vec);
+  __syncthreads();
+  const int wave = threadIdx.x >> 6, wm = wave >> 1, wn = wave & 1;
+  const int lane = threadIdx.x & 63, lr = lane & 31, lh = lane >> 5;
+  const f32x16 li = panel_mma(Ai, Xj, wm * 32, wn * 32);
+  f32x16 ln;
+  if (n != i) ln = panel_mma(An, Xj, wm * 32, wn * 32);
+  __syncthreads();  // raw blocks and X_jj read
+  panel_put_l(Ai, li, wm, wn, p.nbk);
+  if (n != i) panel_put_l(An, ln, wm, wn, p.nbk);
+  if (n == 0) {
+    // L rows of tile-row i into the panel buffer (column j − k on)
+    float* Lb = p.Lp + b * C * NBO + (p.j - p.k);
+    const int col = wn * 32 + lr;
+    if (col < p.nbk) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t r = ri + wm * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+        if (r < C) Lb[r * NBO + col] = __builtin_fmaf(1.f, li[v], 0.f);
+      }
+    }
+  }
+  __syncthreads();  // L blocks in LDS
+  const float* Ln = (n != i) ? An : Ai;
+  const f32x16 acc = panel_mma(Ai, Ln, wm * 32, wn * 32);
+  // Epilogue: Â[r][c] = −1·acc + 1·Â[r][c] on the lower part inside the
+  // panel; the tile (0, 0) sends the next diagonal block to LDS instead.
+  const bool pot = p.pot_nb > 0 && i == 0 && n == 0;
+  float* Xs = Xj;  // the potrf staging reuses X_jj's buffer (read above)
+  const int64_t c = rn + wn * 32 + lr;
+  float cv[16];
+#pragma unroll
+  for (int v = 0; v < 16; ++v) {
+    const int64_t r = ri + wm * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+    cv[v] = (r < C && c < p.pe) ? 1.f * Wb[r * C + c] : 0.f;
+  }
+#pragma unroll
+  for (int v = 0; v < 16; ++v) {
+    const int rl = wm * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+    const int64_t r = ri + rl;
+    const float val = __builtin_fmaf(-1.f, acc[v], cv[v]);
+    if (pot) {
+      const int cl = wn * 32 + lr, nb = p.pot_nb;
+      Xs[rl * XP + cl] = (rl < nb && cl < nb) ? (cl <= rl ? val : 0.f) : (rl == cl ? 1.f : 0.f);
+      if (rl < nb && cl < nb) continue;
+    }
+    if (r < C && c < p.pe && c <= r) Wb[r * C + c] = val;
+  }
+  if (!pot) return;
+  __syncthreads();
+  const int fail = potrf_core(Xs, Ai, An, &fail_s);  // L and the pivots' 1/sqrt in Ai, An
+  if (fail) {
+    if (threadIdx.x == 0) {
+      p.info[b] = (int)(r0 + fail);
+      p.st[b] = 1;
+    }
+    return;
+  }
+  const int wv = threadIdx.x >> 6;
+  if (lane < p.pot_nb) {
+    for (int r = wv; r < p.pot_nb; r += 4)
+      Wb[(r0 + r) * C + r0 + lane] = (lane <= r) ? Xs[r * XP + lane] : 0.f;
+  }
+}
+
+// The panel's last column block [j, pe): workgroup t owns rows
+// [k + 64(t + 1), +64).  Rows below the panel get their TRSM for this block in
+// place (L = Â·X_jjᵀ; nothing else reads these raw values); every row gets the
+// panel buffer's L columns left of its own diagonal block (or of this block)
+// copied into Â.
+__global__ __launch_bounds__(256) void panel_finish_kernel(PanelArgs p) {
+  __shared__ __attribute__((aligned(16))) float Xj[64 * SLP];
+  __shared__ __attribute__((aligned(16))) float Ai[64 * SLP];
+  const int64_t b = blockIdx.y;
+  if (p.st[b]) return;
+  const int64_t C = p.C;
+  const int64_t R0 = p.k + 64 * ((int64_t)blockIdx.x + 1);
+  float* Wb = p.WA + b * C * C;
+  const float* Lb = p.Lp + b * C * NBO;
+  const bool vec = (C & 3) == 0;
+  const int64_t cend = (R0 < p.pe ? R0 : p.j) - p.k;  // buffer columns to copy
+  {
+    const int nq = (int)(cend >> 2);  // cend is a multiple of 64
+    for (int q = threadIdx.x; q < 64 * nq; q += 256) {
+      const int64_t r = R0 + q / nq;
+      const int64_t c4 = (int64_t)(q % nq) * 4;
+      if (r >= C) continue;
+      const float* s = Lb + r * NBO + c4;
+      float* d = Wb + r * C + p.k + c4;
+      if (vec) {
+        *reinterpret_cast<float4*>(d) = *reinterpret_cast<const float4*>(s);
+      } else {
+        d[0] = s[0]; d[1] = s[1]; d[2] = s[2]; d[3] = s[3];
+      }
+    }
+  }
+  if (R0 < p.pe) return;
+  panel_load(Xj, Wb, C, p.j, p.j, p.nbk, p.nbk, vec);
+  panel_load(Ai, Wb, C, R0, p.j, C - R0, p.nbk, vec);
+  __syncthreads();
+  const int wave = threadIdx.x >> 6, wm = wave >> 1, wn = wave & 1;
+  const int lane = threadIdx.x & 63, lr = lane & 31, lh = lane >> 5;
+  const f32x16 li = panel_mma(Ai, Xj, wm * 32, wn * 32);
+  const int col = wn * 32 + lr;
+  if (col < p.nbk) {
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int64_t r = R0 + wm * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+      if (r < C) Wb[r * C + p.j + col] = __builtin_fmaf(1.f, li[v], 0.f);
+    }
   }
 }
 
@@ -153,7 +388,7 @@ __global__ void unreverse_kernel(const float* __restrict__ WA, int64_t C, const 
 }
 
 struct FactorWs {
-  size_t wa, wt, ti, sums, st, total;
+  size_t wa, wt, ti, lp, sums, st, total;
 };
 
 FactorWs factor_ws(int64_t B, int64_t C) {
@@ -163,9 +398,10 @@ FactorWs factor_ws(int64_t B, int64_t C) {
   const int64_t half = std::min<int64_t>((C + 1) / 2, NBO);
   w.wt = al((size_t)B * half * half * 4 + 4);        // in-panel inverse products
   w.ti = al((size_t)B * NBO * C * 4 + 4);            // inverse block-row products
+  w.lp = al((size_t)B * C * NBO * 4);                // a panel's L until its last step
   w.sums = al((size_t)B * 4);
   w.st = al((size_t)B * 4);
-  w.total = w.wa + w.wt + w.ti + w.sums + w.st;
+  w.total = w.wa + w.wt + w.ti + w.lp + w.sums + w.st;
   return w;
 }
 
@@ -211,8 +447,9 @@ extern "C" int g2ptq_inv_chol_upper(void* stream, const float* H, int64_t B, int
   float* WA = reinterpret_cast<float*>(base);
   float* WT = reinterpret_cast<float*>(base + w.wa);
   float* TI = reinterpret_cast<float*>(base + w.wa + w.wt);
-  float* sums = reinterpret_cast<float*>(base + w.wa + w.wt + w.ti);
-  int* st = reinterpret_cast<int*>(base + w.wa + w.wt + w.ti + w.sums);
+  float* Lp = reinterpret_cast<float*>(base + w.wa + w.wt + w.ti);
+  float* sums = reinterpret_cast<float*>(base + w.wa + w.wt + w.ti + w.lp);
+  int* st = reinterpret_cast<int*>(base + w.wa + w.wt + w.ti + w.lp + w.sums);
   const int64_t CC = C * C;
 
   hipLaunchKernelGGL(diag_sum_kernel, dim3((unsigned)B), dim3(256), 0, s, H, C, skip, sums, st,
@@ -271,8 +508,10 @@ extern "C" int g2ptq_inv_chol_upper(void* stream, const float* H, int64_t B, int
   // while the next panel (updated first, on the caller's stream) is factored,
   // so the latency-bound panel chain overlaps the MFMA-bound SYRK.  The first
   // diagonal block of a panel is factored by potrf_diag_kernel; every later
-  // one by the panel-remainder update that produces it (its top-left
-  // workgroup factors the block in LDS right after computing it).
+  // one by the panel step that produces it (its first workgroup factors the
+  // block in LDS right after computing it).  One launch per 64 columns: the
+  // step's TRSM and update run together, L of the panel goes to the Lp buffer
+  // and reaches Â in the panel's last step.
   // Once a panel is factored, a third stream inverts it into X = L̂⁻¹:
   //   the panel's diagonal block (recursive doubling from the NB inverses,
   //   in place), then, in block-row order so that X[0:k, 0:k] is final,
@@ -285,37 +524,34 @@ extern "C" int g2ptq_inv_chol_upper(void* stream, const float* H, int64_t B, int
   G2PTQ_TRY(side_stream(s, side));
   bool inv_pending = false;  // inverse work queued on stream2
   auto factor_panel = [&](int64_t k, int64_t kb) -> int {
-    bool fused = false;
+    PanelArgs pa;
+    pa.WA = WA; pa.Lp = Lp; pa.C = C; pa.k = k; pa.pe = k + kb; pa.st = st; pa.info = info;
     for (int64_t j = k; j < k + kb; j += NB) {
       const int nbk = (int)std::min<int64_t>(NB, k + kb - j);
-      if (!fused) {
-        hipLaunchKernelGGL(potrf_diag_kernel, dim3((unsigned)B), dim3(128), 0, s, WA, C, j, nbk,
+      if (j == k) {
+        hipLaunchKernelGGL(potrf_diag_kernel, dim3((unsigned)B), dim3(256), 0, s, WA, C, j, nbk,
                            st, info);
         G2PTQ_LAUNCHED();
       }
-      fused = false;
-      const int64_t rest = C - j - nbk;
-      if (rest <= 0) break;
-      GemmF32 t;  // panel ← panel · inv(L_jj)ᵀ
-      t.M = rest; t.N = nbk; t.K = nbk; t.batch = B;
-      t.A = WA + (j + nbk) * C + j; t.lda = C; t.sA = CC;
-      t.B = WA + j * C + j; t.ldb = C; t.sB = CC; t.b_kcontig = 1;
-      t.D = WA + (j + nbk) * C + j; t.ldd = C; t.sD = CC;
-      t.skip = st;
-      G2PTQ_TRY(gemm_f32(s, t));
+      pa.j = j; pa.nbk = nbk;
       const int64_t pw = k + kb - (j + nbk);  // panel columns still to factor
-      if (pw <= 0) continue;
-      GemmF32 y;  // panel remainder ← remainder − L[:, j] · L[panel rows, j]ᵀ (lower)
-      y.M = rest; y.N = pw; y.K = nbk; y.batch = B;
-      y.A = WA + (j + nbk) * C + j; y.lda = C; y.sA = CC;
-      y.B = WA + (j + nbk) * C + j; y.ldb = C; y.sB = CC; y.b_kcontig = 1;
-      y.C = WA + (j + nbk) * C + (j + nbk); y.ldc = C; y.sC = CC;
-      y.D = WA + (j + nbk) * C + (j + nbk); y.ldd = C; y.sD = CC;
-      y.alpha = -1.f; y.beta = 1.f; y.uplo = 1; y.skip = st;
-      y.pot_nb = (int)std::min<int64_t>(NB, pw); y.pot_k = j + nbk;
-      y.pot_st = st; y.pot_info = info;
-      G2PTQ_TRY(gemm_f32(s, y));
-      fused = true;
+      if (pw > 0) {
+        // TRSM of the rows below, update of the panel remainder, next diagonal block
+        pa.pot_nb = (int)std::min<int64_t>(NB, pw);
+        pa.ncb = (int)cdiv(pw, 64);
+        pa.nrb = (int)cdiv(C - j - nbk, 64);
+        const int64_t tiles = (int64_t)pa.ncb * (pa.ncb + 1) / 2 + (int64_t)(pa.nrb - pa.ncb) * pa.ncb;
+        hipLaunchKernelGGL(panel_step_kernel, dim3((unsigned)tiles, (unsigned)B), dim3(256), 0, s,
+                           pa);
+        G2PTQ_LAUNCHED();
+      } else if (C - k > NB) {
+        // TRSM of the rows below the panel for its last block; the panel
+        // buffer's L into Â
+        pa.pot_nb = 0;
+        hipLaunchKernelGGL(panel_finish_kernel, dim3((unsigned)cdiv(C - k - NB, 64), (unsigned)B),
+                           dim3(256), 0, s, pa);
+        G2PTQ_LAUNCHED();
+      }
     }
     G2PTQ_HIP(hipEventRecord(side.factored, s));
     G2PTQ_HIP(hipStreamWaitEvent(side.stream2, side.factored, 0));

@@ -35,7 +35,6 @@
 // sits as [k][n] with a 136-float pitch and is read 4 bytes per lane (the
 // two lane halves land 32 banks apart).
 #include "common.hpp"
-#include "potrf.hpp"
 
 namespace g2ptq {
 namespace {
@@ -103,7 +102,7 @@ __device__ __forceinline__ void tile_of(int64_t id, int64_t tm, int64_t tn, int6
 // TILE × TILE output per workgroup (4 waves in 2×2, each TILE/2 square made
 // of 32×32 MFMA blocks): 128 for large products, 64 when a 128 grid would
 // leave most CUs idle (the factor's TRSM / panel updates, short tails).
-template <int TILE, bool B_KCONTIG, bool VEC, bool POT, bool SPLIT>
+template <int TILE, bool B_KCONTIG, bool VEC, bool SPLIT>
 __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmF32 g, int64_t tm, int64_t tn) {
   constexpr int BM = TILE, BN = TILE;
   constexpr int PN = BN + 8;                       // [k][n] pitch (floats)
@@ -115,12 +114,6 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmF32 g, int64_t tm,
   constexpr int RB = BN / 32;                      // float4 per thread per slab (B)
   __shared__ __attribute__((aligned(16))) float As[2][LDS_A];
   __shared__ __attribute__((aligned(16))) float Bs[2][LDS_B];
-  // Fused factor (POT): its staging reuses the operand buffers after the main loop.
-  static_assert(!POT || 2 * LDS_A >= POT_NB * XP + 2 * POT_NB + 4, "fused factor LDS");
-  float* Xs = &As[0][0];
-  float (*colL)[POT_NB] = reinterpret_cast<float (*)[POT_NB]>(&As[0][0] + POT_NB * XP);
-  float* rdl = &As[0][0] + POT_NB * XP + 2 * POT_NB;
-  int* fail_s = reinterpret_cast<int*>(rdl + 2);
 
   const int z = blockIdx.z;
   const int64_t b1 = z / g.batch2, b2 = z % g.batch2;
@@ -164,7 +157,6 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmF32 g, int64_t tm,
     im = tm - 1 - im;
   }
   const int64_t m0 = im * BM, n0 = in * BN;
-  const bool pot_here = POT && im == 0 && in == 0;
   if (g.uplo == 1 && n0 > m0 + BM - 1) return;
   if (g.uplo == 2 && m0 > n0 + BN - 1) return;
 
@@ -516,33 +508,11 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmF32 g, int64_t tm,
       for (int v = 0; v < 16; ++v) {
         const int64_t m = m0 + wm * WT + i * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
         const float val = g.alpha * acc[i][j][v] + cv[j][v];
-        if (POT && pot_here && m < POT_NB && n < POT_NB) {
-          // the block goes to LDS for the fused factor, not to D
-          const int r = (int)m, c = (int)n, nb = g.pot_nb;
-          Xs[r * XP + c] = (r < nb && c < nb) ? (c <= r ? val : 0.f) : (r == c ? 1.f : 0.f);
-          if (r < nb && c < nb) continue;
-        }
         if (m >= M || n >= N) continue;
         if (g.uplo == 1 && n > m) continue;
         if (g.uplo == 2 && m > n) continue;
         D[m * g.ldd + n] = val;
       }
-    }
-  }
-  if (POT && pot_here) {
-    __syncthreads();
-    const int fail = potrf_core(Xs, colL, rdl, fail_s);
-    if (fail) {
-      if (threadIdx.x == 0) {
-        g.pot_info[b1] = (int)(g.pot_k + fail);
-        g.pot_st[b1] = 1;
-      }
-      return;
-    }
-    const int lane_i = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    if (lane_i < g.pot_nb) {
-      for (int r = wv; r < g.pot_nb; r += 4)
-        D[(int64_t)r * g.ldd + lane_i] = (lane_i <= r) ? Xs[r * XP + lane_i] : 0.f;
     }
   }
 }
@@ -552,14 +522,14 @@ void launch_variant(hipStream_t stream, const GemmF32& g, bool vec, dim3 grid, i
                     int64_t tn) {
   if (g.b_kcontig) {
     if (vec)
-      hipLaunchKernelGGL((gemm_f32_kernel<TILE, true, true, false, SPLIT>), grid, dim3(256), 0, stream, g, tm, tn);
+      hipLaunchKernelGGL((gemm_f32_kernel<TILE, true, true, SPLIT>), grid, dim3(256), 0, stream, g, tm, tn);
     else
-      hipLaunchKernelGGL((gemm_f32_kernel<TILE, true, false, false, SPLIT>), grid, dim3(256), 0, stream, g, tm, tn);
+      hipLaunchKernelGGL((gemm_f32_kernel<TILE, true, false, SPLIT>), grid, dim3(256), 0, stream, g, tm, tn);
   } else {
     if (vec)
-      hipLaunchKernelGGL((gemm_f32_kernel<TILE, false, true, false, SPLIT>), grid, dim3(256), 0, stream, g, tm, tn);
+      hipLaunchKernelGGL((gemm_f32_kernel<TILE, false, true, SPLIT>), grid, dim3(256), 0, stream, g, tm, tn);
     else
-      hipLaunchKernelGGL((gemm_f32_kernel<TILE, false, false, false, SPLIT>), grid, dim3(256), 0, stream, g, tm, tn);
+      hipLaunchKernelGGL((gemm_f32_kernel<TILE, false, false, SPLIT>), grid, dim3(256), 0, stream, g, tm, tn);
   }
 }
 
@@ -567,12 +537,7 @@ template <int TILE>
 void launch_gemm(hipStream_t stream, const GemmF32& g, bool vec, int64_t nz, bool split) {
   const int64_t tm = cdiv(g.M, (int64_t)TILE), tn = cdiv(g.N, (int64_t)TILE);
   dim3 grid((unsigned)(tm * tn), 1, (unsigned)nz);
-  if (g.pot_nb > 0) {  // the factor's panel update (B given N×K)
-    if (vec)
-      hipLaunchKernelGGL((gemm_f32_kernel<TILE, true, true, true, false>), grid, dim3(256), 0, stream, g, tm, tn);
-    else
-      hipLaunchKernelGGL((gemm_f32_kernel<TILE, true, false, true, false>), grid, dim3(256), 0, stream, g, tm, tn);
-  } else if (split) {
+  if (split) {
     launch_variant<TILE, true>(stream, g, vec, grid, tm, tn);
   } else {
     launch_variant<TILE, false>(stream, g, vec, grid, tm, tn);
@@ -599,16 +564,12 @@ int gemm_f32(hipStream_t stream, const GemmF32& g) {
                             s1 % 4 == 0 && s2 % 4 == 0);
   };
   const bool vec = al(g.A, g.lda, g.sA, g.sA2) && al(g.B, g.ldb, g.sB, g.sB2);
-  G2PTQ_CHECK(g.pot_nb == 0 || (g.b_kcontig && g.pot_nb <= 64 && g.pot_nb <= g.M &&
-                                g.pot_nb <= g.N && g.pot_st && g.pot_info && g.batch2 == 1),
-              "gemm_f32: fused factor needs B given N×K, a block of at most 64 inside D, "
-              "status pointers and one batch level");
   // 128×128 tiles unless that grid would leave most of the 256 CUs (two
   // workgroups each) idle.
   // Products with K >= 128 run on the bf16 matrix cores from split operands
   // (about 1.3x the fp32 MFMA rate, and no less accurate); the short-K updates
   // of the factor's panels are latency-bound and keep the fp32 MFMAs.
-  const bool split = g.pot_nb == 0 && g.K >= 128;
+  const bool split = g.K >= 128;
   G2PTQ_CHECK(!split || g.b_kcontig || g.ldb < (1ll << 27),
               "gemm_f32: ldb %lld too large for the split path's 32-bit row offsets",
               (long long)g.ldb);
