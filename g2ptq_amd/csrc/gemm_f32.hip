@@ -398,12 +398,38 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmF32 g, int64_t tm,
     // Step t: the MMAs of slab t (buffer t % 2), then slab t+1 goes from its
     // register set into the other buffer and that set loads slab t+5.  Slabs
     // past the end load zeros and skip their MMAs.
+    // Interleave the step's MFMAs with the next slab's split (VALU), LDS
+    // stores and global loads, so one wave's conversions overlap its own
+    // matrix-core work instead of waiting behind the whole MFMA burst.
+    constexpr int NMF = 6 * NBLK * NBLK;                   // MFMAs per step
+#define GS_PATTERN()                                                                           \
+  do {                                                                                         \
+    __builtin_amdgcn_sched_group_barrier(0x100, 6 * NBLK, 0); /* DS read */                    \
+    __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);        /* VALU */                       \
+    _Pragma("unroll") for (int r_ = 0; r_ < NMF; ++r_) {                                       \
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);      /* MFMA */                       \
+      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);                                       \
+      if (r_ % 2 == 1) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0); /* DS write */       \
+      if (r_ % 4 == 3) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0); /* VMEM read */      \
+    }                                                                                          \
+  } while (0)
 #define GS_STEP(t, RA_, RB_, BS_)                                                              \
   do {                                                                                         \
     __builtin_amdgcn_sched_barrier(0);                                                         \
     if ((t) < nk) GS_MMA((t) & 1);                                                             \
     GS_STORE(RA_, RB_, BS_, ((t) + 1) & 1);                                                    \
     GS_LOAD(RA_, RB_, BS_, (t) + 5);                                                           \
+    __builtin_amdgcn_sched_barrier(0);                                                         \
+    __syncthreads();                                                                           \
+  } while (0)
+    // A step known to be inside the K range: one basic block, interleaved.
+#define GS_STEP_IN(t, RA_, RB_, BS_)                                                           \
+  do {                                                                                         \
+    __builtin_amdgcn_sched_barrier(0);                                                         \
+    GS_MMA((t) & 1);                                                                           \
+    GS_STORE(RA_, RB_, BS_, ((t) + 1) & 1);                                                    \
+    GS_LOAD(RA_, RB_, BS_, (t) + 5);                                                           \
+    GS_PATTERN();                                                                              \
     __builtin_amdgcn_sched_barrier(0);                                                         \
     __syncthreads();                                                                           \
   } while (0)
@@ -417,7 +443,14 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmF32 g, int64_t tm,
       GS_LOAD(ra0, rb0, bs0, 4);
     }
     __syncthreads();
-    for (int kt = 0; kt < nk; kt += 4) {
+    int kt = 0;
+    for (; kt + 4 <= nk; kt += 4) {
+      GS_STEP_IN(kt, ra1, rb1, bs1);
+      GS_STEP_IN(kt + 1, ra2, rb2, bs2);
+      GS_STEP_IN(kt + 2, ra3, rb3, bs3);
+      GS_STEP_IN(kt + 3, ra0, rb0, bs0);
+    }
+    if (kt < nk) {
       GS_STEP(kt, ra1, rb1, bs1);
       GS_STEP(kt + 1, ra2, rb2, bs2);
       GS_STEP(kt + 2, ra3, rb3, bs3);
@@ -428,6 +461,8 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmF32 g, int64_t tm,
 #undef GS_STORE
 #undef GS_MMA
 #undef GS_STEP
+#undef GS_STEP_IN
+#undef GS_PATTERN
   } else {
     // Slabs are processed in pairs; a trailing odd slab and the prefetches
     // past the end load zeros (k >= K is masked), which add nothing.
