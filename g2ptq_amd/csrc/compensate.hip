@@ -30,6 +30,33 @@ __global__ void triu1_kernel(float* t, int64_t C) {
   }
 }
 
+// Ut[j][i] = U[i][j] for the 64×64 tiles on and above U's diagonal (Ut's
+// tiles below its diagonal are not written): the block tails read the
+// factor as N×K rows, k-contiguous, which the GEMM stages and splits once
+// per workgroup (faster than splitting a K×N operand per wave).
+__global__ __launch_bounds__(256) void transpose_upper_kernel(const float* __restrict__ U,
+                                                              int64_t C, float* __restrict__ Ut) {
+  const int64_t bi = blockIdx.y, bj = blockIdx.x, b = blockIdx.z;
+  if (bi > bj) return;
+  __shared__ float t[64][65];
+  const float* Ub = U + b * C * C;
+  float* Tb = Ut + b * C * C;
+  const int c = threadIdx.x & 63, r0 = threadIdx.x >> 6;
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const int r = r0 + 4 * q;
+    const int64_t i = bi * 64 + r, j = bj * 64 + c;
+    t[r][c] = (i < C && j < C) ? Ub[i * C + j] : 0.f;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const int r = r0 + 4 * q;
+    const int64_t j = bj * 64 + r, i = bi * 64 + c;
+    if (i < C && j < C) Tb[j * C + i] = t[c][r];
+  }
+}
+
 // diag(A⁻¹)[c] = Σ_i U[i][c]² (A⁻¹ = UᵀU): a workgroup per 64 columns,
 // four row phases per column (rows i ≡ p mod 4, four loads in flight per
 // thread), the phases summed in a fixed order.
@@ -145,17 +172,19 @@ static int64_t super_block(int variant, int64_t bs, int64_t groupsize, int stati
 
 extern "C" int g2ptq_compensate_workspace(int variant, int64_t B, int64_t R, int64_t C,
                                           int64_t blocksize, size_t* bytes) {
-  (void)C;
   G2PTQ_CHECK(bytes != nullptr, "compensate_workspace: null out");
   // The super-block width depends on the group layout; size for the widest
   // (a dynamic group size that is coprime to the block size is bounded by C),
   // twice: the error columns of consecutive super-blocks alternate between
   // two buffers so that one's far tail can run while the next is swept.
   // G2PTQ adds one block's near-tail operand (E2, below).
+  // Then the factor transposed (Ut, B·C² floats), which lets every block
+  // tail read it k-contiguous.
   const int64_t bs = std::max<int64_t>(blocksize, 1);
   const int64_t widest = std::max<int64_t>(512, bs);
   *bytes = 2 * al256((size_t)B * R * widest * 4) +
-           (variant == G2PTQ_VARIANT_G2PTQ ? al256((size_t)B * R * bs * 4) : 0);
+           (variant == G2PTQ_VARIANT_G2PTQ ? al256((size_t)B * R * bs * 4) : 0) +
+           al256((size_t)B * C * C * 4);
   return G2PTQ_OK;
 }
 
@@ -169,7 +198,8 @@ static int compensate_impl(hipStream_t s, int variant, int64_t B, int64_t R, int
                            int mse_grid, float mse_norm, float mse_maxshrink, const float* hdiag,
                            int64_t hblocks, const int* colgroup, float* scale_tab,
                            float* zero_tab, float* Q, float* Wint, float* Scale, int* flags,
-                           void* ws, size_t ws_bytes, bool allow_overlap) {
+                           void* ws, size_t ws_bytes, bool allow_overlap,
+                           bool allow_transpose) {
   G2PTQ_CHECK(W && U && scale_tab && zero_tab && Q, "compensate: null pointer");
   G2PTQ_CHECK(bits >= 2 && bits <= 16, "compensate: bits=%d unsupported", bits);
   G2PTQ_CHECK(bs >= 1 && bs <= kMaxBlock, "compensate: blocksize %lld not in [1, %d]",
@@ -194,19 +224,33 @@ static int compensate_impl(hipStream_t s, int variant, int64_t B, int64_t R, int
   }
   G2PTQ_CHECK(ws && ws_bytes >= need + need2, "compensate: workspace %zu < %zu", ws_bytes,
               need + need2);
+  // Workspace layout: E (one super-block's error columns), E2 (G2PTQ), then,
+  // as far as the workspace reaches, Ut (the factor transposed, for
+  // k-contiguous tail products) and a second E buffer (lookahead).
+  const size_t need_t = al256((size_t)B * C * C * 4);
+  const bool transposed = allow_transpose && ws_bytes >= need + need2 + need_t;
   // Lookahead: with room for two error buffers, and outside graph capture,
   // the tail of a super-block beyond the next super-block's columns (the
   // "far" tail) runs on the side stream while the next super-block is swept.
   hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
   G2PTQ_HIP(hipStreamIsCapturing(s, &capture));
-  const bool overlap = allow_overlap && ws_bytes >= 2 * need + need2 &&
+  const size_t base = need + need2 + (transposed ? need_t : 0);
+  const bool overlap = allow_overlap && ws_bytes >= base + need &&
                        capture == hipStreamCaptureStatusNone && SB < C;
   SideStream side;
   if (overlap) G2PTQ_TRY(side_stream(s, side));
-  float* Ebuf[2] = {static_cast<float*>(ws),
-                    overlap ? static_cast<float*>(ws) + need / 4 : static_cast<float*>(ws)};
-  float* E2buf = need2 ? static_cast<float*>(ws) + (overlap ? 2 : 1) * need / 4 : nullptr;
+  char* wsb = static_cast<char*>(ws);
+  float* Ebuf[2] = {reinterpret_cast<float*>(wsb),
+                    reinterpret_cast<float*>(wsb + (overlap ? base : 0))};
+  float* E2buf = need2 ? reinterpret_cast<float*>(wsb + need) : nullptr;
+  float* Ut = transposed ? reinterpret_cast<float*>(wsb + need + need2) : nullptr;
   const int64_t RC = R * C, CC = C * C;
+  if (Ut) {
+    const unsigned nt = (unsigned)cdiv(C, (int64_t)64);
+    hipLaunchKernelGGL(transpose_upper_kernel, dim3(nt, nt, (unsigned)B), dim3(256), 0, s, U, C,
+                       Ut);
+    G2PTQ_LAUNCHED();
+  }
 
   // W[:, :, c0:c1] -= Ecols · U[k0:k1, c0:c1]  (+ GPTAQ: += Q[:, :, k0:k1] · P[k0:k1, c0:c1]),
   // on stream q.  Every tail reads and writes only its own columns c0..c1.
@@ -215,7 +259,11 @@ static int compensate_impl(hipStream_t s, int variant, int64_t B, int64_t R, int
     GemmF32 t;
     t.M = R; t.N = c1 - c0; t.K = k1 - k0; t.batch = B;
     t.A = Ecols; t.lda = lde; t.sA = R * lde;
-    t.B = U + k0 * C + c0; t.ldb = C; t.sB = CC;
+    if (Ut) {  // U[k0:k1, c0:c1] as rows of Ut (every c > every k: Ut's written tiles)
+      t.B = Ut + c0 * C + k0; t.ldb = C; t.sB = CC; t.b_kcontig = 1;
+    } else {
+      t.B = U + k0 * C + c0; t.ldb = C; t.sB = CC;
+    }
     t.C = W + c0; t.ldc = C; t.sC = RC;
     t.D = W + c0; t.ldd = C; t.sD = RC;
     t.alpha = -1.f; t.beta = 1.f;
@@ -228,7 +276,7 @@ static int compensate_impl(hipStream_t s, int variant, int64_t B, int64_t R, int
     if (variant == G2PTQ_VARIANT_GPTAQ) {
       GemmF32 p = t;  // W += Q1 · P[k0:k1, c0:c1]
       p.A = Q + k0; p.lda = C; p.sA = RC;
-      p.B = P + k0 * C + c0;
+      p.B = P + k0 * C + c0; p.ldb = C; p.sB = CC; p.b_kcontig = 0;
       p.alpha = 1.f;
       G2PTQ_TRY(gemm_f32(q, p));
     } else if (variant == G2PTQ_VARIANT_G2PTQ) {
@@ -359,7 +407,7 @@ extern "C" int g2ptq_compensate(void* stream, int variant, int64_t B, int64_t R,
   return compensate_impl(as_stream(stream), variant, B, R, C, bs, W, U, P, Z, GH, bits, sym,
                          groupsize, static_groups, mse_grid, mse_norm, mse_maxshrink, hdiag,
                          hblocks, colgroup, scale_tab, zero_tab, Q, Wint, Scale, flags, ws,
-                         ws_bytes, true);
+                         ws_bytes, true, true);
 }
 
 // Scratch memory of g2ptq_compensate_noalloc: the error columns of the loop,
@@ -406,7 +454,7 @@ extern "C" int g2ptq_compensate_noalloc(void* stream, int variant, int64_t B, in
   return compensate_impl(as_stream(stream), variant, B, R, C, bs, W, U, P, Z, GH, bits, sym,
                          groupsize, static_groups, mse_grid, mse_norm, mse_maxshrink, hdiag,
                          hblocks, colgroup, scale_tab, zero_tab, Q, Wint, Scale, flags, ws,
-                         kScratchBytes, false);
+                         kScratchBytes, false, false);
 }
 
 extern "C" int g2ptq_gptaq_p(void* stream, const float* Dx, const float* U, int64_t B, int64_t C,
