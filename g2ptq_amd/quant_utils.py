@@ -14,6 +14,8 @@ symmetric ``s = max(|xmin|, xmax) / (bit_range / 2)``, ``z = 0``; asymmetric
 ``q = clamp(round(x / s) + z, minq, maxq)`` with round-half-to-even and
 ``x̂ = s·(q - z)``.
 """
+import collections
+
 import torch
 
 from . import _lib
@@ -75,6 +77,9 @@ def sym_quant_dequant(x, scale, maxq):
     return _fake_quant_rows(x, scale, torch.zeros_like(scale), maxq, want_codes=False)[0]
 
 
+_CONTAINERS = frozenset((dict, collections.OrderedDict, set, list))
+
+
 class WeightQuantizer(torch.nn.Module):
     """Drop-in for ``utils/quant_utils.py:341-465`` (``WeightQuantizer``)."""
 
@@ -88,18 +93,18 @@ class WeightQuantizer(torch.nn.Module):
         """An independent copy, as ``copy.deepcopy`` of the module would make,
         without nn.Module's generic deep-copy machinery (make_group_quantizers
         copies one quantizer per group: 112 copies for a 14336-column layer)."""
-        cls = self.__class__
-        new = cls.__new__(cls)
+        new = object.__new__(self.__class__)
         memo[id(self)] = new
-        d = new.__dict__
-        for k, v in self.__dict__.items():
-            if k == "_buffers":
-                v = v.__class__((n, None if b is None else b.clone()) for n, b in v.items())
-            elif isinstance(v, (dict, set, list)):
-                v = v.copy()
+        src = self.__dict__
+        d = src.copy()  # scalars and flags shared, containers and tensors replaced below
+        for k, v in src.items():
+            t = type(v)
+            if t in _CONTAINERS:
+                d[k] = v.copy()
             elif isinstance(v, torch.Tensor):
-                v = v.clone()
-            d[k] = v
+                d[k] = v.clone()
+        d["_buffers"] = {n: None if b is None else b.clone() for n, b in src["_buffers"].items()}
+        object.__setattr__(new, "__dict__", d)
         return new
 
     def configure(self, bits, perchannel: bool = False, sym: bool = True, mse: bool = False,

@@ -102,8 +102,9 @@ class SharedInputHessian:
         for inst in insts:
             inst.H = None
         _core.prepare_hessian(H, W)
-        U, _ = _core.factor(H, percdamp, self, key=False)
+        # host work that does not need the factor goes before its status read
         qs = [copy.deepcopy(q) for q in insts[0].quantizer]
+        U, _ = _core.factor(H, percdamp, self, key=False)
         Q, W_int, Scale = _core.compensate(_lib.VARIANT_GPTQ, W, U, qs, blocksize, groupsize,
                                            False, None, flags)
         off = 0
