@@ -181,23 +181,23 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmF32 g, int64_t tm,
   const int rb_k = tid / KQ, rb_nq = (tid % KQ) * 4;
 
   auto ld4 = [&](const float* base, int64_t ld, int64_t r, int64_t c, int64_t R, int64_t Ccols) {
+    if (VEC) {
+      // Rows of a multiple of 4 columns (c is one): a 16-byte chunk is wholly
+      // inside or outside, so one load from a clamped address and a select
+      // replace per-element tests (no branches).
+      const bool ok = r < R && c < Ccols;
+      const uint4 w = *reinterpret_cast<const uint4*>(base + (ok ? r * ld + c : 0));
+      const uint32_t m = ok ? 0xffffffffu : 0u;  // a mask, not a branch around the load
+      return make_float4(__uint_as_float(w.x & m), __uint_as_float(w.y & m),
+                         __uint_as_float(w.z & m), __uint_as_float(w.w & m));
+    }
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
     if (r < R) {
       const float* p = base + r * ld + c;
-      if (VEC) {
-        if (c + 3 < Ccols) {
-          v = *reinterpret_cast<const float4*>(p);
-        } else {
-          if (c < Ccols) v.x = p[0];
-          if (c + 1 < Ccols) v.y = p[1];
-          if (c + 2 < Ccols) v.z = p[2];
-        }
-      } else {
-        if (c < Ccols) v.x = p[0];
-        if (c + 1 < Ccols) v.y = p[1];
-        if (c + 2 < Ccols) v.z = p[2];
-        if (c + 3 < Ccols) v.w = p[3];
-      }
+      if (c < Ccols) v.x = p[0];
+      if (c + 1 < Ccols) v.y = p[1];
+      if (c + 2 < Ccols) v.z = p[2];
+      if (c + 3 < Ccols) v.w = p[3];
     }
     return v;
   };
@@ -598,7 +598,9 @@ int gemm_f32(hipStream_t stream, const GemmF32& g) {
     return p == nullptr || ((reinterpret_cast<uintptr_t>(p) & 15) == 0 && ld % 4 == 0 &&
                             s1 % 4 == 0 && s2 % 4 == 0);
   };
-  const bool vec = al(g.A, g.lda, g.sA, g.sA2) && al(g.B, g.ldb, g.sB, g.sB2);
+  // ... and whole 16-byte chunks along k (and along n for B given K×N).
+  const bool vec = al(g.A, g.lda, g.sA, g.sA2) && al(g.B, g.ldb, g.sB, g.sB2) && g.K % 4 == 0 &&
+                   (g.b_kcontig || g.N % 4 == 0);
   // 128×128 tiles unless that grid would leave most of the 256 CUs (two
   // workgroups each) idle.
   // Products with K >= 128 run on the bf16 matrix cores from split operands
