@@ -15,9 +15,27 @@ from . import _lib
 
 def make_group_quantizers(quantizer, columns, groupsize):
     """gptq_utils/common_utils.py:13-16: a deep copy of ``quantizer`` per
-    ``groupsize``-column group (one for ``groupsize == -1``)."""
+    ``groupsize``-column group (one for ``groupsize == -1``).
+
+    For a WeightQuantizer the copies' buffers are cloned together: one tensor
+    per buffer name holding every copy's value, unbound into per-copy views
+    (each an independent tensor of the original's shape, as a clone is), so a
+    14336-column layer's 112 copies cost two tensor operations instead of 224.
+    """
+    from .quant_utils import WeightQuantizer
     count = 1 if groupsize == -1 else -(-columns // groupsize)
-    return [copy.deepcopy(quantizer) for _ in range(count)]
+    if type(quantizer) is not WeightQuantizer or count == 1:
+        return [copy.deepcopy(quantizer) for _ in range(count)]
+    bufs = quantizer._buffers
+    per_copy = {n: (None if b is None else
+                    b.detach().unsqueeze(0).expand(count, *b.shape).clone().unbind(0))
+                for n, b in bufs.items()}
+    out = []
+    for i in range(count):
+        q = quantizer.__deepcopy__({}, clone_buffers=False)
+        q.__dict__["_buffers"] = {n: (None if v is None else v[i]) for n, v in per_copy.items()}
+        out.append(q)
+    return out
 
 
 def merge_group_quantizers(quantizers, start, end, groupsize):

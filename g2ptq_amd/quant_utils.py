@@ -89,7 +89,7 @@ class WeightQuantizer(torch.nn.Module):
         self.register_buffer("zero", torch.zeros(shape))
         self._ready = False
 
-    def __deepcopy__(self, memo):
+    def __deepcopy__(self, memo, clone_buffers=True):
         """An independent copy, as ``copy.deepcopy`` of the module would make,
         without nn.Module's generic deep-copy machinery (make_group_quantizers
         copies one quantizer per group: 112 copies for a 14336-column layer)."""
@@ -103,7 +103,8 @@ class WeightQuantizer(torch.nn.Module):
                 d[k] = v.copy()
             elif isinstance(v, torch.Tensor):
                 d[k] = v.clone()
-        d["_buffers"] = {n: None if b is None else b.clone() for n, b in src["_buffers"].items()}
+        if clone_buffers:
+            d["_buffers"] = {n: None if b is None else b.clone() for n, b in src["_buffers"].items()}
         object.__setattr__(new, "__dict__", d)
         return new
 
