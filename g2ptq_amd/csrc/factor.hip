@@ -250,9 +250,18 @@ __global__ __launch_bounds__(256) void panel_step_kernel(PanelArgs p) {
   panel_load(Xj, Wb, C, p.j, p.j, p.nbk, p.nbk, vec);
   panel_load(Ai, Wb, C, ri, p.j, C - ri, p.nbk, vec);
   if (n != i) panel_load(An, Wb, C, rn, p.j, C - rn, p.nbk, vec);
-  __syncthreads();
   const int wave = threadIdx.x >> 6, wm = wave >> 1, wn = wave & 1;
   const int lane = threadIdx.x & 63, lr = lane & 31, lh = lane >> 5;
+  // The update's Â operand, read with the raw blocks (nothing in this launch
+  // writes it before this workgroup's own epilogue).
+  const int64_t c = rn + wn * 32 + lr;
+  float cv[16];
+#pragma unroll
+  for (int v = 0; v < 16; ++v) {
+    const int64_t r = ri + wm * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+    cv[v] = (r < C && c < p.pe) ? 1.f * Wb[r * C + c] : 0.f;
+  }
+  __syncthreads();
   const f32x16 li = panel_mma(Ai, Xj, wm * 32, wn * 32);
   f32x16 ln;
   if (n != i) ln = panel_mma(An, Xj, wm * 32, wn * 32);
@@ -278,13 +287,6 @@ __global__ __launch_bounds__(256) void panel_step_kernel(PanelArgs p) {
   // panel; the tile (0, 0) sends the next diagonal block to LDS instead.
   const bool pot = p.pot_nb > 0 && i == 0 && n == 0;
   float* Xs = Xj;  // the potrf staging reuses X_jj's buffer (read above)
-  const int64_t c = rn + wn * 32 + lr;
-  float cv[16];
-#pragma unroll
-  for (int v = 0; v < 16; ++v) {
-    const int64_t r = ri + wm * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
-    cv[v] = (r < C && c < p.pe) ? 1.f * Wb[r * C + c] : 0.f;
-  }
 #pragma unroll
   for (int v = 0; v < 16; ++v) {
     const int rl = wm * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
