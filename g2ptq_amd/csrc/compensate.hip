@@ -175,21 +175,23 @@ extern "C" int g2ptq_compensate_workspace(int variant, int64_t B, int64_t R, int
   G2PTQ_CHECK(bytes != nullptr, "compensate_workspace: null out");
   // The super-block width depends on the group layout; size for the widest
   // (a dynamic group size that is coprime to the block size is bounded by C),
-  // twice: the error columns of consecutive super-blocks alternate between
-  // two buffers so that one's far tail can run while the next is swept.
+  // three times: the error columns of consecutive super-blocks rotate over
+  // three buffers so that the far tails of the two before run on the side
+  // stream while the next is swept.
   // G2PTQ adds one block's near-tail operand (E2, below).
   // Then the factor transposed (Ut, B·C² floats), which lets every block
   // tail read it k-contiguous.
   const int64_t bs = std::max<int64_t>(blocksize, 1);
   const int64_t widest = std::max<int64_t>(512, bs);
-  *bytes = 2 * al256((size_t)B * R * widest * 4) +
+  *bytes = 3 * al256((size_t)B * R * widest * 4) +
            (variant == G2PTQ_VARIANT_G2PTQ ? al256((size_t)B * R * bs * 4) : 0) +
            al256((size_t)B * C * C * 4);
   return G2PTQ_OK;
 }
 
 // The lazy-batch loop behind g2ptq_compensate and g2ptq_compensate_noalloc.
-// ws holds the error columns of one super-block (two with overlap allowed);
+// ws holds the error columns of one super-block (two or three with overlap
+// allowed);
 // every column of it is written by a sweep before a tail reads it, so it
 // needs no clearing.
 static int compensate_impl(hipStream_t s, int variant, int64_t B, int64_t R, int64_t C,
@@ -226,22 +228,29 @@ static int compensate_impl(hipStream_t s, int variant, int64_t B, int64_t R, int
               need + need2);
   // Workspace layout: E (one super-block's error columns), E2 (G2PTQ), then,
   // as far as the workspace reaches, Ut (the factor transposed, for
-  // k-contiguous tail products) and a second E buffer (lookahead).
+  // k-contiguous tail products) and a second and third E buffer (lookahead).
   const size_t need_t = al256((size_t)B * C * C * 4);
   const bool transposed = allow_transpose && ws_bytes >= need + need2 + need_t;
   // Lookahead: with room for two error buffers, and outside graph capture,
   // the tail of a super-block beyond the next super-block's columns (the
   // "far" tail) runs on the side stream while the next super-block is swept.
+  // With a third buffer the far tail goes out in two launches, the columns
+  // of the super-block after next first: the caller's stream then waits only
+  // for that part (and the side stream's earlier work), and the rest of the
+  // far tail runs beside two sweeps instead of one.
   hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
   G2PTQ_HIP(hipStreamIsCapturing(s, &capture));
   const size_t base = need + need2 + (transposed ? need_t : 0);
   const bool overlap = allow_overlap && ws_bytes >= base + need &&
                        capture == hipStreamCaptureStatusNone && SB < C;
+  const bool deep = overlap && ws_bytes >= base + 2 * need;
+  const int nbuf = deep ? 3 : overlap ? 2 : 1;
   SideStream side;
   if (overlap) G2PTQ_TRY(side_stream(s, side));
   char* wsb = static_cast<char*>(ws);
-  float* Ebuf[2] = {reinterpret_cast<float*>(wsb),
-                    reinterpret_cast<float*>(wsb + (overlap ? base : 0))};
+  float* Ebuf[3] = {reinterpret_cast<float*>(wsb),
+                    reinterpret_cast<float*>(wsb + (overlap ? base : 0)),
+                    reinterpret_cast<float*>(wsb + (deep ? base + need : 0))};
   float* E2buf = need2 ? reinterpret_cast<float*>(wsb + need) : nullptr;
   float* Ut = transposed ? reinterpret_cast<float*>(wsb + need + need2) : nullptr;
   const int64_t RC = R * C, CC = C * C;
@@ -294,11 +303,14 @@ static int compensate_impl(hipStream_t s, int variant, int64_t B, int64_t R, int
   // Every column receives the tails of the super-blocks before it in order:
   // the far tail of super-block p (columns from p + 2 on, side stream) lands
   // before the near tail of p + 1 (columns of p + 2, caller's stream), which
-  // waits for it; that wait also frees p's error buffer for p + 2's sweeps.
-  bool far_pending = false;
+  // waits for it (for its first launch, with three buffers: the columns of
+  // p + 2; the side stream runs its launches in order, so everything issued
+  // there before is done too); that wait also frees the error buffer that
+  // p + 1's successor overwrites (p's with two buffers, p − 1's with three).
+  bool far_pending = false, side_used = false;
   for (int64_t s0 = 0, sbi = 0; s0 < C; s0 += SB, ++sbi) {
     const int64_t s1 = std::min(s0 + SB, C);
-    float* E = Ebuf[sbi & 1];
+    float* E = Ebuf[sbi % nbuf];
     // GPTQ with full 128-column blocks, 16 lanes per row and groups fitted in
     // the sweep (or static): one launch sweeps the whole super-block and
     // applies its near tails itself.
@@ -381,18 +393,24 @@ static int compensate_impl(hipStream_t s, int variant, int64_t B, int64_t R, int
         continue;
       }
       const int64_t nxt = std::min(s1 + SB, C);  // end of the next super-block's columns
+      const int64_t nxt2 = std::min(nxt + SB, C);  // ... and of the one after
       if (far_pending) G2PTQ_HIP(hipStreamWaitEvent(s, side.tailed, 0));
       far_pending = nxt < C;
       if (far_pending) {
         G2PTQ_HIP(hipEventRecord(side.swept, s));
         G2PTQ_HIP(hipStreamWaitEvent(side.stream, side.swept, 0));
-        G2PTQ_TRY(tail_on(side.stream, E, SB, s0, s1, nxt, C));
+        G2PTQ_TRY(tail_on(side.stream, E, SB, s0, s1, nxt, deep ? nxt2 : C));
         G2PTQ_HIP(hipEventRecord(side.tailed, side.stream));
+        if (deep && nxt2 < C) G2PTQ_TRY(tail_on(side.stream, E, SB, s0, s1, nxt2, C));
+        side_used = true;
       }
       G2PTQ_TRY(tail(E, SB, s0, s1, s1, nxt));
     }
   }
-  if (far_pending) G2PTQ_HIP(hipStreamWaitEvent(s, side.tailed, 0));
+  if (side_used) {  // the side stream's last launches (the event marks only a first part)
+    G2PTQ_HIP(hipEventRecord(side.tailed, side.stream));
+    G2PTQ_HIP(hipStreamWaitEvent(s, side.tailed, 0));
+  }
   return G2PTQ_OK;
 }
 

@@ -478,12 +478,13 @@ def test_factor_damp_retry_batched_multipanel(dev):
 @pytest.mark.parametrize("variant,groupsize", [(0, 128), (0, -1), (1, 128), (2, 128), (0, 96)])
 def test_compensate_far_tail_lookahead_is_bit_identical(dev, variant, groupsize):
     """The native loop with room for two error buffers runs each super-block's far
-    tail on the side stream while the next super-block is swept; every column
-    still receives its tails in order, so the results equal the one-buffer
-    (serial) schedule bit for bit.  C = 1664 gives four 512-column super-blocks,
-    the last one ragged."""
+    tail on the side stream while the next super-block is swept, with three it
+    splits the far tail in two launches (the super-block after next first) that
+    run beside two sweeps; every column still receives its tails in order, so
+    both results equal the one-buffer (serial) schedule bit for bit.  C = 2688
+    gives six 512-column super-blocks, the last one ragged."""
     from g2ptq_amd import _lib
-    B, R, C, bs, bits = 2, 300, 1664, 128, 4
+    B, R, C, bs, bits = 2, 300, 2688, 128, 4
     g = gen(7100 + 10 * variant + (groupsize > 0))
     W0 = torch.randn(B, R, C, generator=g) * 0.05
     U = torch.triu(torch.randn(B, C, C, generator=g) * (0.5 / C ** 0.5), diagonal=1)
@@ -496,10 +497,11 @@ def test_compensate_far_tail_lookahead_is_bit_identical(dev, variant, groupsize)
     Pd = P.to(dev) if P is not None else None
     Zd = Z.to(dev) if Z is not None else None
     full = _lib.query_size("g2ptq_compensate_workspace", variant, B, R, C, bs)
-    # without one of the two super-block error buffers the loop runs serially
+    # one super-block error buffer less: two buffers (far tail in one launch);
+    # two less: the loop runs serially
     one = -(-(B * R * max(512, bs) * 4) // 256) * 256
     outs = []
-    for ws_bytes in (full, full - one):
+    for ws_bytes in (full, full - one, full - 2 * one):
         W = W0.clone().to(dev)
         GH = GH0.clone().to(dev) if GH0 is not None else None
         stab = torch.empty(ngroups, B * R, device=dev)
@@ -517,8 +519,9 @@ def test_compensate_far_tail_lookahead_is_bit_identical(dev, variant, groupsize)
                   _lib.ptr(Wi), _lib.ptr(Sc), _lib.ptr(flags), _lib.ptr(ws), ws_bytes)
         torch.cuda.synchronize()
         outs.append([t.cpu() for t in (Q, Wi, Sc, W, stab) + ((GH,) if GH is not None else ())])
-    for a, b, name in zip(outs[0], outs[1], ("Q", "W_int", "Scale", "W", "scales", "GH")):
-        assert torch.equal(a, b), name
+    for run in (0, 1):
+        for a, b, name in zip(outs[run], outs[2], ("Q", "W_int", "Scale", "W", "scales", "GH")):
+            assert torch.equal(a, b), (run, name)
 
 
 @pytest.mark.parametrize("K", [64, 128, 1536])
