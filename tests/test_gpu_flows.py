@@ -261,6 +261,16 @@ def test_flow_from_x_matches_oracle(dev, case):
         assert_beta_close(gq._beta.cpu(), ref["beta"], name)
 
 
+def test_flow_from_x_quad_lanes(dev):
+    """Config 2's GPTQ W4 sym g128 with 2 × 4200 rows: more than 8192 rows
+    take the sweep with a quad of lanes per row (the gate/up projections'
+    28672 rows do).  Against the oracle under the parity protocol."""
+    print("flow from X: gptq w4 sym g128, 2 x 4200 rows", flush=True)
+    layers, quantizers, ref, W0, H, gq = run_flow_from_x(dev, "gptq", 4, True, 128, R=4200,
+                                                         seed=395)
+    assert_flow_parity("gptq quad lanes", layers, quantizers, ref, W0, H, 4, 128, False)
+
+
 def test_g2ptq_dead_features_keep_gradients(dev):
     """g2ptq_utils.py:394-401: a dead input feature (zero Hessian diagonal)
     zeroes that weight column and sets H[d, d] = 1, but the gradients are

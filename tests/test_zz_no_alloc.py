@@ -96,10 +96,11 @@ def test_noalloc_beyond_the_super_block_range(dev):
     """B·R above 16384 rows: the scratch holds one 128-column block's errors
     only, and the result equals g2ptq_compensate's with a one-block
     workspace; then a small call again."""
-    for i, (B, R, C) in enumerate(((1, 20000, 384), (1, 512, 256))):
+    for i, (B, R, C) in enumerate(((1, 20000, 640), (1, 512, 256))):
         print(f"noalloc large case call {i} B={B} R={R} C={C}", flush=True)
         inputs = _inputs(B, R, C, 950 + i)
-        sb = 512 if B * R * 512 * 4 <= SCRATCH else BS
+        width = min(512, math.ceil(C / BS) * BS)  # the loop's super-block width
+        sb = width if B * R * width * 4 <= SCRATCH else BS
         ref = _run("g2ptq_compensate", 0, inputs, 4, True, 128, ws_bytes=_al256(B * R * sb * 4))
         got = _run("g2ptq_compensate_noalloc", 0, inputs, 4, True, 128)
         for k in ref:
