@@ -20,6 +20,8 @@ Prints one JSON line (rank 0).  ``--gpus N`` with N > 1 exits: this build
 runs on one GPU.
 """
 import argparse
+import contextlib
+import gc
 import json
 import os
 import platform
@@ -295,6 +297,23 @@ def workload_cfg4(dev, steps, warmup):
                   f"{stats['max_tokens']}), GPTQ W4 sym g128, 64 linears per launch")
 
 
+@contextlib.contextmanager
+def quiet_collector():
+    """The timed steps with the interpreter's long-lived objects (torch's and
+    this process's set-up) moved out of the garbage collector's generations:
+    a full collection otherwise re-traverses all of them (about 60 ms on this
+    image) and, when it falls while the GPU waits for the host, stalls the
+    step (config 1 measured 6 ms per Hessian stage, 70 ms in the step with
+    the collection).  Objects the steps create are still collected; no work
+    of the path is skipped."""
+    gc.collect()
+    gc.freeze()
+    try:
+        yield
+    finally:
+        gc.unfreeze()
+
+
 def run_other(args, dev):
     make = {"cfg1": workload_cfg1, "cfg3": workload_cfg3, "cfg4": workload_cfg4,
             "cfg5": workload_cfg5}[args.workload]
@@ -307,10 +326,11 @@ def run_other(args, dev):
     for _ in range(args.warmup):
         step(ev)
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    recs = [step(ev) for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    wall = (time.perf_counter() - t0) / args.steps
+    with quiet_collector():
+        t0 = time.perf_counter()
+        recs = [step(ev) for _ in range(args.steps)]
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) / args.steps
     h = sum(e[0].elapsed_time(e[1]) for e, _ in recs) / len(recs)
     qz = sum(e[2].elapsed_time(e[3]) for e, _ in recs) / len(recs)
     flops = recs[0][1]
@@ -530,10 +550,11 @@ def g2ptq_block(dev, steps=2, warmup=1):
     for _ in range(warmup):
         step(ev)
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    recs = [step(ev) for _ in range(steps)]
-    torch.cuda.synchronize()
-    wall = (time.perf_counter() - t0) / steps
+    with quiet_collector():
+        t0 = time.perf_counter()
+        recs = [step(ev) for _ in range(steps)]
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) / steps
     h = sum(e[0].elapsed_time(e[1]) for e, _ in recs) / steps
     qz = sum(e[2].elapsed_time(e[3]) for e, _ in recs) / steps
     return {"workload": desc, "sec_per_block": round(wall, 4), "steps": steps, "warmup": warmup,
@@ -599,13 +620,14 @@ def main():
     torch.cuda.synchronize()
     hess, quant = [], []
     _stage.TIMING = []  # HIP events around every Gram launch of the timed steps
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        h, q = run_step(acts, layers, w0, args.tokens, ev)
-        hess.append(h)
-        quant.append(q)
-    torch.cuda.synchronize()
-    wall = (time.perf_counter() - t0) / args.steps
+    with quiet_collector():
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            h, q = run_step(acts, layers, w0, args.tokens, ev)
+            hess.append(h)
+            quant.append(q)
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) / args.steps
     grams, _stage.TIMING = _stage.TIMING, None
     hflops = hessian_flops(args.tokens)
     h_avg = sum(hess) / len(hess) / 1e3

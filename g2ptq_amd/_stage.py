@@ -64,6 +64,18 @@ def _ceil(x, m):
     return (x + m - 1) // m * m
 
 
+_QUERY_BYTES = 1 << 30  # buffers from this size on are checked against free memory
+_MEMORY = {}
+
+
+def _device_memory(device):
+    """Total memory of a device (cached: the property query is a device call)."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    if idx not in _MEMORY:
+        _MEMORY[idx] = torch.cuda.get_device_properties(idx).total_memory
+    return _MEMORY[idx]
+
+
 class GramStager:
     def __init__(self, columns, device, kind=KIND_GPTQ, groups=0, budget_bytes=None):
         self.C = columns
@@ -74,8 +86,7 @@ class GramStager:
         self.rows = _lib.query_size_i64("g2ptq_hessian_stage_rows", columns)
         budget = budget_bytes if budget_bytes is not None else DEFAULT_BUDGET
         if budget is None:
-            total = torch.cuda.get_device_properties(torch.device(device)).total_memory
-            budget = min(_MAX_BUDGET, total // 4)
+            budget = min(_MAX_BUDGET, _device_memory(torch.device(device)) // 4)
         per_token = self.planes * self.rows * 2
         self.max_tokens = max(_GRAM_PAD * 2, budget // per_token // _GRAM_PAD * _GRAM_PAD)
         self.buf = None
@@ -105,13 +116,17 @@ class GramStager:
         self.buf = None
         # Stay within what the device has free (other stagers of the same layer
         # group, the caller's tensors): shrink a large buffer rather than fail.
+        # Buffers under _QUERY_BYTES skip the query (a device call per buffer:
+        # the many small per-expert stagers of an MoE block would pay it often).
         per_token = self.planes * self.rows * 2
-        free, _ = torch.cuda.mem_get_info(self.device)
-        cached = torch.cuda.memory_reserved(self.device) - torch.cuda.memory_allocated(self.device)
-        avail = free + cached - _FREE_MARGIN
-        if cap * per_token > avail:
-            cap = _ceil(max(need, avail // per_token - _PITCH_SKEW - _GRAM_PAD),
-                        _GRAM_PAD) + _PITCH_SKEW
+        if cap * per_token >= _QUERY_BYTES:
+            free, _ = torch.cuda.mem_get_info(self.device)
+            cached = (torch.cuda.memory_reserved(self.device)
+                      - torch.cuda.memory_allocated(self.device))
+            avail = free + cached - _FREE_MARGIN
+            if cap * per_token > avail:
+                cap = _ceil(max(need, avail // per_token - _PITCH_SKEW - _GRAM_PAD),
+                            _GRAM_PAD) + _PITCH_SKEW
         self.buf = torch.empty(self.planes, self.rows, cap, dtype=torch.bfloat16,
                                device=self.device)
         self.cap = cap
