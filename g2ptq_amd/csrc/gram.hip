@@ -609,23 +609,36 @@ __global__ __launch_bounds__(256) void gram_reduce_kernel(G2Args a) {
 
 // Split plan.  Splits per operand half: the smallest power of two that gives
 // at least 4096 workgroups (16 waves of one 256×256 tile per CU), at most 16
-// splits in all and at least 16 KS-token stages per split.  Powers of two
-// keep every split on whole XCDs (the workgroup order is split-major and
-// XCD-contiguous), so the workgroups of one XCD read one K range; measured on
-// MI355X with random bf16 operands (C=4096: S=16; C=14336: S=4).  Every split
-// gets an even number of stages, so the staged width is K padded to a
-// multiple of 2·KS·(splits per half), at most 2048.
+// splits in all and at least 16 KS-token stages per split; then, among the
+// counts down to three quarters of it, the one whose grid fills its last wave
+// of workgroups best (one workgroup per CU, kCUs of them): C=4096 has 136
+// tiles, 2176 workgroups (8.5 waves) at 16 splits and 2040 (7.97) at 15, and
+// its Gram takes 4.25 instead of 4.49 ms; C=14336 keeps 4 splits (6384
+// workgroups, 24.9 waves).  Measured on MI355X with random bf16 operands.
+// Every split gets an even number of stages, so the staged width is K padded
+// to a multiple of 2·KS·(splits per half), at most 2048.
 struct GramPlan {
   int S;        // total splits
   int64_t Kp;   // padded tokens per half
   int64_t kc;   // tokens per split
 };
 
+constexpr int64_t kCUs = 256;  // MI355X
+
+// Share of the workgroup slots that a grid of n workgroups keeps busy over its waves.
+double wave_fill(int64_t n) { return (double)n / (double)(cdiv(n, kCUs) * kCUs); }
+
 GramPlan gram_plan(int64_t tiles, int64_t K, int halves) {
   const int64_t K1 = std::max<int64_t>(K, 1);
   const int64_t smax = std::max<int64_t>(1, std::min<int64_t>(16 / halves, K1 / (KS * 16)));
   int s = 1;
   while (s * 2 <= smax && tiles * halves * s < 4096) s *= 2;
+  {
+    int best = s;
+    for (int c = s - 1; c >= 1 && 4 * c >= 3 * s; --c)
+      if (wave_fill(tiles * halves * c) > wave_fill(tiles * halves * best) + 1e-9) best = c;
+    s = best;
+  }
   const int64_t step = (int64_t)2 * KS * s;
   GramPlan p;
   p.S = s * halves;
