@@ -169,6 +169,8 @@ def factor(H, percdamp, shared=None, key=None):
             U1, d1 = factor(H[:1], percdamp)
             hit = (U1[0], d1[0])
             shared.store_factor(ck, *hit)
+        if B == 1:  # the cached factor itself: every later use only reads it
+            return hit[0].unsqueeze(0), [hit[1]]
         U = torch.empty_like(H)
         U.copy_(hit[0].unsqueeze(0).expand(B, C, C))
         return U, [hit[1]] * B

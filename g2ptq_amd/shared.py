@@ -98,7 +98,7 @@ class SharedInputHessian:
         dev = W.device
         flags = torch.zeros(1, dtype=torch.int32, device=dev)
         with insts[0]._maybe_onload_hessian():
-            H = insts[0].H[:1].clone()
+            H = insts[0].H[:1]  # a view: the instances drop their H right after
         for inst in insts:
             inst.H = None
         _core.prepare_hessian(H, W)
