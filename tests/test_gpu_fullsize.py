@@ -8,6 +8,10 @@ exact arithmetic fixes, evaluated in fp64:
   compensation is self-consistent — with E = (W − Q)·U⁻¹ (the GPTQ identity
   W − Q = E·U, gptq_utils.py:28-51, 180-230), every pre-quantization value
   x_j = q_j + E_j·U_jj rounds to its code under its group's scale;
+* config 2's q/k/v input (C = 4096, 262,144 tokens): every Hessian entry
+  against fp64 sums; this Gram splits K 15 ways (the count that fills the
+  last wave of workgroups), so the tokens are zero-padded to a multiple of
+  15·128;
 * config 5's factor (C = 28672, GPTAQ's 70B down_proj width): A·UᵀU = I on
   sampled columns (A = H + 0.01·mean(diag H)·I, gptq_utils.py:291-302), with
   a residual no worse than the reference's own fp32 chain
@@ -104,6 +108,28 @@ def test_down_proj_hessian_and_compensation_at_full_size(dev):
     lo = codes[rows] == -8
     hi = codes[rows] == 7
     assert (t[lo] <= 0.5 + 1e-3).all() and (t[hi] >= -0.5 - 1e-3).all()
+
+
+def test_qkv_hessian_at_full_size(dev):
+    from g2ptq_amd import GPTQ, _lib
+    C, N = 4096, 262144
+    tiles = (C // 256) * (C // 256 + 1) // 2
+    splits = _lib.query_size("g2ptq_hessian_gram_workspace", N, C) // (tiles * 256 * 256 * 4)
+    print(f"full-size q/k/v Hessian: C={C} tokens={N}, {splits} K splits", flush=True)
+    assert splits == 15
+    X = _acts(N, C, 81, dev)
+    lin = torch.nn.Linear(C, 256, bias=False, device=dev, dtype=torch.bfloat16)
+    gq = GPTQ([lin])
+    _accumulate(gq, X, 8192)
+    H = gq.H[0].double()
+    Xd = X.double()
+    del X
+    ref = Xd.T @ Xd * (2.0 / 128)  # 128 sequences of 2048 tokens
+    del Xd
+    d = torch.diagonal(ref)
+    err = ((H - ref).abs() / torch.sqrt(d.unsqueeze(1) * d.unsqueeze(0))).max().item()
+    print(f"Hessian: max |H − fp64| / sqrt(H_ii·H_jj) = {err:.3g} over all entries", flush=True)
+    assert err <= 2e-5, err
 
 
 def test_cfg5_factor_at_full_width(dev):
