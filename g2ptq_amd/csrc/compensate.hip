@@ -191,9 +191,8 @@ extern "C" int g2ptq_compensate_workspace(int variant, int64_t B, int64_t R, int
 
 // The lazy-batch loop behind g2ptq_compensate and g2ptq_compensate_noalloc.
 // ws holds the error columns of one super-block (two or three with overlap
-// allowed);
-// every column of it is written by a sweep before a tail reads it, so it
-// needs no clearing.
+// allowed); every column of it is written by a sweep before a tail reads it,
+// so it needs no clearing.
 static int compensate_impl(hipStream_t s, int variant, int64_t B, int64_t R, int64_t C,
                            int64_t bs, float* W, const float* U, const float* P, const float* Z,
                            float* GH, int bits, int sym, int64_t groupsize, int static_groups,
