@@ -129,19 +129,22 @@ def query_size_i64(name, *args):
 
 
 def ptr(t):
-    """Device pointer of a tensor (None → NULL)."""
+    """Device pointer of a tensor as an integer (None → NULL); every entry
+    point declares its pointer arguments ``c_void_p``, which takes either."""
     if t is None:
         return None
-    return ctypes.c_void_p(t.data_ptr())
+    return t.data_ptr()
 
 
 def stream_ptr(device=None):
-    """The current stream of ``device`` (default: the current device)."""
+    """The current stream of ``device`` (default: the current device), as an
+    integer handle.  The raw device query skips ``torch.cuda.current_device``'s
+    lazy-init checks: the callers already hold CUDA tensors."""
     if device is None or device.index is None:
-        index = torch.cuda.current_device()
+        index = torch._C._cuda_getDevice()
     else:
         index = device.index
-    return ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(index))
+    return torch._C._cuda_getCurrentRawStream(index)
 
 
 _WORKSPACES = {}

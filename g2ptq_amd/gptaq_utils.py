@@ -73,9 +73,7 @@ class GPTAQ:
         """gptaq_utils.py:130-148 (``fp_inp[idx]`` is a FIFO of (tokens, C) tensors):
         H and dXXT ← ·n/(n+t) + (2/(n+t))·(XᵀX, (X_fp − X)ᵀX), staged."""
         fp = self.fp_inp[idx][0].to(inp.device, non_blocking=True)
-        if len(inp.shape) == 2:
-            inp = inp.unsqueeze(0)
-        tmp = inp.shape[0]
+        tmp = 1 if inp.dim() == 2 else inp.shape[0]  # a 2-D input is one sequence
         X = _core.as_bf16_tokens(inp)
         Xfp = _core.as_bf16_tokens(fp.to(inp.dtype))
         if Xfp.shape != X.shape:

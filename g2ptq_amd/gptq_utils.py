@@ -67,9 +67,7 @@ class GPTQ:
 
     def add_batch(self, idx, inp, out):
         """gptq_utils.py:115-126: H ← H·n/(n+t) + (2/(n+t))·XᵀX, t = #sequences."""
-        if len(inp.shape) == 2:
-            inp = inp.unsqueeze(0)
-        tmp = inp.shape[0]
+        tmp = 1 if inp.dim() == 2 else inp.shape[0]  # a 2-D input is one sequence
         X = _core.as_bf16_tokens(inp)
         T = X.shape[0]
         st = self._stagers[idx]
