@@ -15,6 +15,11 @@
 namespace g2ptq {
 namespace {
 
+template <bool B>
+struct ExactTag {
+  static constexpr bool value = B;
+};
+
 // NaN-propagating clamp (torch.clamp semantics).
 __device__ __forceinline__ float clamp_nan(float v, float lo, float hi) {
   return v < lo ? lo : (v > hi ? hi : v);
@@ -29,12 +34,21 @@ __device__ __forceinline__ float clamp_nan(float v, float lo, float hi) {
 // infinite or NaN operands) takes the IEEE division, on a wave-uniform branch
 // that real data never enters.  Three dependent operations instead of the
 // eleven of the IEEE division sequence on the sweep's per-column chain.
+__device__ __forceinline__ bool recip_div_exact(float a, float q) {
+  const float aa = fabsf(a), aq = fabsf(q);
+  return aa >= 0x1p-100f && aa <= 0x1p100f && aq >= 0x1p-100f && aq <= 0x1p100f;
+}
+// Markstein's sequence alone: the IEEE quotient when recip_div_exact(a, RN(a·y)).
+__device__ __forceinline__ float div_markstein(float a, float b, float y) {
+  const float q = __fmul_rn(a, y);
+  const float r = __fmaf_rn(-b, q, a);
+  return __fmaf_rn(r, y, q);
+}
 __device__ __forceinline__ float div_rn_recip(float a, float b, float y) {
   const float q = __fmul_rn(a, y);
   const float r = __fmaf_rn(-b, q, a);
   float res = __fmaf_rn(r, y, q);
-  const float aa = fabsf(a), aq = fabsf(q);
-  const bool slow = !(aa >= 0x1p-100f && aa <= 0x1p100f && aq >= 0x1p-100f && aq <= 0x1p100f);
+  const bool slow = !recip_div_exact(a, q);
   if (__builtin_amdgcn_ballot_w64(slow) != 0) {
     asm volatile("" ::: "memory");  // keeps the branch: the division is not speculated
     res = slow ? __fdiv_rn(a, b) : res;
@@ -744,83 +758,135 @@ __global__ __launch_bounds__(256) void sweep4_kernel(SweepArgs a) {
     // The panel's pivots and their reciprocals are read up front, and each
     // column's U row one column ahead, so the per-column dependency chain
     // (quantise, error, broadcast, update) never waits for LDS.
-    float qb[NS], ib[NS], eb[NS], gb[NS], ysv[NS], dcol[PW], ycol[PW];
+    float qb[NS], ib[NS], eb[NS], gb[NS], ysv[NS];
 #pragma unroll
     for (int s = 0; s < NS; ++s) ysv[s] = __fdiv_rn(1.f, sv[s]);
-#pragma unroll
-    for (int q4 = 0; q4 < PW / 4; ++q4) {
-      const float4 dv = *reinterpret_cast<const float4*>(&dg[p0 + 4 * q4]);
-      const float4 yv = *reinterpret_cast<const float4*>(&rdiag[p0 + 4 * q4]);
-      dcol[4 * q4] = dv.x; dcol[4 * q4 + 1] = dv.y; dcol[4 * q4 + 2] = dv.z; dcol[4 * q4 + 3] = dv.w;
-      ycol[4 * q4] = yv.x; ycol[4 * q4 + 1] = yv.y; ycol[4 * q4 + 2] = yv.z; ycol[4 * q4 + 3] = yv.w;
-    }
-    float uc[NS], pc[NS];
+    // The divisions of the column chain run as Markstein's sequence with no
+    // per-column range test (a test and branch per division cost the chain
+    // its scheduling).  After the panel each lane re-derives, for the columns
+    // it owns, both divisions' operands and first quotients from the values
+    // it kept (x, deq, gh) and tests their range; if any lane of the wave
+    // fails, the panel runs again from its saved inputs with div_rn_recip,
+    // which takes the IEEE division where needed.  The results therefore
+    // equal a sweep with div_rn_recip on every column.
+    float w0[NS], g0[NS], xo[NS];
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-      uc[s] = Us[tri_base(p0, n) + p0 + sub + L * s];
-      if (V == 1) pc[s] = Ps[tri_base(p0, n) + p0 + sub + L * s];
+      w0[s] = w[s];
+      if (V == 2) g0[s] = gh[s];
     }
+    auto sweep_panel = [&](auto exact_tag, int sub, int rr, int p0) __attribute__((always_inline)) {
+      constexpr bool EXACT = decltype(exact_tag)::value;
+      float dcol[PW], ycol[PW];
 #pragma unroll
-    for (int jj = 0; jj < PW; ++jj) {
-      const int sl = jj / L, o = jj % L;
-      const bool own = sub == o;
-      const int j = p0 + jj;
-      float un[NS], pn[NS];
-      if (jj + 1 < PW) {
-#pragma unroll
-        for (int s = 0; s < NS; ++s) {
-          un[s] = Us[tri_base(j + 1, n) + p0 + sub + L * s];
-          if (V == 1) pn[s] = Ps[tri_base(j + 1, n) + p0 + sub + L * s];
-        }
+      for (int q4 = 0; q4 < PW / 4; ++q4) {
+        const float4 dv = *reinterpret_cast<const float4*>(&dg[p0 + 4 * q4]);
+        const float4 yv = *reinterpret_cast<const float4*>(&rdiag[p0 + 4 * q4]);
+        dcol[4 * q4] = dv.x; dcol[4 * q4 + 1] = dv.y; dcol[4 * q4 + 2] = dv.z; dcol[4 * q4 + 3] = dv.w;
+        ycol[4 * q4] = yv.x; ycol[4 * q4 + 1] = yv.y; ycol[4 * q4 + 2] = yv.z; ycol[4 * q4 + 3] = yv.w;
       }
-      const float x = w[sl];  // meaningful on the owner lane
-      const float sc = sv[sl];
-      const float z0 = zv[sl];
-      const float q = clamp_nan(__fadd_rn(rintf(div_rn_recip(x, sc, ysv[sl])), z0), minq, fmaxq);
-      const float deq = __fmul_rn(sc, __fsub_rn(q, z0));
-      const float d = dcol[jj];
-      const float yd = ycol[jj];
-      float err0;
-      if (V == 2) err0 = div_rn_recip(__fsub_rn(__fsub_rn(x, deq), gh[sl]), d, yd);
-      else err0 = div_rn_recip(__fsub_rn(x, deq), d, yd);
-      const float err = group_bcast<L>(err0, o);
-      const float xb = (V == 1 || jj == PW - 1) ? group_bcast<L>(x, o) : 0.f;
-      const float zj = (V == 2) ? group_bcast<L>(zg[sl], o) : 0.f;
-      bad |= own && !(sc > 0.f);
-      qb[sl] = own ? deq : qb[sl];
-      ib[sl] = own ? q : ib[sl];
-      eb[sl] = own ? err0 : eb[sl];
-      if (V == 2) gb[sl] = own ? gh[sl] : gb[sl];
-      if (sub == 0) {
-        e_s[j * RW + rr] = err;
-        if (V == 1) t_s[j * RW + rr] = xb;
-        if (V == 2) z_s[j * RW + rr] = zj;
-      }
-      if (jj == PW - 1) last_x = xb;
+      float uc[NS], pc[NS];
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
-        if (L * s + L - 1 <= jj) continue;       // every column of the slot is done
-        const bool upd = L * s > jj || sub > jj - L * s;
-        const float u = uc[s];
-        if (V == 0) {
-          const float nw = __fsub_rn(w[s], __fmul_rn(u, err));
-          w[s] = upd ? nw : w[s];
-        } else if (V == 1) {
-          const float nw = __fadd_rn(__fsub_rn(w[s], __fmul_rn(u, err)), __fmul_rn(pc[s], xb));
-          w[s] = upd ? nw : w[s];
-        } else {
-          const float nw = __fsub_rn(__fsub_rn(w[s], gh[s]), __fmul_rn(u, err));
-          const float ng = __fsub_rn(gh[s], __fmul_rn(u, zj));
-          w[s] = upd ? nw : w[s];
-          gh[s] = upd ? ng : gh[s];
-        }
+        uc[s] = Us[tri_base(p0, n) + p0 + sub + L * s];
+        if (V == 1) pc[s] = Ps[tri_base(p0, n) + p0 + sub + L * s];
       }
-      if (jj + 1 < PW) {
+#pragma unroll
+      for (int jj = 0; jj < PW; ++jj) {
+        const int sl = jj / L, o = jj % L;
+        const bool own = sub == o;
+        const int j = p0 + jj;
+        float un[NS], pn[NS];
+        if (jj + 1 < PW) {
+#pragma unroll
+          for (int s = 0; s < NS; ++s) {
+            un[s] = Us[tri_base(j + 1, n) + p0 + sub + L * s];
+            if (V == 1) pn[s] = Ps[tri_base(j + 1, n) + p0 + sub + L * s];
+          }
+        }
+        const float x = w[sl];  // meaningful on the owner lane
+        const float sc = sv[sl];
+        const float z0 = zv[sl];
+        const float t = EXACT ? div_rn_recip(x, sc, ysv[sl]) : div_markstein(x, sc, ysv[sl]);
+        const float q = clamp_nan(__fadd_rn(rintf(t), z0), minq, fmaxq);
+        const float deq = __fmul_rn(sc, __fsub_rn(q, z0));
+        const float d = dcol[jj];
+        const float yd = ycol[jj];
+        const float a2 = (V == 2) ? __fsub_rn(__fsub_rn(x, deq), gh[sl]) : __fsub_rn(x, deq);
+        const float err0 = EXACT ? div_rn_recip(a2, d, yd) : div_markstein(a2, d, yd);
+        const float err = group_bcast<L>(err0, o);
+        const float xb = (V == 1 || jj == PW - 1) ? group_bcast<L>(x, o) : 0.f;
+        const float zj = (V == 2) ? group_bcast<L>(zg[sl], o) : 0.f;
+        bad |= own && !(sc > 0.f);
+        qb[sl] = own ? deq : qb[sl];
+        ib[sl] = own ? q : ib[sl];
+        eb[sl] = own ? err0 : eb[sl];
+        if (!EXACT) xo[sl] = own ? x : xo[sl];
+        if (V == 2) gb[sl] = own ? gh[sl] : gb[sl];
+        if (sub == 0) {
+          e_s[j * RW + rr] = err;
+          if (V == 1) t_s[j * RW + rr] = xb;
+          if (V == 2) z_s[j * RW + rr] = zj;
+        }
+        if (jj == PW - 1) last_x = xb;
+        // With 16 lanes every column of a slot that is not wholly done takes
+        // the update, the done ones too (the owner's and earlier columns):
+        // nothing reads their values again, and no lane mask is needed.  (A
+        // quad per row measured faster with the mask.)
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
-          uc[s] = un[s];
-          if (V == 1) pc[s] = pn[s];
+          if (L * s + L - 1 <= jj) continue;       // every column of the slot is done
+          const bool upd = L == 16 || L * s > jj || sub > jj - L * s;
+          const float u = uc[s];
+          if (V == 0) {
+            const float nw = __fsub_rn(w[s], __fmul_rn(u, err));
+            w[s] = upd ? nw : w[s];
+          } else if (V == 1) {
+            const float nw = __fadd_rn(__fsub_rn(w[s], __fmul_rn(u, err)), __fmul_rn(pc[s], xb));
+            w[s] = upd ? nw : w[s];
+          } else {
+            const float nw = __fsub_rn(__fsub_rn(w[s], gh[s]), __fmul_rn(u, err));
+            const float ng = __fsub_rn(gh[s], __fmul_rn(u, zj));
+            w[s] = upd ? nw : w[s];
+            gh[s] = upd ? ng : gh[s];
+          }
         }
+        if (jj + 1 < PW) {
+#pragma unroll
+          for (int s = 0; s < NS; ++s) {
+            uc[s] = un[s];
+            if (V == 1) pc[s] = pn[s];
+          }
+        }
+      }
+    };
+    // (16 lanes per row only: with a quad per row the saved state of the
+    // re-run does not fit two waves per SIMD.)
+    if constexpr (L != 16) {
+      sweep_panel(ExactTag<true>{}, sub, rr, p0);
+    } else {
+      sweep_panel(ExactTag<false>{}, sub, rr, p0);
+      bool inexact = false;
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        const int c = p0 + L * s + sub;
+        const float a1 = xo[s];
+        const float a2 = (V == 2) ? __fsub_rn(__fsub_rn(a1, qb[s]), gb[s]) : __fsub_rn(a1, qb[s]);
+        inexact |= !recip_div_exact(a1, __fmul_rn(a1, ysv[s])) ||
+                   !recip_div_exact(a2, __fmul_rn(a2, rdiag[c]));
+      }
+      if (__builtin_amdgcn_ballot_w64(inexact) != 0) {
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+          w[s] = w0[s];
+          if (V == 2) gh[s] = g0[s];
+        }
+        // The re-run recomputes its LDS addresses from opaque copies of their
+        // bases and reloads U: keeping the first pass's addresses and loads
+        // live for it would cost a wave's worth of registers.
+        int sub2 = sub, rr2 = rr, p02 = p0;
+        asm volatile("" : "+v"(sub2), "+v"(rr2), "+s"(p02)::"memory");
+        sweep_panel(ExactTag<true>{}, sub2, rr2, p02);
       }
     }
     // ---- panel outputs ------------------------------------------------------

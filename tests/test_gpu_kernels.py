@@ -290,6 +290,61 @@ def test_g2ptq_block_bitexact(dev, case):
     assert_bitexact(dgh, egh, "ghinv")
 
 
+def _special_rows(w, s, z):
+    """Rows whose divisions leave the reciprocal sequence's exact range (the
+    sweep's exact re-run): all +0, all −0, tiny, subnormal, huge, and values
+    on the quantization grid (x − deq = 0 in every column)."""
+    w = w.clone()
+    w[:, :, 0] = 0.0
+    w[:, :, 1] = -0.0
+    w[:, :, 9] *= 1e-36
+    w[:, :, 40] *= 1e-40
+    w[:, :, 20] *= 1e31
+    w[:, :, 14] = torch.round(w[:, :, 14] / s[:, :, 14]) * s[:, :, 14]
+    return w
+
+
+def _assert_same_bits(a, e, what):
+    a, e = a.detach().cpu().contiguous(), e.detach().cpu().contiguous()
+    same = (a.view(torch.int32) == e.view(torch.int32)) | (torch.isnan(a) & torch.isnan(e))
+    assert bool(same.all()), f"{what}: {int((~same).sum())} entries differ in their bits"
+
+
+@pytest.mark.parametrize("variant", ["gptq", "gptaq", "g2ptq"])
+def test_block_sweep_exact_rerun_bitexact(dev, variant):
+    """16 lanes per row, 128-column block: the waves holding the special rows
+    re-run their panels with the exact division, the others keep the fast
+    pass; every output equals the oracle's bit for bit (signed zeros too)."""
+    batch, columns, rows, maxq = 2, 128, 300, 7
+    w, h, s, z = ref_inputs(batch, columns, rows, maxq, True, 411)
+    w = _special_rows(w, s, z)
+    hd, sd, zd = h.to(dev), s.to(dev), z.to(dev)
+    ew, ei, ee = w.clone(), torch.empty_like(w), torch.empty_like(w)
+    dw, di, de = w.to(dev), torch.empty_like(w, device=dev), torch.empty_like(w, device=dev)
+    extra = []
+    if variant == "gptq":
+        from g2ptq_amd.gptq_utils import run_eager
+        ocomp.gptq_block(ew, h, s, z, ei, ee, maxq)
+        run_eager(dw, hd, sd, zd, maxq, "hip", di, de)
+    elif variant == "gptaq":
+        from g2ptq_amd.gptaq_utils import run_eager
+        p = gptaq_p(w, 3411)
+        ecw, dcw = torch.empty(batch, rows), torch.empty(batch, rows, device=dev)
+        ocomp.gptaq_block(ew, h, p, s, z, ecw, ei, ee, maxq)
+        run_eager(dw, hd, p.to(dev), sd, zd, maxq, "hip", dcw, di, de)
+        extra.append((dcw, ecw, "column_weight"))
+    else:
+        from g2ptq_amd.g2ptq_utils import run_eager
+        zz, gh = g2_inputs(w, s, 1411)
+        egh, dgh = gh.clone(), gh.to(dev)
+        ocomp.g2ptq_block(ew, h, s, z, zz, egh, ei, ee, maxq)
+        run_eager(dw, hd, sd, zd, zz.to(dev), dgh, maxq, "hip", di, de)
+        extra.append((dgh, egh, "ghinv"))
+    torch.cuda.synchronize()
+    for a, e, what in [(di, ei, "codes"), (dw, ew, "weight"), (de, ee, "error")] + extra:
+        _assert_same_bits(a, e, what)
+
+
 @pytest.mark.parametrize("T,C,calls", [(300, 200, 3), (1000, 129, 1), (64, 384, 2), (2048, 512, 4),
                                         (4096, 1024, 2), (8192, 600, 1), (1536, 2304, 1)])
 def test_hessian_update_matches_oracle(dev, T, C, calls):
