@@ -693,7 +693,7 @@ __global__ __launch_bounds__(256) void sweep4_kernel(SweepArgs a) {
         a.FZ[b * a.sb + r * a.sr + gidx * a.sg] = fz;
       }
     }
-    // ---- panel inputs of the lane's NS columns, all issued before any store -
+    // ---- panel inputs of the lane's NS columns -------------------------------
     float w[NS], gh[NS], sv[NS], zv[NS], zg[NS];
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
@@ -708,52 +708,61 @@ __global__ __launch_bounds__(256) void sweep4_kernel(SweepArgs a) {
         sv[s] = Sp[(int64_t)gidx * a.sg];
         zv[s] = Zp[(int64_t)gidx * a.sg];
       }
-      w[s] = Win[(int64_t)j * a.wc];
-      if (V == 2) {
-        zg[s] = Zg[(int64_t)j * a.zc];
-        gh[s] = GH[(int64_t)j * a.gc];
-      }
+      if (V == 2) zg[s] = Zg[(int64_t)j * a.zc];
     }
-    // ---- replay updates of the columns swept in earlier panels (LDS only) ---
-    // Eight columns at a time: their LDS operands are all read before the
-    // updates, which then run in the reference's column order.
-    // Sixteen columns at a time where the registers allow (16 lanes per row,
-    // no P), so fewer LDS round trips stay exposed; row j + 1 of the packed
-    // triangle starts n − j − 1 entries after row j.
-    constexpr int RB = (L == 16 && V != 1) ? 16 : 8;
-    for (int j0 = 0; j0 < p0; j0 += RB) {
-      float e[RB], t[RB], zj[RB], u[RB][NS], pu[RB][NS];
-      const int row0 = tri_base(j0, n) + p0 + sub, step = n - j0 - 1;
+    // The panel's weights (and GH) as the earlier panels leave them: loaded
+    // from the block's input (nothing in this kernel writes it) and updated
+    // with the earlier panels' errors from LDS.  Called again, from opaque
+    // copies of its index bases, when the panel is swept a second time.
+    auto load_panel = [&](int sub, int rr, int p0) __attribute__((always_inline)) {
 #pragma unroll
-      for (int q = 0; q < RB; ++q) {
-        const int j = j0 + q;
-        e[q] = e_s[j * RW + rr];
-        if (V == 1) t[q] = t_s[j * RW + rr];
-        if (V == 2) zj[q] = z_s[j * RW + rr];
-        const int off = row0 + q * step - q * (q - 1) / 2;  // tri_base(j, n) + p0 + sub
-        const float* Uj = Us + off;
-        const float* Pj = (V == 1) ? Ps + off : nullptr;
-#pragma unroll
-        for (int s = 0; s < NS; ++s) {
-          u[q][s] = Uj[L * s];
-          if (V == 1) pu[q][s] = Pj[L * s];
-        }
+      for (int s = 0; s < NS; ++s) {
+        const int j = p0 + L * s + sub;
+        w[s] = Win[(int64_t)j * a.wc];
+        if (V == 2) gh[s] = GH[(int64_t)j * a.gc];
       }
+      // Replay of the columns swept in earlier panels (LDS only), eight
+      // columns at a time: their LDS operands are all read before the
+      // updates, which then run in the reference's column order.  Sixteen
+      // at a time where the registers allow (16 lanes per row, no P), so
+      // fewer LDS round trips stay exposed; row j + 1 of the packed triangle
+      // starts n − j − 1 entries after row j.
+      constexpr int RB = (L == 16 && V != 1) ? 16 : 8;
+      for (int j0 = 0; j0 < p0; j0 += RB) {
+        float e[RB], t[RB], zj[RB], u[RB][NS], pu[RB][NS];
+        const int row0 = tri_base(j0, n) + p0 + sub, step = n - j0 - 1;
 #pragma unroll
-      for (int q = 0; q < RB; ++q) {
+        for (int q = 0; q < RB; ++q) {
+          const int j = j0 + q;
+          e[q] = e_s[j * RW + rr];
+          if (V == 1) t[q] = t_s[j * RW + rr];
+          if (V == 2) zj[q] = z_s[j * RW + rr];
+          const int off = row0 + q * step - q * (q - 1) / 2;  // tri_base(j, n) + p0 + sub
+          const float* Uj = Us + off;
+          const float* Pj = (V == 1) ? Ps + off : nullptr;
 #pragma unroll
-        for (int s = 0; s < NS; ++s) {
-          if (V == 0) {
-            w[s] = __fsub_rn(w[s], __fmul_rn(u[q][s], e[q]));
-          } else if (V == 1) {
-            w[s] = __fadd_rn(__fsub_rn(w[s], __fmul_rn(u[q][s], e[q])), __fmul_rn(pu[q][s], t[q]));
-          } else {
-            w[s] = __fsub_rn(__fsub_rn(w[s], gh[s]), __fmul_rn(u[q][s], e[q]));
-            gh[s] = __fsub_rn(gh[s], __fmul_rn(u[q][s], zj[q]));
+          for (int s = 0; s < NS; ++s) {
+            u[q][s] = Uj[L * s];
+            if (V == 1) pu[q][s] = Pj[L * s];
+          }
+        }
+#pragma unroll
+        for (int q = 0; q < RB; ++q) {
+#pragma unroll
+          for (int s = 0; s < NS; ++s) {
+            if (V == 0) {
+              w[s] = __fsub_rn(w[s], __fmul_rn(u[q][s], e[q]));
+            } else if (V == 1) {
+              w[s] = __fadd_rn(__fsub_rn(w[s], __fmul_rn(u[q][s], e[q])), __fmul_rn(pu[q][s], t[q]));
+            } else {
+              w[s] = __fsub_rn(__fsub_rn(w[s], gh[s]), __fmul_rn(u[q][s], e[q]));
+              gh[s] = __fsub_rn(gh[s], __fmul_rn(u[q][s], zj[q]));
+            }
           }
         }
       }
-    }
+    };
+    load_panel(sub, rr, p0);
     // ---- sweep the panel column by column -----------------------------------
     // The panel's pivots and their reciprocals are read up front, and each
     // column's U row one column ahead, so the per-column dependency chain
@@ -766,15 +775,10 @@ __global__ __launch_bounds__(256) void sweep4_kernel(SweepArgs a) {
     // its scheduling).  After the panel each lane re-derives, for the columns
     // it owns, both divisions' operands and first quotients from the values
     // it kept (x, deq, gh) and tests their range; if any lane of the wave
-    // fails, the panel runs again from its saved inputs with div_rn_recip,
-    // which takes the IEEE division where needed.  The results therefore
-    // equal a sweep with div_rn_recip on every column.
-    float w0[NS], g0[NS], xo[NS];
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
-      w0[s] = w[s];
-      if (V == 2) g0[s] = gh[s];
-    }
+    // fails, the wave reloads the panel and sweeps it again with
+    // div_rn_recip, which takes the IEEE division where needed.  The results
+    // therefore equal a sweep with div_rn_recip on every column.
+    float xo[NS];
     auto sweep_panel = [&](auto exact_tag, int sub, int rr, int p0) __attribute__((always_inline)) {
       constexpr bool EXACT = decltype(exact_tag)::value;
       float dcol[PW], ycol[PW];
@@ -860,8 +864,8 @@ __global__ __launch_bounds__(256) void sweep4_kernel(SweepArgs a) {
         }
       }
     };
-    // (16 lanes per row only: with a quad per row the saved state of the
-    // re-run does not fit two waves per SIMD.)
+    // (16 lanes per row only: with a quad per row the owned values kept for
+    // the test cost the second wave per SIMD.)
     if constexpr (L != 16) {
       sweep_panel(ExactTag<true>{}, sub, rr, p0);
     } else {
@@ -876,16 +880,13 @@ __global__ __launch_bounds__(256) void sweep4_kernel(SweepArgs a) {
                    !recip_div_exact(a2, __fmul_rn(a2, rdiag[c]));
       }
       if (__builtin_amdgcn_ballot_w64(inexact) != 0) {
-#pragma unroll
-        for (int s = 0; s < NS; ++s) {
-          w[s] = w0[s];
-          if (V == 2) gh[s] = g0[s];
-        }
-        // The re-run recomputes its LDS addresses from opaque copies of their
-        // bases and reloads U: keeping the first pass's addresses and loads
-        // live for it would cost a wave's worth of registers.
+        // The second sweep recomputes its addresses from opaque copies of
+        // their bases and reloads its operands: keeping the first pass's
+        // addresses and loads live for it would cost a wave's worth of
+        // registers.
         int sub2 = sub, rr2 = rr, p02 = p0;
         asm volatile("" : "+v"(sub2), "+v"(rr2), "+s"(p02)::"memory");
+        load_panel(sub2, rr2, p02);
         sweep_panel(ExactTag<true>{}, sub2, rr2, p02);
       }
     }
