@@ -71,7 +71,7 @@ def write_back(layers, Q, flags):
 
 def as_bf16_tokens(inp):
     """Flatten a hook payload to (T, C) bf16 contiguous."""
-    x = inp.reshape(-1, inp.shape[-1])
+    x = inp if inp.dim() == 2 else inp.reshape(-1, inp.shape[-1])
     if x.dtype != torch.bfloat16:
         raise NotImplementedError(
             f"Hessian accumulation takes bf16 activations (got {x.dtype}); the path's "
