@@ -345,6 +345,47 @@ def test_block_sweep_exact_rerun_bitexact(dev, variant):
         _assert_same_bits(a, e, what)
 
 
+def test_superblock_sweep_exact_rerun_matches_fast_pass(dev):
+    """GPTQ's super-block launch (C = 1024: two super-blocks of four blocks,
+    16 lanes per row): rows of ±0, tiny, subnormal and huge values make their
+    waves sweep panels a second time with the exact division.  Rows are
+    independent, so every ordinary row, including the ones sharing a wave
+    with a special row, equals the same row of a run without special rows
+    bit for bit; the zero and tiny rows quantize to code 0."""
+    from g2ptq_amd import _lib
+    B, R, C, bs, bits = 1, 64, 1024, 128, 4
+    g = gen(7311)
+    W0 = torch.randn(B, R, C, generator=g) * 0.05
+    U = torch.triu(torch.randn(B, C, C, generator=g) * (0.5 / C ** 0.5), diagonal=1)
+    U.diagonal(dim1=1, dim2=2).copy_(torch.rand(B, C, generator=g) * 0.5 + 0.75)
+    special = {0: 0.0, 1: -0.0, 9: 1e-36, 40: 1e-40, 20: 1e31}
+    W1 = W0.clone()
+    for r, v in special.items():
+        W1[:, r] = torch.full_like(W0[:, r], v) if v == 0 else W0[:, r] * v
+    Ud = U.to(dev)
+    ws_bytes = _lib.query_size("g2ptq_compensate_workspace", 0, B, R, C, bs)
+    outs = []
+    for Win in (W0, W1):
+        W = Win.clone().to(dev)
+        stab = torch.full((1, B * R), 0.05 / 7, device=dev)
+        ztab = torch.zeros(1, B * R, device=dev)
+        Q, Wi, Sc = (torch.empty_like(W) for _ in range(3))
+        flags = torch.zeros(1, dtype=torch.int32, device=dev)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        _lib.call("g2ptq_compensate", _lib.stream_ptr(dev), 0, B, R, C, bs, _lib.ptr(W),
+                  _lib.ptr(Ud), None, None, None, bits, 1, -1, 0, 0, 2.4, 0.5, None, 0, None,
+                  _lib.ptr(stab), _lib.ptr(ztab), _lib.ptr(Q), _lib.ptr(Wi), _lib.ptr(Sc),
+                  _lib.ptr(flags), _lib.ptr(ws), ws_bytes)
+        torch.cuda.synchronize()
+        assert int(flags.item()) == 0
+        outs.append([t.cpu() for t in (Q, Wi, W)])
+    ordinary = [r for r in range(R) if r not in special]
+    for a, b, name in zip(outs[0], outs[1], ("Q", "W_int", "W")):
+        _assert_same_bits(a[:, ordinary], b[:, ordinary], name)
+    for r in (0, 1, 9, 40):
+        assert torch.all(outs[1][1][:, r] == 0) and torch.all(outs[1][0][:, r] == 0), r
+
+
 @pytest.mark.parametrize("T,C,calls", [(300, 200, 3), (1000, 129, 1), (64, 384, 2), (2048, 512, 4),
                                         (4096, 1024, 2), (8192, 600, 1), (1536, 2304, 1)])
 def test_hessian_update_matches_oracle(dev, T, C, calls):
