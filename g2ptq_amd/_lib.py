@@ -108,12 +108,37 @@ def call(name, *args):
     lib = load()
     status = getattr(lib, name)(*args)
     if status != 0:
-        detail = lib.g2ptq_last_error().decode(errors="replace")
-        kind = lib.g2ptq_status_string(status).decode()
-        if status == -1:
-            raise ValueError(f"{name}: {kind}: {detail}")
-        raise RuntimeError(f"{name}: {kind}: {detail}")
+        raise_status(name, status)
     return status
+
+
+def raise_status(name, status):
+    """The exception for a nonzero status of entry point ``name``."""
+    lib = load()
+    detail = lib.g2ptq_last_error().decode(errors="replace")
+    kind = lib.g2ptq_status_string(status).decode()
+    if status == -1:
+        raise ValueError(f"{name}: {kind}: {detail}")
+    raise RuntimeError(f"{name}: {kind}: {detail}")
+
+
+_FAST = None
+
+
+def fastcall():
+    """The CPython fast-call module of the per-batch staging entry points
+    (``g2ptq_amd/_fastcall``, built with the library), or None when it is
+    not built; it calls the same entry points as ``call``, without ctypes'
+    per-argument conversions."""
+    global _FAST
+    if _FAST is None:
+        load()  # the module links against the library loaded here
+        try:
+            from . import _fastcall
+            _FAST = _fastcall
+        except ImportError:
+            _FAST = False
+    return _FAST or None
 
 
 def query_size(name, *args):

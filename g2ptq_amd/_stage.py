@@ -137,7 +137,13 @@ class GramStager:
         T, C = X.shape
         st, xt = _lib.stream_ptr(), _lib.ptr(self.buf)
         if self.kind == KIND_GPTQ:
-            _lib.call("g2ptq_hessian_stage", st, _lib.ptr(X), T, C, C, xt, self.cap, self.k)
+            fast = _lib.fastcall()
+            if fast is None:
+                _lib.call("g2ptq_hessian_stage", st, _lib.ptr(X), T, C, C, xt, self.cap, self.k)
+            else:
+                status = fast.hessian_stage(st, X.data_ptr(), T, C, C, xt, self.cap, self.k)
+                if status:
+                    _lib.raise_status("g2ptq_hessian_stage", status)
         elif self.kind == KIND_GPTAQ:
             _lib.call("g2ptq_gptaq_stage", st, _lib.ptr(X), _lib.ptr(Xfp), T, C, C, C, xt,
                       self.cap, self.k)

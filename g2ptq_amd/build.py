@@ -2,12 +2,14 @@
 
 ``python -m g2ptq_amd.build`` compiles every ``csrc/*.hip`` translation unit
 for gfx950 and links them into ``g2ptq_amd/libg2ptq_hip.so`` in-tree, so the
-library travels with the source tree.
+library travels with the source tree, then builds ``csrc/fastcall.c`` (gcc)
+into the CPython module ``g2ptq_amd/_fastcall`` beside it.
 """
 import concurrent.futures
 import os
 import subprocess
 import sys
+import sysconfig
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
@@ -60,7 +62,23 @@ def build(verbose=False):
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
     os.replace(tmp, LIB)
+    build_fastcall()
     return LIB
+
+
+def build_fastcall():
+    """The CPython fast-call module (csrc/fastcall.c) beside the library: gcc,
+    linked against libg2ptq_hip.so and resolving it next to itself."""
+    ext = os.path.join(HERE, "_fastcall" + sysconfig.get_config_var("EXT_SUFFIX"))
+    tmp = ext + ".tmp"
+    cmd = ["gcc", "-O2", "-std=c11", "-shared", "-fPIC", "-Wall",
+           "-I", sysconfig.get_paths()["include"], os.path.join(CSRC, "fastcall.c"),
+           "-L", HERE, "-lg2ptq_hip", "-Wl,-rpath,$ORIGIN", "-o", tmp]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"gcc failed for fastcall.c:\n{res.stderr}")
+    os.replace(tmp, ext)
+    return ext
 
 
 if __name__ == "__main__":

@@ -90,3 +90,20 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "_LIB", None)
     with pytest.raises(_lib.HipLibraryError):
         _lib.load()
+
+
+def test_fastcall_module_binds_the_same_entry_point(lib):
+    """The CPython fast-call module is built with the library, shares its one
+    loaded copy (one status and error state), and reports argument errors as
+    the ctypes binding does."""
+    fast = _lib.fastcall()
+    assert fast is not None, "g2ptq_amd/_fastcall is not built"
+    maps = [l for l in open("/proc/self/maps") if "libg2ptq_hip.so" in l and "r-xp" in l]
+    assert len(maps) == 1
+    with pytest.raises(TypeError):
+        fast.hessian_stage(0, 0, 1)
+    status = fast.hessian_stage(None, None, 4, 8, 8, None, 8, 0)  # no XT: argument error
+    assert status == -1
+    assert b"hessian_stage" in lib.g2ptq_last_error()
+    with pytest.raises(ValueError, match="hessian_stage: bad arguments"):
+        _lib.raise_status("g2ptq_hessian_stage", status)
