@@ -73,12 +73,14 @@ class GPTQ:
         st = self._stagers[idx]
         if st is None:
             st = self._stagers[idx] = GramStager(self.columns, X.device)
-        if not st.fits(T):
+        fits = st.fits(T)
+        if not fits:
             self._flush_staged(idx)
             if st.can_stage(T):
                 st.reserve(T)
+            fits = st.fits(T)
         n = self._n[idx] + tmp
-        if st.fits(T):
+        if fits:
             st.stage(X)
         else:
             # a batch larger than the staging budget: update H directly
