@@ -152,7 +152,7 @@ def permute_sym(H, perm):
     return out
 
 
-def factor(H, percdamp, shared=None, key=None):
+def factor(H, percdamp, shared=None, key=None, alias=None):
     """U[b] = chol((H[b] + p·mean(diag)·I)⁻¹, upper) with the reference's retry loop.
 
     gptq_utils.py:291-311: on a failed factorization (non-PD pivot or NaN) the
@@ -160,8 +160,19 @@ def factor(H, percdamp, shared=None, key=None):
     (0, 1) raises ``ValueError``.  Layers that succeed keep their damp.
     ``shared`` (a SharedInputHessian whose members are all of H's slots, so all
     slots hold the same matrix) factors one slot once and reuses the result.
+    ``alias`` ({slot: earlier slot holding the same matrix}) factors only the
+    other slots and gives each aliased slot its source's U and damp: the
+    factor of a slot depends on that slot alone, so the result is the same.
     """
     B, C, _ = H.shape
+    if shared is None and alias:
+        src = [b for b in range(B) if b not in alias]
+        pos = {b: i for i, b in enumerate(src)}
+        if len(src) < B and all(alias[b] in pos for b in alias):
+            dev = H.device
+            Uu, du = factor(H.index_select(0, torch.tensor(src, device=dev)), percdamp)
+            at = [pos[alias.get(b, b)] for b in range(B)]
+            return Uu.index_select(0, torch.tensor(at, device=dev)), [du[i] for i in at]
     if shared is not None:
         ck = (percdamp, key)
         hit = shared.cached_factor(ck)

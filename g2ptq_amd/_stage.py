@@ -238,8 +238,9 @@ def staged_attr(name):
             self._flush_staged()
         elif value is not None and getattr(self, private, None) is not None:
             # a replaced Hessian is no longer the one a shared-input group's
-            # cached factor was computed from
+            # cached factor (or its slot copies) came from
             self.__dict__.pop("_shared_factor", None)
+            self.__dict__.pop("_h_alias", None)
         setattr(self, private, value)
         if value is None:
             for st in getattr(self, "_stagers", None) or ():

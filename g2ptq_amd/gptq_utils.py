@@ -67,6 +67,8 @@ class GPTQ:
 
     def add_batch(self, idx, inp, out):
         """gptq_utils.py:115-126: H ← H·n/(n+t) + (2/(n+t))·XᵀX, t = #sequences."""
+        if self.__dict__.get("_h_alias"):
+            self._h_alias = None  # slot copies made by a shared finalize are stale now
         tmp = 1 if inp.dim() == 2 else inp.shape[0]  # a 2-D input is one sequence
         X = _core.as_bf16_tokens(inp)
         T = X.shape[0]
@@ -149,7 +151,7 @@ class GPTQ:
                 if H_diag is not None:
                     H_diag = _core.permute_cols(H_diag, perm)
             Hinv, _ = _core.factor(H, percdamp, getattr(self, "_shared_factor", None),
-                                   key=bool(actorder))
+                                   key=bool(actorder), alias=self.__dict__.pop("_h_alias", None))
         Q, W_int, Scale = _compensate(_lib.VARIANT_GPTQ, self.quantizer, W, Hinv, blocksize,
                                       groupsize, static_groups,
                                       perm if static_groups and actorder else None, flags, graph,

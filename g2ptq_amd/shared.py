@@ -57,6 +57,12 @@ class SharedInputHessian:
         for inst, js in slots.values():
             if js == set(range(inst.num_layers)):
                 inst._shared_factor = self
+            # the instance's other member slots now hold copies of its first
+            # one: its batched factor need not factor them again (an add_batch
+            # on the instance drops the map)
+            first = min(js)
+            alias = inst.__dict__.setdefault("_h_alias", {})
+            alias.update({j: first for j in js if j != first})
 
     def fasterquant(self, blocksize=128, percdamp=0.01, groupsize=-1, actorder=False,
                     static_groups=False, export_compressed_tensors=False, backend="hip",

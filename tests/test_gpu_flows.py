@@ -497,3 +497,45 @@ def test_shared_input_joint_fasterquant_matches_per_instance(dev, rows_q, rows_k
     for xa, xb in zip(ia, ib):
         for qa, qb in zip(xa.quantizer, xb.quantizer):
             assert torch.equal(qa.scale, qb.scale) and torch.equal(qa.zero, qb.zero)
+
+
+def test_grouped_launch_factors_shared_slots_once(dev):
+    """One launch of four linears in two shared-input pairs (an MoE chunk's
+    gate/up): finalize maps slots 1 and 3 to 0 and 2, the batched factor
+    factors two Hessians instead of four, and the written weights equal a run
+    without the map bit for bit."""
+    from g2ptq_amd import GPTQ, SharedInputHessian, WeightQuantizer, make_group_quantizers
+    C, R = 256, 96
+    g = gen(4711)
+    w0 = [(torch.randn(R, C, generator=g) * 0.02).to(torch.bfloat16) for _ in range(4)]
+    sig = torch.exp(torch.randn(C, generator=g))
+    xs = [[(torch.randn(T, C, generator=g) * sig).to(torch.bfloat16).to(dev) for T in (300, 77, 512)]
+          for _ in range(2)]
+
+    def run(keep_map):
+        layers = [torch.nn.Linear(C, R, bias=False, device=dev, dtype=torch.bfloat16)
+                  for _ in range(4)]
+        with torch.no_grad():
+            for lin, w in zip(layers, w0):
+                lin.weight.copy_(w.to(dev))
+        gq = GPTQ(layers)
+        q = WeightQuantizer()
+        q.configure(4, perchannel=True, sym=True)
+        gq.quantizer = make_group_quantizers(q, C, 128)
+        shares = [SharedInputHessian([(gq, 0), (gq, 1)]), SharedInputHessian([(gq, 2), (gq, 3)])]
+        for sh, batches in zip(shares, xs):
+            for x in batches:
+                sh.add_batch(x)
+        for sh in shares:
+            sh.finalize()
+        assert gq._h_alias == {1: 0, 3: 2}
+        if not keep_map:
+            gq._h_alias = None
+        gq.fasterquant(blocksize=128, percdamp=0.01, groupsize=128, backend="hip")
+        torch.cuda.synchronize()
+        return [lin.weight.detach().cpu().view(torch.int16) for lin in layers]
+
+    with_map, without = run(True), run(False)
+    for a, b in zip(with_map, without):
+        assert torch.equal(a, b)
+    assert not torch.equal(with_map[0], with_map[2])  # the two pairs differ

@@ -113,6 +113,42 @@ def test_shared_input_factor_cache_invalidation():
     assert not hasattr(a, "_shared_factor") and b._shared_factor is sh
 
 
+def test_shared_input_slot_copies_map():
+    """finalize maps an instance's later member slots to its first one (the
+    batched factor factors that one only); the map goes away when the
+    instance's Hessian is replaced, and each share adds its own slots."""
+    from g2ptq_amd import GPTQ
+    g = GPTQ([torch.nn.Linear(8, 4, bias=False) for _ in range(4)])
+    SharedInputHessian([(g, 0), (g, 1)]).finalize()
+    SharedInputHessian([(g, 2), (g, 3)]).finalize()
+    assert g._h_alias == {1: 0, 3: 2}
+    assert not hasattr(g, "_shared_factor")  # two shares: no single cached factor
+    g.H = torch.ones(4, 8, 8)
+    assert "_h_alias" not in g.__dict__
+
+
+def test_factor_alias_map_is_checked(monkeypatch):
+    """_core.factor factors the unaliased slots once, as one batch, and hands
+    each aliased slot its source's U and damp."""
+    from g2ptq_amd import _core
+    seen = []
+
+    def fake(H, percdamp, shared=None, key=None, alias=None):
+        if alias:
+            return real(H, percdamp, shared, key, alias)
+        seen.append(H[:, 0, 0].tolist())
+        return H * 2, [percdamp + i for i in range(H.shape[0])]
+
+    real = _core.factor
+    monkeypatch.setattr(_core, "factor", fake)
+    H = torch.arange(4.0).view(4, 1, 1).expand(4, 2, 2).contiguous()
+    H[1] = H[0]
+    H[3] = H[2]
+    U, d = real(H, 0.5, alias={1: 0, 3: 2})
+    assert seen == [[0.0, 2.0]]
+    assert torch.equal(U, H * 2) and d == [0.5, 0.5, 1.5, 1.5]
+
+
 def test_weight_quantizer_deepcopy_is_independent():
     """make_group_quantizers deep-copies one quantizer per group: the copies are
     independent modules with the same configuration and buffers."""
