@@ -19,9 +19,21 @@ import torch
 
 class SharedInputHessian:
     def __init__(self, members):
-        """``members``: list of ``(quantizer_instance, layer_index)`` pairs."""
+        """``members``: list of ``(quantizer_instance, layer_index)`` pairs.
+
+        Only plain-Hessian quantizers share: GPTAQ's cross term takes each
+        linear's own full-precision input, and the weighted Hessians of G2PTQ
+        and GuidedQuant each linear's own saliencies, so their members are
+        refused."""
         if not members:
             raise ValueError("SharedInputHessian needs at least one member")
+        from .g2ptq_utils import G2PTQ
+        from .gptaq_utils import GPTAQ
+        from .gptq_guided_utils import GPTQGuided
+        for inst, _ in members:
+            if isinstance(inst, (GPTAQ, G2PTQ, GPTQGuided)):
+                raise ValueError(f"SharedInputHessian shares plain GPTQ Hessians; a "
+                                 f"{type(inst).__name__} Hessian depends on more than the input")
         self.members = list(members)
         self._factors = {}
 

@@ -113,6 +113,15 @@ def test_shared_input_factor_cache_invalidation():
     assert not hasattr(a, "_shared_factor") and b._shared_factor is sh
 
 
+def test_shared_input_refuses_non_plain_hessians():
+    """GPTAQ, G2PTQ and GuidedQuant Hessians depend on more than the shared
+    input: such members are refused."""
+    from g2ptq_amd import GPTAQ, GPTQ
+    lin = torch.nn.Linear(8, 4, bias=False)
+    with pytest.raises(ValueError, match="GPTAQ"):
+        SharedInputHessian([(GPTQ([lin]), 0), (GPTAQ([lin]), 0)])
+
+
 def test_shared_input_slot_copies_map():
     """finalize maps an instance's later member slots to its first one (the
     batched factor factors that one only); the map goes away when the
