@@ -338,7 +338,7 @@ def onload_attrs(owner, names, enabled=True, device=None):
         host = getattr(owner, n, None)
         if host is not None:
             staged[n] = host
-            setattr(owner, n, host.to(device=device, non_blocking=host.is_pinned()))
+            _swap(owner, n, host.to(device=device, non_blocking=host.is_pinned()))
     try:
         yield
     finally:
@@ -350,7 +350,18 @@ def onload_attrs(owner, names, enabled=True, device=None):
             if host is None or host.shape != v.shape or host.dtype != v.dtype:
                 host = torch.empty(v.shape, dtype=v.dtype, pin_memory=True)
             host.copy_(v)
-            setattr(owner, n, host)
+            _swap(owner, n, host)
+
+
+def _swap(owner, name, value):
+    """``owner.<name> = value`` for a copy of the same values on another
+    device: the attribute's setter keeps what it derived from the old
+    tensor (a shared-input group's cached factor, slot copies)."""
+    owner.__dict__["_same_values"] = True
+    try:
+        setattr(owner, name, value)
+    finally:
+        owner.__dict__.pop("_same_values", None)
 
 
 def alloc(shape, device, dtype=torch.float32, pin=False):

@@ -155,9 +155,16 @@ def query_size_i64(name, *args):
 
 def ptr(t):
     """Device pointer of a tensor as an integer (None → NULL); every entry
-    point declares its pointer arguments ``c_void_p``, which takes either."""
+    point declares its pointer arguments ``c_void_p``, which takes either.
+    Every kernel reads and writes device memory: a host tensor is refused
+    here, as torch refuses to mix devices (an offloaded Hessian outside its
+    onload context, a CPU input), before any kernel could touch it."""
     if t is None:
         return None
+    if not t.is_cuda:
+        raise RuntimeError(f"g2ptq_amd kernels take GPU tensors; got a {t.device} tensor "
+                           f"of shape {tuple(t.shape)} (an offloaded Hessian is usable only "
+                           "inside its onload context)")
     return t.data_ptr()
 
 

@@ -236,7 +236,8 @@ def staged_attr(name):
     def set(self, value):
         if value is None and getattr(self, private, None) is not None:
             self._flush_staged()
-        elif value is not None and getattr(self, private, None) is not None:
+        elif (value is not None and getattr(self, private, None) is not None
+              and not self.__dict__.get("_same_values")):
             # a replaced Hessian is no longer the one a shared-input group's
             # cached factor (or its slot copies) came from
             self.__dict__.pop("_shared_factor", None)

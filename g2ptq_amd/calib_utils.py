@@ -97,7 +97,7 @@ class _Slab:
         self.batches = []      # row views of the buffer, one per batch
         self.origins = []      # (address, shape) of the tensor each batch came from
         self._stream = None
-        self._pending = None   # event of the last device→host copy
+        self._pending = []     # events of the device→host copies in flight
 
     def take(self, k, x, name):
         origin = (x.data_ptr(), tuple(x.shape))
@@ -119,26 +119,35 @@ class _Slab:
         self.origins.append(origin)
         return rows
 
+    # device→host copies allowed in flight before the oldest is waited for
+    # (utils/offload_utils.py:60,114-117 bounds them the same way)
+    MAX_INFLIGHT = 2
+
     def _store(self, rows, x):
         if not x.is_cuda:
             rows.copy_(x)
             return
         # The copy runs on a stream of its own, after the work that produced x,
-        # so the forward pass is not held up by the device→host transfer.
+        # so the forward pass is not held up by the device→host transfer.  x's
+        # block stays reserved for the copy stream (record_stream), so the
+        # allocator cannot hand it out again before the copy has read it; a
+        # caller that writes into x itself must first wait for settle().
         if self._stream is None:
             self._stream = torch.cuda.Stream(device=x.device)
         self._stream.wait_stream(torch.cuda.current_stream(x.device))
         with torch.cuda.stream(self._stream):
             rows.copy_(x, non_blocking=True)
             x.record_stream(self._stream)
-            self._pending = torch.cuda.Event()
-            self._pending.record(self._stream)
+            done = torch.cuda.Event()
+            done.record(self._stream)
+        self._pending.append(done)
+        while len(self._pending) > self.MAX_INFLIGHT:
+            self._pending.pop(0).synchronize()
 
     def settle(self):
         """Wait until every stored batch has reached the host buffer."""
-        if self._pending is not None:
-            self._pending.synchronize()
-            self._pending = None
+        while self._pending:
+            self._pending.pop(0).synchronize()
 
 
 class FPInputsCache:

@@ -30,15 +30,20 @@ __device__ __forceinline__ float clamp_nan(float v, float lo, float hi) {
 // "Computation of elementary functions on the IBM RISC System/6000
 // processor", IBM J. Res. Dev. 34(1), 1990).  It equals the IEEE quotient
 // whenever r is exactly representable and nothing overflows, which holds for
-// |a|, |q| in [2^-100, 2^100]; any lane outside that range (zero, tiny, huge,
-// infinite or NaN operands) takes the IEEE division, on a wave-uniform branch
-// that real data never enters.  Three dependent operations instead of the
-// eleven of the IEEE division sequence on the sweep's per-column chain.
-__device__ __forceinline__ bool recip_div_exact(float a, float q) {
-  const float aa = fabsf(a), aq = fabsf(q);
-  return aa >= 0x1p-100f && aa <= 0x1p100f && aq >= 0x1p-100f && aq <= 0x1p100f;
+// |a|, |q| in [2^-100, 2^100].  It also gives the IEEE quotient for a = +0
+// whenever y is finite and nonzero (q = ±0 with the quotient's sign, r = +0,
+// q + r·y = q), which is what dead columns and exactly representable values
+// produce.  Any lane outside those cases (−0, tiny, huge, infinite or NaN
+// operands, a zero or infinite divisor) takes the IEEE division, on a
+// wave-uniform branch that real data never enters.  Three dependent
+// operations instead of the eleven of the IEEE division sequence on the
+// sweep's per-column chain.
+__device__ __forceinline__ bool recip_div_exact(float a, float q, float y) {
+  const float aa = fabsf(a), aq = fabsf(q), ay = fabsf(y);
+  const bool pos_zero = __float_as_uint(a) == 0u && ay > 0.f && ay < __builtin_inff();
+  return pos_zero || (aa >= 0x1p-100f && aa <= 0x1p100f && aq >= 0x1p-100f && aq <= 0x1p100f);
 }
-// Markstein's sequence alone: the IEEE quotient when recip_div_exact(a, RN(a·y)).
+// Markstein's sequence alone: the IEEE quotient when recip_div_exact(a, RN(a·y), y).
 __device__ __forceinline__ float div_markstein(float a, float b, float y) {
   const float q = __fmul_rn(a, y);
   const float r = __fmaf_rn(-b, q, a);
@@ -48,7 +53,7 @@ __device__ __forceinline__ float div_rn_recip(float a, float b, float y) {
   const float q = __fmul_rn(a, y);
   const float r = __fmaf_rn(-b, q, a);
   float res = __fmaf_rn(r, y, q);
-  const bool slow = !recip_div_exact(a, q);
+  const bool slow = !recip_div_exact(a, q, y);
   if (__builtin_amdgcn_ballot_w64(slow) != 0) {
     asm volatile("" ::: "memory");  // keeps the branch: the division is not speculated
     res = slow ? __fdiv_rn(a, b) : res;
@@ -876,8 +881,8 @@ __global__ __launch_bounds__(256) void sweep4_kernel(SweepArgs a) {
         const int c = p0 + L * s + sub;
         const float a1 = xo[s];
         const float a2 = (V == 2) ? __fsub_rn(__fsub_rn(a1, qb[s]), gb[s]) : __fsub_rn(a1, qb[s]);
-        inexact |= !recip_div_exact(a1, __fmul_rn(a1, ysv[s])) ||
-                   !recip_div_exact(a2, __fmul_rn(a2, rdiag[c]));
+        inexact |= !recip_div_exact(a1, __fmul_rn(a1, ysv[s]), ysv[s]) ||
+                   !recip_div_exact(a2, __fmul_rn(a2, rdiag[c]), rdiag[c]);
       }
       if (__builtin_amdgcn_ballot_w64(inexact) != 0) {
         // The second sweep recomputes its addresses from opaque copies of

@@ -67,8 +67,8 @@ class GPTQ:
 
     def add_batch(self, idx, inp, out):
         """gptq_utils.py:115-126: H ← H·n/(n+t) + (2/(n+t))·XᵀX, t = #sequences."""
-        if self.__dict__.get("_h_alias"):
-            self._h_alias = None  # slot copies made by a shared finalize are stale now
+        # slot copies made by a shared finalize are stale now
+        self.__dict__.pop("_h_alias", None)
         tmp = 1 if inp.dim() == 2 else inp.shape[0]  # a 2-D input is one sequence
         X = _core.as_bf16_tokens(inp)
         T = X.shape[0]

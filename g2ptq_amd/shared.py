@@ -73,8 +73,9 @@ class SharedInputHessian:
             # one: its batched factor need not factor them again (an add_batch
             # on the instance drops the map)
             first = min(js)
-            alias = inst.__dict__.setdefault("_h_alias", {})
+            alias = inst.__dict__.get("_h_alias") or {}
             alias.update({j: first for j in js if j != first})
+            inst._h_alias = alias
 
     def fasterquant(self, blocksize=128, percdamp=0.01, groupsize=-1, actorder=False,
                     static_groups=False, export_compressed_tensors=False, backend="hip",

@@ -237,9 +237,10 @@ int g2ptq_compensate(void* stream, int variant, int64_t B, int64_t R, int64_t C,
  * of 32 MiB (33554432 bytes), one per device, held until the process ends;
  * B·R·blocksize·4 must not exceed it (at blocksize 128, B·R ≤ 65536 rows),
  * else the call fails with G2PTQ_ERR_ARG before touching the device.  With
- * B·R·512·4 within it (B·R ≤ 16384) the loop runs as g2ptq_compensate does
- * with a one-buffer workspace; beyond that it applies every 128-column block's
- * tail separately.  It never overlaps tails on a side stream.  All calls on one
+ * B·R·512·4 within it (B·R ≤ 16384; G2PTQ also keeps one block's near-tail
+ * operand, B·R·640·4 in all, so B·R ≤ 13107 there) the loop runs as
+ * g2ptq_compensate does with a one-buffer workspace; beyond that it applies
+ * every 128-column block's tail separately.  It never overlaps tails on a side stream.  All calls on one
  * device share the array: calls that overlap in time on one device (two
  * streams or two host threads) race on it.  Everything else is as for
  * g2ptq_compensate; nothing is allocated. */

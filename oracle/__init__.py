@@ -24,6 +24,7 @@ Pinning (what checks each function independently of its own formula) lives in
   ⇒ RTN, blocksize invariance, GPTAQ(P=0) == GPTQ, G2PTQ(β=0) == GPTQ, a tiny-C
   fp64 optimal-brain-surgeon brute force, and the reference test's
   pre-refactor loops restated independently in ``original_loops``;
-* trust region (``flows.g2ptq_trust_region``): β∈[0,1], β=0 at α=0, and
-  ``GHinv == β·Grad·A⁻¹``.
+* trust region (``flows.g2ptq_trust_region``): β∈[0,1], β=0 at α=0,
+  ``GHinv == β·Grad·A⁻¹``, a 1×2 case worked by hand, and a diagonal A whose
+  β, Z and GHinv reduce to a scalar closed form (with and without the clamp).
 """

@@ -167,7 +167,7 @@ def gptaq_compensation(W, Hinv, P, quantizers, blocksize=128, groupsize=-1, stat
         S1, Z1 = _stack_params(cq, W1.shape)
         wt = W1.transpose(1, 2).contiguous()
         it, et, xt = torch.empty_like(wt), torch.empty_like(wt), torch.empty_like(wt)
-        cw = torch.empty(wt.shape[0], wt.shape[2])
+        cw = torch.empty(wt.shape[0], wt.shape[2], dtype=wt.dtype)
         gptaq_block(wt, Hinv[:, i1:i2, i1:i2].contiguous(), P[:, i1:i2, i1:i2].contiguous(),
                     S1.transpose(1, 2).contiguous(), Z1.transpose(1, 2).contiguous(), cw, it, et,
                     _maxq(quantizers), xt)

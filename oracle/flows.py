@@ -39,9 +39,13 @@ def _loop_record(record, perm):
 
 
 def gptq_fasterquant(W, H, bits, sym, blocksize=128, percdamp=0.01, groupsize=-1, actorder=False,
-                     static_groups=False, quantizers=None, mse=False, hclip=False):
-    """gptq_utils/gptq_utils.py:234-353 (returns instead of writing layers)."""
-    W = W.clone().float()
+                     static_groups=False, quantizers=None, mse=False, hclip=False,
+                     dtype=torch.float32):
+    """gptq_utils/gptq_utils.py:234-353 (returns instead of writing layers).
+
+    ``dtype=torch.float64`` (with an fp64 ``H``) runs the same steps in fp64:
+    the parity tests' measure of how far fp32 orderings move x/s."""
+    W = W.clone().to(dtype)
     H = H.clone()
     B, R, C = W.shape
     if quantizers is None:
@@ -74,9 +78,9 @@ def gptq_fasterquant(W, H, bits, sym, blocksize=128, percdamp=0.01, groupsize=-1
 
 def gptaq_fasterquant(W, H, dXXT, bits, sym, blocksize=128, percdamp=0.01, groupsize=-1,
                       actorder=False, static_groups=False, alpha=0.25, quantizers=None,
-                      mse=False, hclip=False):
-    """gptq_utils/gptaq_utils.py:263-391."""
-    W = W.clone().float()
+                      mse=False, hclip=False, dtype=torch.float32):
+    """gptq_utils/gptaq_utils.py:263-391 (``dtype`` as for gptq_fasterquant)."""
+    W = W.clone().to(dtype)
     H = H.clone()
     dXXT = dXXT.clone()
     B, R, C = W.shape
@@ -131,16 +135,17 @@ def g2ptq_trust_region(gradients_sub, Hinv_init, Hinv, Q_sub, W_sub, alpha, enab
 def g2ptq_fasterquant(W, H, gradients, act_square, bits, sym, num_groups, blocksize=128,
                       percdamp=0.01, groupsize=-1, actorder=False, static_groups=False,
                       enable_gradient_update=True, alpha=0.0, quantizers=None, mse=False,
-                      hclip=False):
-    """gptq_utils/g2ptq_utils.py:349-519.  ``H`` is (B, G, C, C), mutated like the reference."""
-    W = W.clone().float()
+                      hclip=False, dtype=torch.float32):
+    """gptq_utils/g2ptq_utils.py:349-519.  ``H`` is (B, G, C, C), mutated like the reference
+    (``dtype`` as for gptq_fasterquant)."""
+    W = W.clone().to(dtype)
     B, R, C = W.shape
     G = num_groups
     if quantizers is None:
         quantizers = _configure(bits, sym, C, groupsize, mse, hclip)
     W_flat = W.view(B * R, C)
     W_sub = W.contiguous().view(B * G, R // G, C)
-    grads = gradients.reshape(B * G, R // G, C).clone()
+    grads = gradients.reshape(B * G, R // G, C).to(dtype).clone()
     H_sub = H.view(B * G, C, C)
     H_diag = _hdiag(quantizers, H_sub)
     _static_params(quantizers, W_flat, groupsize, static_groups, H_diag)
@@ -191,9 +196,9 @@ def g2ptq_fasterquant(W, H, gradients, act_square, bits, sym, num_groups, blocks
 
 def guided_fasterquant(W, H, act_square, bits, sym, num_groups, blocksize=128, percdamp=0.01,
                        groupsize=-1, actorder=False, static_groups=False, quantizers=None,
-                       mse=False, hclip=False):
-    """gptq_utils/gptq_guided_utils.py:83-211."""
-    W = W.clone().float()
+                       mse=False, hclip=False, dtype=torch.float32):
+    """gptq_utils/gptq_guided_utils.py:83-211 (``dtype`` as for gptq_fasterquant)."""
+    W = W.clone().to(dtype)
     B, R, C = W.shape
     G = num_groups
     if quantizers is None:

@@ -121,7 +121,9 @@ def test_fp_inputs_cache_offload_from_gpu(dev):
     """gptaq_utils.py:442-555 with device activations: offloaded batches go to
     page-locked host slabs through a copy stream and are complete once the hooks
     are cleared; shared-input members get the same host rows; GPTAQ consumes
-    the FIFO exactly as it would the device tensors."""
+    the FIFO exactly as it would the device tensors.  Each source tensor is
+    dropped right after its forward and its memory refilled at once: the
+    copy stream keeps the freed block reserved until the copy has read it."""
     from g2ptq_amd import GPTAQ
     from g2ptq_amd.calib_utils import FPInputsCache
     torch.manual_seed(11)
@@ -129,11 +131,13 @@ def test_fp_inputs_cache_offload_from_gpu(dev):
     cache = FPInputsCache([["q", "k"]], full, nsamples=3, seqlen=128, dtype=torch.bfloat16,
                           offload_inps=True, shared_input_groups=[("q", "k")])
     cache.add_hook(full)
-    xs = [torch.randn(1, 128, 256, device=dev).bfloat16() for _ in range(3)]
-    for x in xs:
+    refill = []
+    for _ in range(3):
+        x = torch.randn(1, 128, 256, device=dev).bfloat16()
         for n in ("q", "k"):
             full[n](x)
-        x.mul_(0)  # overwrite the device tensor: the copy must have been ordered before
+        del x  # the block returns to the allocator while its copy may be in flight
+        refill.append(torch.zeros(1, 128, 256, device=dev, dtype=torch.bfloat16))
     cache.clear_hook()
     for n in ("q", "k"):
         assert len(cache.fp_cache[n]) == 3

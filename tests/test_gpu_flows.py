@@ -240,6 +240,10 @@ FROM_X_CASES = (
     ("cfg5_gptaq_w2_g64_alpha0.25", "gptaq", 2, True, 64, False, 0.25),
     ("gptaq_w4_asym_g128_actorder_static", "gptaq", 4, False, 128, True, 0.25),
     ("guided_w4_sym_g128", "guided", 4, True, 128, False, None),
+    # act-order from calibration data: G2PTQ and GuidedQuant order columns by
+    # act_square (g2ptq_utils.py:417-419), GPTQ/GPTAQ by the Hessian diagonal
+    ("g2ptq_w3_sym_g128_actorder_static_alpha0.1", "g2ptq", 3, True, 128, True, 0.1),
+    ("guided_w4_asym_g128_actorder_static", "guided", 4, False, 128, True, None),
 )
 
 
@@ -385,6 +389,88 @@ def test_gptq_without_calibration_is_rtn(dev, sym):
     Qd = torch.stack([l.weight.detach().float().cpu() for l in layers])
     fq, _, _ = oflows.rtn(W0, 4, sym, gs)
     assert torch.equal(Qd, fq.bfloat16().float())
+
+
+@pytest.mark.parametrize("method", ["gptq", "gptaq", "g2ptq", "guided"])
+def test_offload_hessians_bit_identical(dev, method):
+    """offload_hessians=True (gptq_utils.py:103-113, 507-509; the G2PTQ and
+    GuidedQuant variants): the Hessians live in host memory, calibration runs
+    inside the onload context (two windows, as a driver onloads per layer
+    batch), and fasterquant onloads them again.  The weights and fitted
+    group parameters equal a resident run's bit for bit (the resident run
+    reads H where the offloaded one leaves its onload context, so both fold
+    their staged tokens at the same points); outside an onload context the
+    host Hessian is refused before any kernel runs."""
+    from g2ptq_amd import G2PTQ, GPTAQ, GPTQ, GPTQGuided, WeightQuantizer, make_group_quantizers
+    B, R, C, T, chunk, G, bits, gs = 2, 128, 512, 4096, 1024, 4, 4, 128
+    print(f"offload_hessians: {method}", flush=True)
+    g = gen(950)
+    sig = torch.exp(torch.randn(C, generator=g))
+    X = (torch.randn(T, C, generator=g) * sig).bfloat16().to(dev)
+    Xfp = (X.float() + 0.05 * sig.to(dev) * torch.randn(T, C, generator=g).to(dev)).bfloat16()
+    sal = (torch.rand(T, G, generator=g) + 0.1).to(dev)
+    grads = [1e-3 * torch.randn(R, C, generator=g) for _ in range(B)]
+    W = (torch.randn(B, R, C, generator=g) * 0.02).bfloat16()
+    batches = list(range(0, T, chunk))
+
+    def make(offload):
+        layers = []
+        for b in range(B):
+            lin = torch.nn.Linear(C, R, bias=False).to(torch.bfloat16)
+            with torch.no_grad():
+                lin.weight.copy_(W[b])
+            layers.append(lin.to(dev))
+        if method == "gptq":
+            gq = GPTQ(layers, offload_hessians=offload)
+        elif method == "gptaq":
+            gq = GPTAQ(layers, offload_hessians=offload)
+            for b in range(B):
+                gq.fp_inp[b] = [Xfp[i:i + chunk] for i in batches]
+        elif method == "g2ptq":
+            gq = G2PTQ(layers, [[sal[i:i + chunk] for i in batches] for _ in range(B)],
+                       [gr.to(dev) for gr in grads], G, offload_hessians=offload)
+        else:
+            gq = GPTQGuided(layers, [sal.reshape(T // chunk, chunk, G) for _ in range(B)], G,
+                            offload_hessians=offload)
+        q = WeightQuantizer()
+        q.configure(bits, perchannel=True, sym=True)
+        gq.quantizer = make_group_quantizers(q, C, gs)
+        return layers, gq
+
+    def onload(gq):
+        if method == "g2ptq":
+            return gq._maybe_onload_hessian_grad()
+        return gq._maybe_onload_hessian()
+
+    kw = dict(blocksize=128, percdamp=0.01, groupsize=gs, backend="hip")
+    if method in ("gptaq", "g2ptq"):
+        kw["alpha"] = 0.25 if method == "gptaq" else 0.1
+    out = []
+    for offload in (False, True):
+        layers, gq = make(offload)
+        for window in (batches[:2], batches[2:]):
+            with onload(gq):
+                for i in window:
+                    for b in range(B):
+                        gq.add_batch(b, X[i:i + chunk].unsqueeze(0), None)
+            if not offload:
+                gq.H  # the offloaded run folds its staged tokens here (onload exit)
+        if offload:
+            assert gq.H.device.type == "cpu"
+        gq.fasterquant(**kw)
+        torch.cuda.synchronize()
+        out.append((torch.stack([l.weight.detach().cpu() for l in layers]),
+                    [(qz.scale.detach().cpu(), qz.zero.detach().cpu()) for qz in gq.quantizer]))
+    (w_res, p_res), (w_off, p_off) = out
+    assert torch.equal(w_res.view(torch.int16), w_off.view(torch.int16))
+    for (s0, z0), (s1, z1) in zip(p_res, p_off):
+        assert torch.equal(s0, s1) and torch.equal(z0, z1)
+    # calibration outside the onload context: the staged tokens cannot be
+    # folded into a host Hessian
+    _, gq = make(True)
+    gq.add_batch(0, X[:chunk].unsqueeze(0), None)
+    with pytest.raises(RuntimeError, match="onload"):
+        gq.H
 
 
 def test_dead_columns_are_zeroed(dev):

@@ -345,6 +345,51 @@ def test_block_sweep_exact_rerun_bitexact(dev, variant):
         _assert_same_bits(a, e, what)
 
 
+@pytest.mark.parametrize("variant", ["gptq", "gptaq", "g2ptq"])
+def test_block_sweep_dead_columns_bitexact(dev, variant):
+    """Dead input columns (the weight column exactly +0 and U's entries above
+    the diagonal in that column zero, so the column stays +0 until it is
+    quantized) and a column on the quantization grid give +0 dividends in the
+    sweep's divisions; the fast pass divides them exactly, and every output
+    equals the oracle's bit for bit."""
+    batch, columns, rows, maxq = 2, 128, 300, 7
+    w, h, s, z = ref_inputs(batch, columns, rows, maxq, True, 421)
+    dead = [0, 5, 37, 64, 127]
+    w = w.clone()
+    h = h.clone()
+    for c in dead:
+        w[:, c, :] = 0.0
+        h[:, :c, c] = 0.0
+    w[:, 90, :] = torch.round(w[:, 90, :] / s[:, 90, :]) * s[:, 90, :]
+    hd, sd, zd = h.to(dev), s.to(dev), z.to(dev)
+    ew, ei, ee = w.clone(), torch.empty_like(w), torch.empty_like(w)
+    dw, di, de = w.to(dev), torch.empty_like(w, device=dev), torch.empty_like(w, device=dev)
+    extra = []
+    if variant == "gptq":
+        from g2ptq_amd.gptq_utils import run_eager
+        ocomp.gptq_block(ew, h, s, z, ei, ee, maxq)
+        run_eager(dw, hd, sd, zd, maxq, "hip", di, de)
+    elif variant == "gptaq":
+        from g2ptq_amd.gptaq_utils import run_eager
+        p = gptaq_p(w, 3421)
+        ecw, dcw = torch.empty(batch, rows), torch.empty(batch, rows, device=dev)
+        ocomp.gptaq_block(ew, h, p, s, z, ecw, ei, ee, maxq)
+        run_eager(dw, hd, p.to(dev), sd, zd, maxq, "hip", dcw, di, de)
+        extra.append((dcw, ecw, "column_weight"))
+    else:
+        from g2ptq_amd.g2ptq_utils import run_eager
+        zz, gh = g2_inputs(w, s, 1421)
+        egh, dgh = gh.clone(), gh.to(dev)
+        ocomp.g2ptq_block(ew, h, s, z, zz, egh, ei, ee, maxq)
+        run_eager(dw, hd, sd, zd, zz.to(dev), dgh, maxq, "hip", di, de)
+        extra.append((dgh, egh, "ghinv"))
+    torch.cuda.synchronize()
+    for a, e, what in [(di, ei, "codes"), (dw, ew, "weight"), (de, ee, "error")] + extra:
+        _assert_same_bits(a, e, what)
+    if variant == "gptq":
+        assert bool((ee[:, dead, :] == 0).all())
+
+
 def test_superblock_sweep_exact_rerun_matches_fast_pass(dev):
     """GPTQ's super-block launch (C = 1024: two super-blocks of four blocks,
     16 lanes per row): rows of ±0, tiny, subnormal and huge values make their

@@ -1,38 +1,44 @@
 """GPU: the Hessian kinds whose staged operand is not bf16-exact, at the
 benchmark configurations' calibration size, held to the end-to-end parity
-protocol.
+protocol, and the tie window that protocol uses at this size measured
+against fp64.
 
 The weighted (G2PTQ) and GPTAQ Hessians stage x·s and X_fp − X as hi + lo
 bf16 planes (16 significant bits; the reference keeps fp32's 24), so their
 rounding differs from the reference's more than a plain Hessian's does.  Each
 test accumulates the Hessians of 262,144 calibration tokens (32 batches of
 8192, LogNormal channel scales) on the GPU, computes the same Hessians
-exactly (fp64 on the GPU, rounded to fp32), and runs the oracle flow
-(oracle.flows) from the exact Hessians on the CPU.  The HIP flow from its own
-Hessians, and the HIP flow from the exact ones, must both meet the bar of
-oracle.parity.check_flow: each row's first differing code at a rounding tie
-of the oracle's run, such rows at most 0.01 % of the entries, scales and
+exactly (fp64 on the GPU), and runs the oracle flow (oracle.flows) from the
+exact Hessians on the CPU twice: in fp32 (the reference's arithmetic) and in
+fp64.  The HIP flow from its own Hessians, and the HIP flow from the exact
+ones (rounded to fp32), must both meet the bar of oracle.parity.check_flow
+against the fp32 oracle: each row's first differing code at a rounding tie
+of the exact run, such rows at most 0.01 % of the entries, scales and
 dequantized weights within 1e-3 before them, reconstruction error within
-0.5 %.  A tie is |frac(x/s) − ½| < 5e-4 here, not the 1e-4 of the C = 1024
-tests: over a 4096-column compensation the fp32 orderings of the two
-implementations (factor, trust region, tails) move x/s by up to 2e-4, and
-the flow from the exact Hessians shows the same farthest divergence
-(1.8e-4) as the flow from the staged ones (measured on MI355X: G2PTQ 14 and
-12 of 256 rows diverge, all but one at 1e-4 ties; GPTAQ none).
+0.5 %.  Over a 4096-column compensation any fp32 ordering moves x/s by a few
+1e-4 at rare entries, so two fp32 computations can round a value that close
+to a tie differently; which one strays is decided by the fp64 run.  A flow's
+codes first differ from the fp64 run's only where the exact x/s lies within
+that flow's own error of a tie, so the largest such tie distance measures how
+far its x/s strays from exact arithmetic: the HIP flow's must be at most
+twice the fp32 oracle's, and where the HIP and fp32 flows differ the exact
+x/s must lie at most twice the oracle's own distance from a tie (at least
+the protocol's 1e-4).
 
-* config 3's G2PTQ at C = 4096 (one linear of 4 row groups × 64 rows, W3 g128,
-  α = 0.1, per-token saliencies);
-* config 5's GPTAQ at C = 8192 (64 rows, W2 g64, α = 0.25, X_fp = X plus
-  N(0, 0.05·σ_c)); config 5's own C = 28672 would take the CPU oracle minutes.
+* config 3's G2PTQ at C = 4096 (one linear of 4 row groups × 256 rows, W3
+  g128, α = 0.1, per-token saliencies);
+* config 5's GPTAQ at C = 8192 (256 rows, W2 g64, α = 0.25, X_fp = X plus
+  N(0, 0.05·σ_c)); config 5's own C = 28672 would take the CPU oracle minutes
+  per run (its full width is checked on sampled rows in test_gpu_configs).
 """
 import pytest
 import torch
 
 from oracle import flows as oflows
-from oracle.parity import check_flow
+from oracle.parity import check_flow, element_params, exported_codes, loop_order, stage_b
 from tests._util import gen
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.timeout(900)]
 
 N_TOKENS, CHUNK = 262144, 8192
 
@@ -58,22 +64,99 @@ def _linear(R, C, seed, dev):
     return lin
 
 
-TIE_TOL = 5e-4
+# Ties are judged by the fp64 run.  A HIP code may differ from the fp32
+# oracle's (first in its row) only where the exact x/s lies within
+# NOISE_FACTOR × the fp32 oracle's own largest such distance of a tie (the
+# oracle itself rounds away from exact that close to a tie), never less than
+# the protocol's MIN_TIE; below FLOOR distances are single roundings.
+NOISE_FACTOR, FLOOR, MIN_TIE = 2.0, 2e-5, 1e-4
 
 
-def _bar(label, layers, quantizers, layers2, quantizers2, ref, W0, H, bits, gs):
-    """The flow from the staged Hessians and the flow from the exact ones,
-    each against the oracle (from the exact Hessians), held to the bar."""
-    staged = check_flow(label + ", staged Hessians", layers, quantizers, ref, W0, H, bits, gs,
-                        False, tie_tol=TIE_TOL)
-    exact = check_flow(label + ", exact Hessians", layers2, quantizers2, ref, W0, H, bits, gs,
-                       False, tie_tol=TIE_TOL)
-    return staged, exact
+def _first_divergence(a, b):
+    """Per row, the first column where ``a`` and ``b`` differ (C if none)."""
+    N, C = a.shape
+    diff = a != b
+    first = torch.full((N,), C, dtype=torch.int64)
+    rows = diff.any(1)
+    first[rows] = diff[rows].to(torch.int8).argmax(1)
+    return first
+
+
+def _exact_ties(label, codes, ref, ref64, gs):
+    """The flow's first divergences from the fp32 oracle, each judged by the
+    fp64 run: its x/s distance from a tie there.  Where the fp32 oracle's row
+    already left the fp64 run's codes earlier, the fp64 value is of another
+    history and the oracle's own x/s is used.  Returns the largest distance."""
+    N, C = codes.shape
+    perm = ref64["perm"]
+    cr = loop_order(ref["W_int"].reshape(N, C), perm)
+    c64 = loop_order(ref64["W_int"].reshape(N, C), perm)
+    ch = loop_order(codes, perm)
+    f_h = _first_divergence(ch, cr)
+    f_64 = _first_divergence(cr, c64)
+    s32, _ = element_params(ref["quantizers"], N, C, gs, False, perm)
+    s64, _ = element_params(ref64["quantizers"], N, C, gs, False, perm)
+    x32 = ref["loop"]["X"].reshape(N, C).double()
+    x64 = ref64["loop"]["X"].reshape(N, C).double()
+    worst, other = 0.0, 0
+    for r in (f_h < C).nonzero().flatten().tolist():
+        j = int(f_h[r])
+        if int(f_64[r]) < j:
+            t = float(x32[r, j] / s32[r, j].double())
+            other += 1
+        else:
+            t = float(x64[r, j] / s64[r, j].double())
+        worst = max(worst, abs(t - float(torch.floor(torch.tensor(t))) - 0.5))
+    print(f"{label}: {int((f_h < C).sum())} rows first differ from the fp32 oracle, the exact "
+          f"x/s at most {worst:.3g} from a tie there ({other} judged by the oracle's x/s)",
+          flush=True)
+    return worst
+
+
+def _fp64_distance(label, codes, quantizers, ref64, gs):
+    """How far a flow strays from exact arithmetic: its codes against the fp64
+    oracle's, in loop order; at each row's first differing code, the fp64
+    run's distance |frac(x/s) − ½| from a rounding tie.  Returns the report
+    (``max_tie_distance``, ``rows_diverged``)."""
+    N, C = codes.shape
+    perm = ref64["perm"]
+    s, z = element_params(quantizers, N, C, gs, False, perm)
+    s64, z64 = element_params(ref64["quantizers"], N, C, gs, False, perm)
+    rep = stage_b(loop_order(codes, perm), loop_order(ref64["W_int"].reshape(N, C), perm),
+                  ref64["loop"]["X"].reshape(N, C), s, s64, z, z64,
+                  loop_order(ref64["Q"].reshape(N, C), perm), tol=0.5)
+    print(f"{label} vs fp64: {rep['rows_diverged']}/{rep['rows']} rows first differ, at most "
+          f"{rep['max_tie_distance']:.3g} from a tie", flush=True)
+    return rep
+
+
+def _bar(label, layers, quantizers, layers2, quantizers2, ref, ref64, W0, H, bits, gs):
+    """The flow from the staged Hessians and the flow from the exact ones.
+    Each one's distance from the fp64 oracle may be at most NOISE_FACTOR × the
+    fp32 oracle's; against the fp32 oracle, each first differing code must lie
+    at a tie of the exact run, as close as the oracle's own divergences from
+    exact (×NOISE_FACTOR); and the rest of the bar of check_flow (first
+    divergences ≤ 0.01 % of entries, scales and dequantized weights within
+    1e-3 before them, write-back, reconstruction error within 0.5 %)."""
+    C = W0.shape[-1]
+    d_ref = _fp64_distance(label + ", fp32 oracle", ref["W_int"].reshape(-1, C),
+                           ref["quantizers"], ref64, gs)["max_tie_distance"]
+    window = max(NOISE_FACTOR * max(d_ref, FLOOR), MIN_TIE)
+    out = []
+    for name, (lay, qz) in (("staged", (layers, quantizers)), ("exact", (layers2, quantizers2))):
+        lab = f"{label}, HIP from {name} Hessians"
+        codes = exported_codes(lay, bits, C)
+        d = _fp64_distance(lab, codes, qz, ref64, gs)["max_tie_distance"]
+        assert d <= NOISE_FACTOR * max(d_ref, FLOOR), (lab, d, d_ref)
+        worst = _exact_ties(lab, codes, ref, ref64, gs)
+        assert worst <= window, (lab, worst, window)
+        out.append(check_flow(lab, lay, qz, ref, W0, H, bits, gs, False, tie_tol=1.0))
+    return out
 
 
 def test_g2ptq_weighted_hessians_at_config3_scale(dev):
     from g2ptq_amd import G2PTQ, WeightQuantizer, make_group_quantizers
-    C, G, Rg, bits, gs, alpha = 4096, 4, 64, 3, 128, 0.1
+    C, G, Rg, bits, gs, alpha = 4096, 4, 256, 3, 128, 0.1
     R = G * Rg
     print(f"G2PTQ full-scale precision: C={C} tokens={N_TOKENS} G={G} R={R}", flush=True)
     X, _, g = _tokens(C, 501, dev)
@@ -98,7 +181,8 @@ def test_g2ptq_weighted_hessians_at_config3_scale(dev):
         for grp in range(G):
             He[grp] += (x * sal[i:i + CHUNK, grp:grp + 1].double()).T @ x
         act += (x * x).sum(0)
-    He = (He / N_TOKENS).float().cpu()
+    He64 = (He / N_TOKENS).cpu()
+    He = He64.float()
     act = (act / N_TOKENS).float().cpu()
     Hd = gq.H[0].detach().cpu()
     rel = ((Hd - He).abs() / torch.sqrt(torch.diagonal(He, dim1=1, dim2=2).unsqueeze(2) *
@@ -117,13 +201,16 @@ def test_g2ptq_weighted_hessians_at_config3_scale(dev):
     torch.cuda.synchronize()
     ref = oflows.g2ptq_fasterquant(W0, He.unsqueeze(0).clone(), grads.unsqueeze(0),
                                    act.unsqueeze(0), bits, True, G, groupsize=gs, alpha=alpha)
-    _bar("G2PTQ C=4096, 262144 tokens", [lin], gq.quantizer, [lin2], gq2.quantizer, ref, W0, He,
-         bits, gs)
+    ref64 = oflows.g2ptq_fasterquant(W0, He64.unsqueeze(0).clone(), grads.unsqueeze(0),
+                                     act.unsqueeze(0).double(), bits, True, G, groupsize=gs,
+                                     alpha=alpha, dtype=torch.float64)
+    _bar("G2PTQ C=4096, 262144 tokens", [lin], gq.quantizer, [lin2], gq2.quantizer, ref, ref64,
+         W0, He, bits, gs)
 
 
 def test_gptaq_cross_term_at_config5_scale(dev):
     from g2ptq_amd import GPTAQ, WeightQuantizer, make_group_quantizers
-    C, R, bits, gs, alpha = 8192, 64, 2, 64, 0.25
+    C, R, bits, gs, alpha = 8192, 256, 2, 64, 0.25
     print(f"GPTAQ full-scale precision: C={C} tokens={N_TOKENS} R={R}", flush=True)
     X, sig, g = _tokens(C, 601, dev)
     lin = _linear(R, C, 602, dev)
@@ -146,8 +233,9 @@ def test_gptaq_cross_term_at_config5_scale(dev):
     # one sequence per batch: H = (2/K)·Σ x·xᵀ, dXXT = (2/K)·Σ (x_fp − x)·xᵀ
     # over the K batches (gptaq_utils.py:130-148)
     K = len(batches)
-    He = (He * (2.0 / K)).float().cpu()
-    De = (De * (2.0 / K)).float().cpu()
+    He64 = (He * (2.0 / K)).cpu()
+    De64 = (De * (2.0 / K)).cpu()
+    He, De = He64.float(), De64.float()
     Hd = gq.H[0].detach().cpu()
     Dd = gq.dXXT[0].detach().cpu()
     d = torch.diagonal(He)
@@ -168,5 +256,7 @@ def test_gptaq_cross_term_at_config5_scale(dev):
     torch.cuda.synchronize()
     ref = oflows.gptaq_fasterquant(W0, He.unsqueeze(0), De.unsqueeze(0), bits, True,
                                    groupsize=gs, alpha=alpha)
-    _bar("GPTAQ C=8192, 262144 tokens", [lin], gq.quantizer, [lin2], gq2.quantizer, ref, W0,
-         He.unsqueeze(0), bits, gs)
+    ref64 = oflows.gptaq_fasterquant(W0, He64.unsqueeze(0), De64.unsqueeze(0), bits, True,
+                                     groupsize=gs, alpha=alpha, dtype=torch.float64)
+    _bar("GPTAQ C=8192, 262144 tokens", [lin], gq.quantizer, [lin2], gq2.quantizer, ref, ref64,
+         W0, He.unsqueeze(0), bits, gs)

@@ -136,6 +136,37 @@ def test_shared_input_slot_copies_map():
     assert "_h_alias" not in g.__dict__
 
 
+def test_shared_input_slot_map_rebuilt_after_recalibration():
+    """add_batch on a two-slot member drops its slot map, and the next
+    finalize builds it again (re-calibration of an MoE-chunk-like instance)."""
+    from g2ptq_amd import GPTQ
+    g = GPTQ([torch.nn.Linear(8, 4, bias=False) for _ in range(2)])
+    sh = SharedInputHessian([(g, 0), (g, 1)])
+    sh.finalize()
+    assert g._h_alias == {1: 0}
+    # the map is dropped before the input is checked (a CPU tensor is refused)
+    with pytest.raises(RuntimeError, match="GPU"):
+        g.add_batch(0, torch.zeros(1, 3, 8, dtype=torch.bfloat16), None)
+    assert "_h_alias" not in g.__dict__
+    sh.finalize()
+    assert g._h_alias == {1: 0}
+
+
+def test_onload_keeps_shared_factor_and_slot_map():
+    """Moving an offloaded Hessian onto the device and back is the same
+    Hessian: the group's cached factor and the slot map survive the swap,
+    while a genuinely new Hessian still drops them."""
+    from g2ptq_amd import GPTQ, _core
+    g = GPTQ([torch.nn.Linear(8, 4, bias=False) for _ in range(2)], offload_hessians=True)
+    sh = SharedInputHessian([(g, 0), (g, 1)])
+    sh.finalize()
+    with _core.onload_attrs(g, ("H",), enabled=True, device="cpu"):
+        assert g._shared_factor is sh and g._h_alias == {1: 0}
+    assert g._shared_factor is sh and g._h_alias == {1: 0}
+    g.H = torch.ones(2, 8, 8)
+    assert "_shared_factor" not in g.__dict__ and "_h_alias" not in g.__dict__
+
+
 def test_factor_alias_map_is_checked(monkeypatch):
     """_core.factor factors the unaliased slots once, as one batch, and hands
     each aliased slot its source's U and damp."""

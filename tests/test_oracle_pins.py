@@ -108,10 +108,11 @@ def test_quant_hclip_uniform_weights():
         assert torch.equal(q.scale, s_24) and torch.equal(q.zero, z_24)
 
 
-def _brute_force_clip(xrow, w, bits, sym, grid=50, maxshrink=0.5):
-    """First strict minimum over the clip grid of sum_c (fq_c - x_c)^2 * w_c,
-    one row at a time with scalar fp32 arithmetic (independent of the
-    oracle's tensor reshapes)."""
+def _brute_force_clip(xrow, w, bits, sym, grid=50, maxshrink=0.5, norm=None, scores=None):
+    """First strict minimum over the clip grid of sum_c (fq_c - x_c)^2 * w_c
+    (or, with ``norm``, of sum_c |fq_c - x_c|^norm), one row at a time with
+    scalar fp32 arithmetic (independent of the oracle's tensor reshapes).
+    ``scores`` (a list) receives every candidate's objective."""
     maxq = 2 ** (bits - 1) - 1
     minq = -(maxq + 1)
     f = lambda v: torch.tensor(v, dtype=torch.float32)
@@ -131,14 +132,45 @@ def _brute_force_clip(xrow, w, bits, sym, grid=50, maxshrink=0.5):
                 z = torch.clamp(torch.round(minq - lo / s), minq, maxq)
             err = 0.0
             for c in range(xrow.numel()):
-                if w[c] == 0:
+                if w is not None and w[c] == 0:
                     continue
                 q = torch.clamp(torch.round(xrow[c] / s) + z, minq, maxq)
                 d = (s * (q - z) - xrow[c]).double().item()
-                err += d * d * float(w[c])
+                err += abs(d) ** norm if norm is not None else d * d * float(w[c])
+            if scores is not None:
+                scores.append(err)
             if err < best:
                 best, choice = err, (s.item(), torch.round(z).item())
     return choice
+
+
+def test_quant_mse_norm_objective_brute_force():
+    """The plain clip search (quant_utils.py:406-425, _quant_err :84-105)
+    minimises sum_c |fq_c − x_c|^2.4.  Rows with one large entry gain from
+    clipping, so the search moves off min/max; the oracle's choice must be
+    the scalar brute force's first strict minimum wherever the runner-up is
+    more than 1e-6 relative away (fp32 sums in another order cannot swap
+    such candidates), and its objective the minimum everywhere."""
+    g = gen(13)
+    x = torch.randn(12, 16, generator=g) * 0.02
+    x[torch.arange(12), torch.randint(0, 16, (12,), generator=g)] *= 6.0
+    checked = moved = 0
+    for sym in (True, False):
+        s_o, z_o = oquant.find_params(x, 3, sym, mse=True)
+        s_m, _ = oquant.find_params(x, 3, sym)
+        for r in range(12):
+            scores = []
+            s_b, z_b = _brute_force_clip(x[r], None, 3, sym, norm=2.4, scores=scores)
+            best = min(scores)
+            second = min(v for v in scores if v > best) if any(v > best for v in scores) else best
+            q = torch.clamp(torch.round(x[r] / s_o[r]) + z_o[r], -4, 3)
+            e_o = float(((s_o[r] * (q - z_o[r]) - x[r]).double().abs() ** 2.4).sum())
+            assert e_o <= best * (1 + 1e-6), (sym, r)
+            if second > best * (1 + 1e-6):
+                assert s_o[r].item() == s_b and z_o[r].item() == z_b, (sym, r)
+                checked += 1
+            moved += int(s_o[r].item() != s_m[r].item())
+    assert checked >= 16 and moved >= 12, (checked, moved)
 
 
 def test_quant_hclip_rows_use_their_block_and_group():
