@@ -54,6 +54,9 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-kernel-rates", action="store_true",
                    help="skip the standalone factor / sweep / tail-product timings")
+    p.add_argument("--no-unchanged-driver", action="store_true",
+                   help="skip the block timed the way the reference driver runs it "
+                        "(per-linear Hessians, per-instance fasterquant)")
     p.add_argument("--no-g2ptq", action="store_true",
                    help="skip the config-3 G2PTQ block reported beside the benchmark line")
     p.add_argument("--tokens", type=int, default=N_TOKENS)
@@ -93,14 +96,22 @@ def _linear(R, C, dtype, g, dev, outlier_cols=0):
     return lin
 
 
-def workload_cfg1(dev, steps, warmup):
-    """configs[0]: one 4096×4096 fp32 linear (1 % of input columns ×10), GPTQ W4
-    asym g128, 262144 tokens in batches of 8192."""
-    from g2ptq_amd import GPTQ, WeightQuantizer, make_group_quantizers
+def cfg1_inputs(dev):
+    """configs[0]'s inputs: 262144 tokens × 4096 (LogNormal channels, bf16) and one
+    4096×4096 fp32 linear ~N(0, 0.02) with round(1 %·4096) input columns ×10."""
     g = torch.Generator(device=dev).manual_seed(42)
     C, R, n = 4096, 4096, N_TOKENS
     X = _tokens(n, C, _lognormal_channels(C, g, dev), g, dev)
     lin = _linear(R, C, torch.float32, g, dev, outlier_cols=round(0.01 * C))
+    return X, lin
+
+
+def workload_cfg1(dev, steps, warmup):
+    """configs[0]: one 4096×4096 fp32 linear (1 % of input columns ×10), GPTQ W4
+    asym g128, 262144 tokens in batches of 8192."""
+    from g2ptq_amd import GPTQ, WeightQuantizer, make_group_quantizers
+    C, n = 4096, N_TOKENS
+    X, lin = cfg1_inputs(dev)
     w0 = lin.weight.detach().clone()
 
     def step(ev):
@@ -407,66 +418,199 @@ def run_step(acts, layers, w0, n_tokens, ev):
     return hess_ms, quant_ms
 
 
-def cpu_baseline(acts, w0):
-    """The oracle (torch-CPU restatement of the reference arithmetic) on a bounded
-    sample of the benchmark's own inputs (slices of the GPU-generated
-    activations and weights, copied to the host), scaled to one block:
-    Hessians on token slices (cost ∝ N), the factor chain on the C=4096
-    slice Hessian (×6 linears; C=14336 extrapolated by C³), compensation of
-    weight-row slices with that factor (rows are independent: scaled by rows)."""
+def run_step_unchanged(acts, layers, w0, n_tokens, ev):
+    """The same block the way the reference's gptq_fwrd driver (gptq_utils.py:478-563)
+    runs it with only the backend switched: per true-sequential stage, one
+    instance per same-shape chunk (build_chunk_specs), each linear's forward hook
+    feeding its own Hessian (7 Hessians, no shared-input de-duplication), then
+    each instance's own fasterquant."""
+    from g2ptq_amd import GPTQ, WeightQuantizer, build_chunk_specs, make_group_quantizers
+    for name, lin in layers.items():
+        lin.weight.data.copy_(w0[name])
+    stream = torch.cuda.current_stream()
+    hess_ms = quant_ms = 0.0
+    for names in SEQUENTIAL:
+        subset = {n: layers[n] for n in names}
+        insts = []
+        for spec in build_chunk_specs(subset, 64):
+            gq = GPTQ([subset[n] for n in spec.chunk_names])
+            q = WeightQuantizer()
+            q.configure(BITS, perchannel=True, sym=SYM)
+            gq.quantizer = make_group_quantizers(q, spec.columns, GROUPSIZE)
+            insts.append(gq)
+        X = acts[LINEARS[names[0]][2]]
+        C = X.shape[1]
+        e0, e1 = ev()
+        e0.record(stream)
+        step_tok = BSZ * SEQ
+        for t0 in range(0, n_tokens, step_tok):
+            xb = X[t0:t0 + step_tok].view(-1, SEQ, C)
+            for gq in insts:
+                for i in range(gq.num_layers):
+                    gq.add_batch(i, xb, None)
+        for gq in insts:
+            gq.H  # the calibration pass ends: fold the staged tokens
+        e1.record(stream)
+        e2, e3 = ev()
+        e2.record(stream)
+        for gq in insts:
+            gq.fasterquant(blocksize=128, percdamp=0.01, groupsize=GROUPSIZE, actorder=False,
+                           static_groups=False, backend="hip")
+            gq.free()
+        e3.record(stream)
+        torch.cuda.synchronize()
+        hess_ms += e0.elapsed_time(e1)
+        quant_ms += e2.elapsed_time(e3)
+    return hess_ms, quant_ms
+
+
+def unchanged_driver(acts, layers, w0, n_tokens, steps=3, warmup=1):
+    """Seconds per block through run_step_unchanged (mean of ``steps``)."""
+    def ev():
+        return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    for _ in range(warmup):
+        run_step_unchanged(acts, layers, w0, n_tokens, ev)
+    torch.cuda.synchronize()
+    hs, qs = [], []
+    with quiet_collector():
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            h, q = run_step_unchanged(acts, layers, w0, n_tokens, ev)
+            hs.append(h)
+            qs.append(q)
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) / steps
+    flops = sum(2.0 * n_tokens * C * C for _, C, _ in LINEARS.values())
+    h = sum(hs) / steps
+    return {"sec_per_block": round(wall, 4), "steps": steps, "warmup": warmup,
+            "stages_ms": {"hessian": round(h, 2), "factor_and_compensation": round(sum(qs) / steps, 2)},
+            "hessian_tflops_per_linear": round(flops / (h / 1e3) / 1e12, 1),
+            "note": "reference driver layout with only the backend switched: 7 per-linear "
+                    "Hessians, one instance per same-shape chunk, per-instance fasterquant"}
+
+
+def _cpu_threads():
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    cores = len(os.sched_getaffinity(0))
+    cores = min(cores, int(os.environ.get("OMP_NUM_THREADS", cores)))
+    torch.set_num_threads(cores)
+    return cores
+
+
+def _timed_cpu(fn):
+    t = time.perf_counter()
+    out = fn()
+    return out, time.perf_counter() - t
+
+
+def cpu_baseline(acts, w0, dev):
+    """The oracle (torch-CPU restatement of the reference arithmetic) on the
+    benchmark's own inputs, copied to the host, for one block as the reference
+    computes it (7 per-linear Hessians, factors and compensations):
+    Hessians on token slices scaled by N (the cost is ∝ N); every linear's
+    damp + Cholesky chain in full, on the step's Hessians (computed on the GPU
+    over all tokens and copied over); every weight row of every linear's
+    compensation in full."""
+    from g2ptq_amd import GPTQ
     from oracle import compensate as ocomp
     from oracle import factor as ofactor
     from oracle import hessian as ohess
     from oracle import quant as oquant
-    cores = len(os.sched_getaffinity(0))
-    cores = min(cores, int(os.environ.get("OMP_NUM_THREADS", cores)))
-    torch.set_num_threads(cores)
-    t_total = 0.0
+    cores = _cpu_threads()
     parts = {}
-    # Hessians: the reference accumulates one per linear (7): C=4096 ×6, C=14336 ×1.
-    for key, slice_tok, count in (("qkv", 8192, 6), ("down", 2048, 1)):
+    for key, slice_tok in (("qkv", 8192), ("down", 2048)):
         x = acts[key][:slice_tok].cpu().unsqueeze(0)
         C = x.shape[-1]
+        count = sum(1 for _, c, _ in LINEARS.values() if c == C)
         st = ohess.gptq_state(1, C)
-        t = time.perf_counter()
-        ohess.gptq_add_batch(st, 0, x)
-        dt = (time.perf_counter() - t) * (N_TOKENS / slice_tok) * count
-        parts[f"hessian_C{C}"] = dt
-        t_total += dt
-        if C == 4096:
-            H4096 = st["H"][0]
-    # Factor chain (damp, cholesky, cholesky_inverse, cholesky) at C=4096 (6
-    # linears); C=14336 by C³ scaling (estimate).
-    t = time.perf_counter()
-    U, _ = ofactor.damp_chol_inv_upper(H4096, 0.01)
-    dt = time.perf_counter() - t
-    parts["factor_C4096"] = dt * 6
-    parts["factor_C14336_est"] = dt * (14336 / 4096) ** 3
-    t_total += parts["factor_C4096"] + parts["factor_C14336_est"]
-    # Compensation of the real weight rows; rows are independent, so a row
-    # slice scales by rows.  C=14336 reuses the C=4096 factor block-diagonally
-    # (the sweep's cost does not depend on U's values).
-    rows_c4096 = 4096 + 2048 + 4096 + 2 * 14336
-    for name, rslice, rows_total in (("q_proj", 256, rows_c4096), ("down_proj", 64, 4096)):
-        W = w0[name][:rslice].float().cpu().unsqueeze(0)
-        C = W.shape[-1]
-        Uc = U if C == 4096 else torch.block_diag(*([U] * 4))[:C, :C].contiguous()
+        _, dt = _timed_cpu(lambda: ohess.gptq_add_batch(st, 0, x))
+        parts[f"hessian_C{C}_x{count}"] = dt * (N_TOKENS / slice_tok) * count
+    # the step's four distinct Hessians, from the GPU
+    Hs = {}
+    for key, X in acts.items():
+        C = X.shape[1]
+        gq = GPTQ([torch.nn.Linear(C, 1, bias=False, device=dev, dtype=torch.bfloat16)])
+        for t0 in range(0, N_TOKENS, BSZ * SEQ):
+            gq.add_batch(0, X[t0:t0 + BSZ * SEQ].view(-1, SEQ, C), None)
+        Hs[key] = gq.H[0].cpu()
+        gq.free()
+    Us = {}
+    for name, (R, C, key) in LINEARS.items():
+        H = Hs[key].clone()
+        W = w0[name].float().cpu().unsqueeze(0)
+        (U, _), dt = _timed_cpu(lambda: ofactor.damp_chol_inv_upper(H, 0.01))
+        parts[f"factor_{name}"] = dt
         qs = [oquant.WeightQuantizer().configure(BITS, sym=SYM) for _ in range(C // GROUPSIZE)]
-        t = time.perf_counter()
-        ocomp.gptq_compensation(W, Uc.unsqueeze(0), qs, 128, GROUPSIZE, False, None)
-        dt = (time.perf_counter() - t) * rows_total / rslice
-        parts[f"compensation_C{C}"] = dt
-        t_total += dt
-    return {"value": t_total, "unit": "s", "cores": cores, "kind": "port",
-            "cpu": _cpu_model(),
-            "sample": ("oracle (torch-CPU, reference op order) on slices of this run's own "
-                       "inputs: Hessian on 8192 (C=4096) / 2048 (C=14336) tokens scaled by N, "
-                       "7 per-linear Hessians as the reference computes them; "
-                       "damp+chol+cholesky_inverse+chol of the C=4096 slice Hessian x6, "
-                       "C=14336 extrapolated by C^3; compensation of 256/64 weight rows "
-                       "scaled by rows"),
-            "parts_s": {k: round(v, 3) for k, v in parts.items()}}
+        _, dt = _timed_cpu(lambda: ocomp.gptq_compensation(W, U.unsqueeze(0), qs, 128, GROUPSIZE,
+                                                           False, None))
+        parts[f"compensation_{name}"] = dt
+        del U, W
+    total = sum(parts.values())
+    del Hs
+    return {"value": total, "unit": "s", "cores": cores, "kind": "port", "cpu": _cpu_model(),
+            "sample": ("oracle (torch-CPU, reference op order) on this run's own inputs: the 7 "
+                       "per-linear Hessians on 8192 (C=4096) / 2048 (C=14336) token slices "
+                       "scaled by N; every linear's damp+cholesky+cholesky_inverse+cholesky and "
+                       "its whole compensation (every weight row) in full, on the step's "
+                       "Hessians"),
+            "parts_s": {k: round(v, 3) for k, v in parts.items()},
+            "config1": cpu_baseline_config1(dev)}
+
+
+def cpu_baseline_config1(dev):
+    """configs[0] (the reference's CPU-runnable case) on the oracle, in full, on the
+    benchmark's config-1 inputs copied to the host: the Hessian over all 262144
+    tokens, damp + Cholesky chain, compensation of all 4096 rows."""
+    from oracle import compensate as ocomp
+    from oracle import factor as ofactor
+    from oracle import hessian as ohess
+    from oracle import quant as oquant
+    X, lin = cfg1_inputs(dev)
+    Xh = X.cpu()
+    W = lin.weight.detach().cpu().unsqueeze(0)
+    del X, lin
+    torch.cuda.empty_cache()
+    cores = _cpu_threads()
+    C = W.shape[-1]
+    st = ohess.gptq_state(1, C)
+    parts = {}
+    t = time.perf_counter()
+    for t0 in range(0, N_TOKENS, BSZ * SEQ):
+        ohess.gptq_add_batch(st, 0, Xh[t0:t0 + BSZ * SEQ].view(-1, SEQ, C))
+    parts["hessian"] = time.perf_counter() - t
+    del Xh
+    H = st["H"]
+
+    def quantize():
+        ofactor.prepare_hessian(H, W)
+        U, _ = ofactor.damp_chol_inv_upper(H[0], 0.01)
+        qs = [oquant.WeightQuantizer().configure(4, sym=False) for _ in range(C // 128)]
+        ocomp.gptq_compensation(W, U.unsqueeze(0), qs, 128, 128, False, None)
+
+    _, parts["factor_and_compensation"] = _timed_cpu(quantize)
+    return {"value": round(sum(parts.values()), 2), "unit": "s per layer", "cores": cores,
+            "kind": "port", "sample": "the whole of configs[0], nothing scaled",
+            "parts_s": {k: round(v, 2) for k, v in parts.items()}}
+
+
+def config1_gpu(dev, steps=3, warmup=1):
+    """configs[0] on the HIP path: seconds per layer (workload_cfg1, mean of ``steps``)."""
+    step, desc = workload_cfg1(dev, steps, warmup)
+
+    def ev():
+        return [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+
+    for _ in range(warmup):
+        step(ev)
+    torch.cuda.synchronize()
+    with quiet_collector():
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step(ev)
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) / steps
+    return {"workload": desc, "sec_per_layer": round(wall, 4), "steps": steps, "warmup": warmup}
 
 
 def kernel_rates(dev, acts, reps=10):
@@ -675,12 +819,18 @@ def main():
     }
     if not args.no_kernel_rates:
         out["kernels"] = kernel_rates(dev, acts)
+    if not args.no_unchanged_driver:
+        out["unchanged_driver"] = unchanged_driver(acts, layers, w0, args.tokens)
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(acts, w0)
+        out["cpu_baseline"] = cpu_baseline(acts, w0, dev)
     if not args.no_g2ptq:
         del acts, layers, w0
         torch.cuda.empty_cache()
         out["g2ptq_block"] = g2ptq_block(dev)
+    out["config1"] = config1_gpu(dev)
+    if out["cpu_baseline"]:
+        out["config1"]["cpu_over_gpu"] = round(
+            out["cpu_baseline"]["config1"]["value"] / out["config1"]["sec_per_layer"], 1)
     print(json.dumps(out), flush=True)
 
 
