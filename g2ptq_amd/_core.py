@@ -69,18 +69,22 @@ def write_back(layers, Q, flags):
             w.copy_(tmp)
 
 
-def as_bf16_tokens(inp):
-    """Flatten a hook payload to (T, C) bf16 contiguous."""
+def as_tokens(inp):
+    """Flatten a hook payload to (T, C) contiguous and return it with its
+    activation dtype code (0 bf16, 1 fp16, 2 fp32): the reference accepts any
+    float input (``inp.float()``, gptq_utils.py:125).  bf16 is staged as is,
+    fp16 and fp32 as two and three bf16 planes that sum to it exactly; fp64
+    and other types are refused."""
     x = inp if inp.dim() == 2 else inp.reshape(-1, inp.shape[-1])
-    if x.dtype != torch.bfloat16:
+    code = _DTYPE_CODE.get(x.dtype)
+    if code is None:
         raise NotImplementedError(
-            f"Hessian accumulation takes bf16 activations (got {x.dtype}); the path's "
-            "MFMA kernels consume bf16 exactly")
+            f"Hessian accumulation takes bf16, fp16 or fp32 activations (got {x.dtype})")
     if not x.is_contiguous():
         x = x.contiguous()
     if not x.is_cuda:
         raise RuntimeError("Hessian accumulation requires GPU tensors")
-    return x
+    return x, code
 
 
 def hessian_update(H, X, alpha, beta):

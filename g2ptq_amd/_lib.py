@@ -45,6 +45,12 @@ SIGNATURES = {
                              _f32],
     "g2ptq_weighted_gram_workspace": [_i64, _i64, _szp],
     "g2ptq_weighted_gram": [_p, _p, _i64, _i64, _i64, _i64, _f32, _f32, _p, _i64, _i64, _p, _sz],
+    "g2ptq_hessian_stage_planes": [_i32, _i32, _i64, ctypes.POINTER(ctypes.c_int64)],
+    "g2ptq_hessian_stage_ex": [_p, _i32, _i32, _p, _p, _i64, _i64, _i64, _i64, _p, _i64, _i64,
+                               _f32, _p, _i64, _i64, _p, _f32, _f32],
+    "g2ptq_hessian_gram_ex_workspace": [_i32, _i32, _i64, _i64, _i64, _szp],
+    "g2ptq_hessian_gram_ex": [_p, _i32, _i32, _p, _i64, _i64, _i64, _i64, _f32, _f32, _p, _i64,
+                              _i64, _p, _i64, _p, _sz],
     "g2ptq_prepare_hessian": [_p, _p, _i64, _i64, _p, _i64, _p, _p, _i64, _p, _sz],
     "g2ptq_factor_workspace": [_i64, _i64, _szp],
     "g2ptq_inv_chol_upper": [_p, _p, _i64, _i64, _f32, _p, _p, _p, _p, _sz],

@@ -16,6 +16,10 @@ long K runs.
 
 Planes per kind: 0 (GPTQ) Xᵀ; 1 (GPTAQ) Xᵀ and the bf16 hi/lo parts of
 (X_fp − X)ᵀ; 2 (weighted, G groups) Xᵀ and the hi/lo parts of (x·s[t,g])ᵀ.
+Activations that are not bf16 take P bf16 planes for Xᵀ that sum to it
+exactly (fp16: 2, fp32: 3; the reference's ``inp.float()``,
+gptq_utils.py:125): every Gram product then runs once per plane of its
+column operand (four, resp. nine times the bf16 Gram work for GPTQ).
 
 The first buffer holds 32 batches of the first batch's size (at least 65536
 tokens): a calibration run is typically 32 or more batches, so its whole set
@@ -58,6 +62,10 @@ KIND_GPTQ, KIND_GPTAQ, KIND_WEIGHTED = 0, 1, 2
 _GRAM_WS = {KIND_GPTQ: "g2ptq_hessian_gram_workspace",
             KIND_GPTAQ: "g2ptq_gptaq_gram_workspace",
             KIND_WEIGHTED: "g2ptq_weighted_gram_workspace"}
+# activation dtype codes of the any-dtype entry points, and the bf16 planes
+# each stages for Xᵀ
+DTYPE_BF16, DTYPE_F16, DTYPE_F32 = 0, 1, 2
+_X_PLANES = {DTYPE_BF16: 1, DTYPE_F16: 2, DTYPE_F32: 3}
 
 
 def _ceil(x, m):
@@ -77,12 +85,15 @@ def _device_memory(device):
 
 
 class GramStager:
-    def __init__(self, columns, device, kind=KIND_GPTQ, groups=0, budget_bytes=None):
+    def __init__(self, columns, device, kind=KIND_GPTQ, groups=0, budget_bytes=None,
+                 dtype=DTYPE_BF16):
         self.C = columns
         self.device = device
         self.kind = kind
         self.G = groups
-        self.planes = {KIND_GPTQ: 1, KIND_GPTAQ: 3, KIND_WEIGHTED: 1 + 2 * groups}[kind]
+        self.dtype = dtype
+        P = _X_PLANES[dtype]
+        self.planes = P + {KIND_GPTQ: 0, KIND_GPTAQ: 2, KIND_WEIGHTED: 2 * groups}[kind]
         self.rows = _lib.query_size_i64("g2ptq_hessian_stage_rows", columns)
         budget = budget_bytes if budget_bytes is not None else DEFAULT_BUDGET
         if budget is None:
@@ -136,7 +147,12 @@ class GramStager:
         saliencies, their scale and the act-square update for the weighted kind."""
         T, C = X.shape
         st, xt = _lib.stream_ptr(), _lib.ptr(self.buf)
-        if self.kind == KIND_GPTQ:
+        if self.dtype != DTYPE_BF16:
+            _lib.call("g2ptq_hessian_stage_ex", st, self.kind, self.dtype, _lib.ptr(X),
+                      _lib.ptr(Xfp), T, C, C, C, _lib.ptr(S), self.G,
+                      S.stride(0) if S is not None else 0, float(s_scale), xt, self.cap, self.k,
+                      _lib.ptr(act), float(act_alpha), float(act_beta))
+        elif self.kind == KIND_GPTQ:
             fast = _lib.fastcall()
             if fast is None:
                 _lib.call("g2ptq_hessian_stage", st, _lib.ptr(X), T, C, C, xt, self.cap, self.k)
@@ -161,14 +177,24 @@ class GramStager:
         if not H.is_cuda or (Dx is not None and not Dx.is_cuda):
             raise RuntimeError("staged Hessian tokens need the Hessian on the GPU: call "
                                "add_batch inside the onload context of the Hessian")
-        nbytes = _lib.query_size(_GRAM_WS[self.kind], self.k, self.C)
+        if self.dtype != DTYPE_BF16:
+            nbytes = _lib.query_size("g2ptq_hessian_gram_ex_workspace", self.kind, self.dtype,
+                                     self.k, self.C, self.G)
+        else:
+            nbytes = _lib.query_size(_GRAM_WS[self.kind], self.k, self.C)
         ws = _lib.workspace(nbytes, self.buf.device)
         if TIMING is not None:
             e0 = torch.cuda.Event(enable_timing=True)
             e1 = torch.cuda.Event(enable_timing=True)
             e0.record()
         st, xt, C = _lib.stream_ptr(), _lib.ptr(self.buf), self.C
-        if self.kind == KIND_GPTQ:
+        if self.dtype != DTYPE_BF16:
+            _lib.call("g2ptq_hessian_gram_ex", st, self.kind, self.dtype, xt, self.cap, self.k, C,
+                      self.G, float(alpha), float(beta), _lib.ptr(H), C, C * C, _lib.ptr(Dx), C,
+                      _lib.ptr(ws), ws.numel())
+            flops = 2.0 * self.k * C * C * {KIND_GPTQ: 1, KIND_GPTAQ: 2,
+                                            KIND_WEIGHTED: self.G}[self.kind]
+        elif self.kind == KIND_GPTQ:
             _lib.call("g2ptq_hessian_gram", st, xt, self.cap, self.k, C, float(alpha),
                       float(beta), _lib.ptr(H), C, _lib.ptr(ws), ws.numel())
             flops = 2.0 * self.k * C * C
@@ -189,6 +215,30 @@ class GramStager:
         self.buf = None
         self.cap = 0
         self.k = 0
+
+
+def stager_for(owner, idx, device, kind, groups, dtype):
+    """Layer ``idx``'s stager for batches of activation ``dtype``.  A stager
+    holding tokens of another dtype is folded into the Hessian first and
+    replaced (the running averages hold across any flush point)."""
+    st = owner._stagers[idx]
+    if st is not None and st.dtype != dtype:
+        owner._flush_staged(idx)
+        st.release()
+        st = None
+    if st is None:
+        st = owner._stagers[idx] = GramStager(owner.columns, device, kind, groups, dtype=dtype)
+    return st
+
+
+def single_batch_stager(columns, device, kind, groups, dtype, T):
+    """A stager holding exactly one batch of T tokens: the path of a batch
+    larger than the staging budget for activations without a one-shot
+    update entry point (fp16, fp32)."""
+    st = GramStager(columns, device, kind, groups, dtype=dtype)
+    st.max_tokens = _ceil(_ceil(T, 64) + _GRAM_PAD, _GRAM_PAD)
+    st.reserve(T)
+    return st
 
 
 def lazy_counter(name):

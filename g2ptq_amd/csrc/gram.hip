@@ -182,12 +182,114 @@ __global__ __launch_bounds__(256) void stage_kernel(StageArgs s) {
   }
 }
 
+// Activations that are not bf16 (fp16: P = 2, fp32: P = 3) are staged as P
+// bf16 planes whose sum is the value exactly: plane q holds bf16(r_q) with
+// r_0 = x and r_{q+1} = r_q − bf16(r_q), each difference exact in fp32 (x and
+// its nearest bf16 are within a factor of two).  An fp16 value (11
+// significant bits) leaves at most 3 bits after its first plane; an fp32
+// value (24) leaves at most 16, then 8.  Planes 0..P−1 then play the part of
+// the bf16 path's Xᵀ, and the GPTAQ / weighted planes follow at P, P + 1, ….
+template <typename TIN>
+__device__ __forceinline__ void load_block_f32(const TIN* __restrict__ X, int64_t ldx, int64_t T,
+                                               int64_t C, int64_t t0, int64_t f0, int vec,
+                                               float (&v)[8][8]) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int64_t t = t0 + i;
+    if (t < T && vec && f0 + 8 <= C) {
+      const TIN* row = X + t * ldx + f0;
+      if constexpr (sizeof(TIN) == 2) {
+        const uint4 u = *reinterpret_cast<const uint4*>(row);
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          v[i][2 * k] = (float)__builtin_bit_cast(_Float16, (unsigned short)(w[k] & 0xffffu));
+          v[i][2 * k + 1] = (float)__builtin_bit_cast(_Float16, (unsigned short)(w[k] >> 16));
+        }
+      } else {
+        const float4 a = *reinterpret_cast<const float4*>(row);
+        const float4 b = *reinterpret_cast<const float4*>(row + 4);
+        v[i][0] = a.x; v[i][1] = a.y; v[i][2] = a.z; v[i][3] = a.w;
+        v[i][4] = b.x; v[i][5] = b.y; v[i][6] = b.z; v[i][7] = b.w;
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        v[i][k] = (t < T && f0 + k < C) ? (float)X[t * ldx + f0 + k] : 0.f;
+    }
+  }
+}
+
+template <typename TIN, int KIND>
+__global__ __launch_bounds__(256) void stage_split_kernel(StageArgs s) {
+  constexpr int P = sizeof(TIN) == 2 ? 2 : 3;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int tb = lane >> 3, fb = lane & 7;
+  const int64_t t0 = (int64_t)blockIdx.x * ST_T + tb * 8;
+  const int64_t f0 = (int64_t)blockIdx.y * ST_C + wave * 64 + fb * 8;
+  float v[8][8];
+  load_block_f32(reinterpret_cast<const TIN*>(s.X), s.ldx, s.T, s.C, t0, f0, s.vec, v);
+  if (t0 >= s.t_end) return;  // t_end is a multiple of 8
+  const int64_t col = s.t_off + t0;
+  {
+    float r[8][8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int k = 0; k < 8; ++k) r[i][k] = v[i][k];
+#pragma unroll
+    for (int q = 0; q < P; ++q) {
+      uint32_t w[8][4];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint32_t h0 = f32_to_bf16_rne(r[i][2 * k]);
+          const uint32_t h1 = f32_to_bf16_rne(r[i][2 * k + 1]);
+          w[i][k] = h0 | (h1 << 16);
+          r[i][2 * k] -= __uint_as_float(h0 << 16);
+          r[i][2 * k + 1] -= __uint_as_float(h1 << 16);
+        }
+      store_block(s.XT + q * s.plane, s.ldt, f0, col, w);
+    }
+  }
+  if (KIND == 1) {
+    float f[8][8];
+    load_block_f32(reinterpret_cast<const TIN*>(s.F), s.ldf, s.T, s.C, t0, f0, s.vec, f);
+    uint32_t h[8][4], l[8][4];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        split2(f[i][2 * k] - v[i][2 * k], f[i][2 * k + 1] - v[i][2 * k + 1], h[i][k], l[i][k]);
+    store_block(s.XT + P * s.plane, s.ldt, f0, col, h);
+    store_block(s.XT + (P + 1) * s.plane, s.ldt, f0, col, l);
+  }
+  if (KIND == 2) {
+    for (int g = 0; g < s.G; ++g) {
+      float sv[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        sv[i] = (t0 + i < s.T) ? s.S[(t0 + i) * s.lds + g] * s.s_scale : 0.f;
+      uint32_t h[8][4], l[8][4];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          split2(v[i][2 * k] * sv[i], v[i][2 * k + 1] * sv[i], h[i][k], l[i][k]);
+      store_block(s.XT + (P + 2 * g) * s.plane, s.ldt, f0, col, h);
+      store_block(s.XT + (P + 2 * g + 1) * s.plane, s.ldt, f0, col, l);
+    }
+  }
+}
+
 // act = act_beta·act + act_alpha·Σ_t x[t,c]² over tokens [t0, t0 + len) of
-// the staged Xᵀ (one wave per feature, 16-byte loads; len a multiple of 8).
+// the staged Xᵀ (one wave per feature, 16-byte loads; len a multiple of 8);
+// x is the sum of the P staged planes (exact, see stage_split_kernel).
 __global__ __launch_bounds__(256) void act_square_kernel(const uint16_t* __restrict__ XT,
                                                          int64_t ldt, int64_t t0, int64_t len,
                                                          int64_t C, float* act, float act_alpha,
-                                                         float act_beta) {
+                                                         float act_beta, int P, int64_t plane) {
   const int64_t c = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (c >= C) return;
@@ -196,11 +298,25 @@ __global__ __launch_bounds__(256) void act_square_kernel(const uint16_t* __restr
   for (int64_t t = (int64_t)lane * 8; t < len; t += 512) {
     const uint4 v = *reinterpret_cast<const uint4*>(row + t);
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    float x[8];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const float a = lo_f32(w[k]), b = hi_f32(w[k]);
-      s += a * a;
-      s += b * b;
+      x[2 * k] = lo_f32(w[k]);
+      x[2 * k + 1] = hi_f32(w[k]);
+    }
+    for (int q = 1; q < P; ++q) {
+      const uint4 u = *reinterpret_cast<const uint4*>(row + q * plane + t);
+      const uint32_t wq[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        x[2 * k] += lo_f32(wq[k]);
+        x[2 * k + 1] += hi_f32(wq[k]);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      s += x[2 * k] * x[2 * k];
+      s += x[2 * k + 1] * x[2 * k + 1];
     }
   }
 #pragma unroll
@@ -219,8 +335,9 @@ __global__ void zero_cols_bf16_kernel(uint16_t* XT, int64_t ldt, int64_t rows, i
 }
 
 struct G2Args {
-  const uint16_t* A1;  // row operand planes (Cp × ldt); A2 feeds the second
-  const uint16_t* A2;  // half of the splits when halves == 2
+  const uint16_t* A1;  // row operand planes (Cp × ldt): A2 feeds the second and
+  const uint16_t* A2;  // A3 the third part of the splits when halves is 2 or 3
+  const uint16_t* A3;
   const uint16_t* B;   // column operand plane
   int64_t ldt;
   int64_t kc;      // tokens per split (an even number of KS stages)
@@ -319,7 +436,7 @@ __global__ __launch_bounds__(NTH) void gram256_kernel(G2Args a) {
   // Split → operand plane and token range.
   const int per_half = a.S / a.halves;
   const int half = split / per_half, sp = split - half * per_half;
-  const uint16_t* Aop = half ? a.A2 : a.A1;
+  const uint16_t* Aop = half == 0 ? a.A1 : (half == 1 ? a.A2 : a.A3);
   const uint16_t* Ag = Aop + (I * TT) * a.ldt + (int64_t)sp * a.kc;
   const uint16_t* Bg = a.B + (J * TT) * a.ldt + (int64_t)sp * a.kc;
 
@@ -656,7 +773,7 @@ size_t plan_ws_bytes(int64_t tiles, const GramPlan& p) {
   return p.S == 1 ? 256 : (size_t)tiles * p.S * TT * TT * sizeof(float);
 }
 
-// The three products, as (full, halves).
+// The products, as (full, halves).
 struct Product {
   bool full;
   int halves;
@@ -664,6 +781,14 @@ struct Product {
 constexpr Product SYM1{false, 1};  // H from Xᵀ
 constexpr Product SYM2{false, 2};  // weighted H[g] from (hi_g, lo_g) against Xᵀ
 constexpr Product FULL2{true, 2};  // GPTAQ Dx from (hi, lo) against Xᵀ
+
+// Staged bf16 planes of one activation: 1 for bf16, 2 for fp16, 3 for fp32
+// (dtype codes 0, 1, 2).  With P > 1 every product runs once per plane q of
+// the column operand (Σ_q planes = X), accumulating into the output, and the
+// plain Hessian's row operand is all P planes (halves = P): H = Σ_q XᵀX_q.
+// Each run computes upper tiles only, which is exact for the symmetric sum.
+int dtype_planes(int dtype) { return dtype == 0 ? 1 : dtype == 1 ? 2 : 3; }
+Product x_product(int P) { return Product{false, P}; }
 
 size_t product_ws(int64_t K, int64_t C, Product pr) {
   const int64_t tiles = n_tiles(C, pr.full);
@@ -674,18 +799,21 @@ int64_t product_width(int64_t K, int64_t C, Product pr) {
   return gram_plan(n_tiles(C, pr.full), K, pr.halves).Kp;
 }
 
-// Planes staged per kind (0 Hessian, 1 GPTAQ, 2 weighted with G groups).
-int64_t kind_planes(int kind, int64_t G) { return kind == 0 ? 1 : kind == 1 ? 3 : 1 + 2 * G; }
+// Planes staged per kind (0 Hessian, 1 GPTAQ, 2 weighted with G groups) for
+// an activation of P planes.
+int64_t kind_planes(int kind, int64_t G, int P = 1) {
+  return P + (kind == 1 ? 2 : kind == 2 ? 2 * G : 0);
+}
 
 // Staged token width and Gram workspace a kind needs for K tokens.
-int64_t kind_width(int kind, int64_t K, int64_t C) {
-  if (kind == 0) return product_width(K, C, SYM1);
-  if (kind == 1) return std::max(product_width(K, C, SYM1), product_width(K, C, FULL2));
+int64_t kind_width(int kind, int64_t K, int64_t C, int P = 1) {
+  if (kind == 0) return product_width(K, C, x_product(P));
+  if (kind == 1) return std::max(product_width(K, C, x_product(P)), product_width(K, C, FULL2));
   return product_width(K, C, SYM2);
 }
-size_t kind_gram_ws(int kind, int64_t K, int64_t C) {
-  if (kind == 0) return product_ws(K, C, SYM1);
-  if (kind == 1) return std::max(product_ws(K, C, SYM1), product_ws(K, C, FULL2));
+size_t kind_gram_ws(int kind, int64_t K, int64_t C, int P = 1) {
+  if (kind == 0) return product_ws(K, C, x_product(P));
+  if (kind == 1) return std::max(product_ws(K, C, x_product(P)), product_ws(K, C, FULL2));
   return product_ws(K, C, SYM2);
 }
 
@@ -703,8 +831,8 @@ int zero_pad(hipStream_t st, uint16_t* XT, int64_t ldt, int64_t rows, int64_t K,
 // out = beta·out + alpha·(product over K staged tokens).  The staged planes
 // must be zero from token roundup(K, 64) up to product_width(K, C, pr).
 int run_product(hipStream_t st, Product pr, const uint16_t* A1, const uint16_t* A2,
-                const uint16_t* B, int64_t ldt, int64_t K, int64_t C, float alpha, float beta,
-                float* out, int64_t ldo, void* ws, size_t ws_bytes) {
+                const uint16_t* A3, const uint16_t* B, int64_t ldt, int64_t K, int64_t C,
+                float alpha, float beta, float* out, int64_t ldo, void* ws, size_t ws_bytes) {
   const int64_t nt = cdiv(C, TT);
   const int64_t tiles = n_tiles(C, pr.full);
   const GramPlan p = gram_plan(tiles, K, pr.halves);
@@ -712,7 +840,7 @@ int run_product(hipStream_t st, Product pr, const uint16_t* A1, const uint16_t* 
               (long long)ldt, (long long)p.Kp);
   G2PTQ_CHECK(tiles * p.S < (1ll << 31) && tiles < 65536, "hessian gram: grid too large");
   G2Args a{};
-  a.A1 = A1; a.A2 = A2; a.B = B; a.ldt = ldt; a.kc = p.kc; a.nt = nt; a.tiles = tiles; a.C = C;
+  a.A1 = A1; a.A2 = A2; a.A3 = A3; a.B = B; a.ldt = ldt; a.kc = p.kc; a.nt = nt; a.tiles = tiles; a.C = C;
   a.S = p.S; a.halves = pr.halves; a.alpha = alpha; a.beta = beta; a.H = out; a.ldh = ldo;
   if (p.S > 1) {
     const size_t need = plan_ws_bytes(tiles, p);
@@ -744,7 +872,7 @@ int64_t padded_features(int64_t C) { return cdiv(C, TT) * TT; }
 
 int stage(hipStream_t st, int kind, const uint16_t* X, const uint16_t* F, const float* S,
           int64_t T, int64_t C, int64_t ldx, int64_t ldf, int64_t G, int64_t lds, float s_scale,
-          uint16_t* XT, int64_t ldt, int64_t t_off) {
+          uint16_t* XT, int64_t ldt, int64_t t_off, int dtype = 0) {
   if (T <= 0) return G2PTQ_OK;
   G2PTQ_CHECK(C > 0 && C <= (1ll << 20), "hessian stage: bad feature count %lld", (long long)C);
   G2PTQ_CHECK(ldt % 8 == 0 && t_off % 64 == 0 && (reinterpret_cast<uintptr_t>(XT) & 15) == 0,
@@ -756,25 +884,36 @@ int stage(hipStream_t st, int kind, const uint16_t* X, const uint16_t* F, const 
   auto aligned = [](const void* p, int64_t ld) {
     return ld % 8 == 0 && (reinterpret_cast<uintptr_t>(p) & 15) == 0;
   };
+  G2PTQ_CHECK(dtype >= 0 && dtype <= 2, "hessian stage: dtype code %d unsupported", dtype);
   StageArgs s{};
   s.X = X; s.F = F; s.S = S; s.T = T; s.C = C; s.ldx = ldx; s.ldf = ldf; s.lds = lds;
   s.G = (int)G; s.s_scale = s_scale; s.XT = XT; s.ldt = ldt; s.plane = Cp * ldt; s.t_off = t_off;
   s.t_end = cdiv(T, KS) * KS;
   s.vec = aligned(X, ldx) && (kind != 1 || aligned(F, ldf));
   const dim3 grid((unsigned)cdiv(T, (int64_t)ST_T), (unsigned)(Cp / ST_C));
-  if (kind == 0) hipLaunchKernelGGL(stage_kernel<0>, grid, dim3(256), 0, st, s);
-  else if (kind == 1) hipLaunchKernelGGL(stage_kernel<1>, grid, dim3(256), 0, st, s);
-  else hipLaunchKernelGGL(stage_kernel<2>, grid, dim3(256), 0, st, s);
+  if (dtype == 0) {
+    if (kind == 0) hipLaunchKernelGGL(stage_kernel<0>, grid, dim3(256), 0, st, s);
+    else if (kind == 1) hipLaunchKernelGGL(stage_kernel<1>, grid, dim3(256), 0, st, s);
+    else hipLaunchKernelGGL(stage_kernel<2>, grid, dim3(256), 0, st, s);
+  } else if (dtype == 1) {
+    if (kind == 0) hipLaunchKernelGGL((stage_split_kernel<_Float16, 0>), grid, dim3(256), 0, st, s);
+    else if (kind == 1) hipLaunchKernelGGL((stage_split_kernel<_Float16, 1>), grid, dim3(256), 0, st, s);
+    else hipLaunchKernelGGL((stage_split_kernel<_Float16, 2>), grid, dim3(256), 0, st, s);
+  } else {
+    if (kind == 0) hipLaunchKernelGGL((stage_split_kernel<float, 0>), grid, dim3(256), 0, st, s);
+    else if (kind == 1) hipLaunchKernelGGL((stage_split_kernel<float, 1>), grid, dim3(256), 0, st, s);
+    else hipLaunchKernelGGL((stage_split_kernel<float, 2>), grid, dim3(256), 0, st, s);
+  }
   G2PTQ_LAUNCHED();
   return G2PTQ_OK;
 }
 
 int act_square(hipStream_t st, const uint16_t* XT, int64_t ldt, int64_t t_off, int64_t T, int64_t C,
-               float* act, float act_alpha, float act_beta) {
+               float* act, float act_alpha, float act_beta, int P = 1) {
   if (!act) return G2PTQ_OK;
   const int64_t len = cdiv(std::max<int64_t>(T, 0), KS) * KS;
   hipLaunchKernelGGL(act_square_kernel, dim3((unsigned)cdiv(C, 4)), dim3(256), 0, st, XT, ldt,
-                     t_off, len, C, act, act_alpha, act_beta);
+                     t_off, len, C, act, act_alpha, act_beta, P, padded_features(C) * ldt);
   G2PTQ_LAUNCHED();
   return G2PTQ_OK;
 }
@@ -789,33 +928,40 @@ int check_gram_args(const uint16_t* XT, int64_t ldt, int64_t K, int64_t C) {
 // The Gram products of each kind over K tokens staged in XT (planes of Cp × ldt).
 int gram_kind(hipStream_t st, int kind, uint16_t* XT, int64_t ldt, int64_t K, int64_t C, int64_t G,
               float alpha, float beta, float* H, int64_t ldh, int64_t sH, float* Dx, int64_t ldd,
-              void* ws, size_t ws_bytes) {
+              void* ws, size_t ws_bytes, int P = 1) {
   G2PTQ_TRY(check_gram_args(XT, ldt, K, C));
   const int64_t Cp = padded_features(C);
   const int64_t plane = Cp * ldt;
-  const int64_t width = kind_width(kind, K, C);
+  const int64_t width = kind_width(kind, K, C, P);
   G2PTQ_CHECK(width <= ldt, "hessian gram: staged operand too narrow (%lld < %lld)",
               (long long)ldt, (long long)width);
-  G2PTQ_TRY(zero_pad(st, XT, ldt, kind_planes(kind, G) * Cp, K, width));
-  if (kind == 0)
-    return run_product(st, SYM1, XT, nullptr, XT, ldt, K, C, alpha, beta, H, ldh, ws, ws_bytes);
-  if (kind == 1) {
-    G2PTQ_TRY(run_product(st, SYM1, XT, nullptr, XT, ldt, K, C, alpha, beta, H, ldh, ws,
-                          ws_bytes));
-    return run_product(st, FULL2, XT + plane, XT + 2 * plane, XT, ldt, K, C, alpha, beta, Dx, ldd,
-                       ws, ws_bytes);
+  G2PTQ_TRY(zero_pad(st, XT, ldt, kind_planes(kind, G, P) * Cp, K, width));
+  const uint16_t* Xq[3] = {XT, XT + plane, XT + 2 * plane};
+  // every product over the column planes q = 0..P−1: the first applies beta,
+  // the others add to it
+  for (int q = 0; q < P; ++q) {
+    const float b = q == 0 ? beta : 1.f;
+    if (kind != 2)
+      G2PTQ_TRY(run_product(st, x_product(P), Xq[0], P > 1 ? Xq[1] : nullptr,
+                            P > 2 ? Xq[2] : nullptr, Xq[q], ldt, K, C, alpha, b, H, ldh, ws,
+                            ws_bytes));
+    if (kind == 1)
+      G2PTQ_TRY(run_product(st, FULL2, XT + P * plane, XT + (P + 1) * plane, nullptr, Xq[q], ldt,
+                            K, C, alpha, b, Dx, ldd, ws, ws_bytes));
+    if (kind == 2)
+      for (int64_t g = 0; g < G; ++g)
+        G2PTQ_TRY(run_product(st, SYM2, XT + (P + 2 * g) * plane, XT + (P + 2 * g + 1) * plane,
+                              nullptr, Xq[q], ldt, K, C, alpha, b, H + g * sH, ldh, ws,
+                              ws_bytes));
   }
-  for (int64_t g = 0; g < G; ++g)
-    G2PTQ_TRY(run_product(st, SYM2, XT + (1 + 2 * g) * plane, XT + (2 + 2 * g) * plane, XT, ldt, K,
-                          C, alpha, beta, H + g * sH, ldh, ws, ws_bytes));
   return G2PTQ_OK;
 }
 
 // One-shot updates (stage + Gram) through a caller workspace laid out as
 // [staged planes: planes × Cp × width bf16][split partials].
-size_t staged_bytes(int kind, int64_t T, int64_t C, int64_t G) {
-  return ((size_t)kind_planes(kind, G) * padded_features(C) * kind_width(kind, T, C) * 2 + 255) /
-         256 * 256;
+size_t staged_bytes(int kind, int64_t T, int64_t C, int64_t G, int P = 1) {
+  return ((size_t)kind_planes(kind, G, P) * padded_features(C) * kind_width(kind, T, C, P) * 2 +
+          255) / 256 * 256;
 }
 size_t update_ws_bytes(int kind, int64_t T, int64_t C, int64_t G) {
   return staged_bytes(kind, T, C, G) + kind_gram_ws(kind, T, C);
@@ -962,4 +1108,53 @@ extern "C" int g2ptq_weighted_gram(void* stream, uint16_t* XT, int64_t ldt, int6
   G2PTQ_CHECK(G >= 1 && G <= 64 && H, "weighted_gram: bad arguments");
   return gram_kind(as_stream(stream), 2, XT, ldt, K, C, G, alpha, beta, H, ldh, sH, nullptr, 0, ws,
                    ws_bytes);
+}
+
+// Any-dtype staging (bf16, fp16, fp32 activations; dtype codes 0, 1, 2): the
+// staged planes of a kind, the stage, the Gram products and their workspace.
+extern "C" int g2ptq_hessian_stage_planes(int kind, int dtype, int64_t G, int64_t* planes) {
+  G2PTQ_CHECK(planes != nullptr && kind >= 0 && kind <= 2 && dtype >= 0 && dtype <= 2 &&
+                  (kind != 2 || (G >= 1 && G <= 64)),
+              "hessian_stage_planes: bad arguments");
+  *planes = kind_planes(kind, G, dtype_planes(dtype));
+  return G2PTQ_OK;
+}
+
+extern "C" int g2ptq_hessian_stage_ex(void* stream, int kind, int dtype, const void* X,
+                                      const void* Xfp, int64_t T, int64_t C, int64_t ldx,
+                                      int64_t ldxf, const float* S, int64_t G, int64_t lds,
+                                      float s_scale, uint16_t* XT, int64_t ldt, int64_t t_off,
+                                      float* act, float act_alpha, float act_beta) {
+  G2PTQ_CHECK(kind >= 0 && kind <= 2 && dtype >= 0 && dtype <= 2,
+              "hessian_stage_ex: kind %d / dtype %d unsupported", kind, dtype);
+  G2PTQ_CHECK(kind != 2 || (G >= 1 && G <= 64), "hessian_stage_ex: G=%lld unsupported",
+              (long long)G);
+  G2PTQ_CHECK(XT && (T == 0 || (X && (kind != 1 || Xfp) && (kind != 2 || S))) && C > 0 && T >= 0,
+              "hessian_stage_ex: bad arguments");
+  hipStream_t st = as_stream(stream);
+  G2PTQ_TRY(stage(st, kind, static_cast<const uint16_t*>(X), static_cast<const uint16_t*>(Xfp), S,
+                  T, C, ldx, ldxf, G, lds, s_scale, XT, ldt, t_off, dtype));
+  if (kind == 2)
+    return act_square(st, XT, ldt, t_off, T, C, act, act_alpha, act_beta, dtype_planes(dtype));
+  return G2PTQ_OK;
+}
+
+extern "C" int g2ptq_hessian_gram_ex_workspace(int kind, int dtype, int64_t K, int64_t C,
+                                               int64_t G, size_t* bytes) {
+  G2PTQ_CHECK(bytes != nullptr && kind >= 0 && kind <= 2 && dtype >= 0 && dtype <= 2 && C > 0 &&
+                  K >= 0,
+              "hessian_gram_ex_workspace: bad arguments");
+  *bytes = kind_gram_ws(kind, K, C, dtype_planes(dtype));
+  return G2PTQ_OK;
+}
+
+extern "C" int g2ptq_hessian_gram_ex(void* stream, int kind, int dtype, uint16_t* XT, int64_t ldt,
+                                     int64_t K, int64_t C, int64_t G, float alpha, float beta,
+                                     float* H, int64_t ldh, int64_t sH, float* Dx, int64_t ldd,
+                                     void* ws, size_t ws_bytes) {
+  G2PTQ_CHECK(kind >= 0 && kind <= 2 && dtype >= 0 && dtype <= 2 && H &&
+                  (kind != 1 || Dx) && (kind != 2 || (G >= 1 && G <= 64)),
+              "hessian_gram_ex: bad arguments");
+  return gram_kind(as_stream(stream), kind, XT, ldt, K, C, G, alpha, beta, H, ldh, sH, Dx, ldd, ws,
+                   ws_bytes, dtype_planes(dtype));
 }

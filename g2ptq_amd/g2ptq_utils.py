@@ -14,7 +14,8 @@ import torch
 
 from . import _core, _lib
 from .common_utils import fake_quantize_grouped
-from ._stage import KIND_WEIGHTED, GramStager, bump, lazy_counter, staged_attr
+from ._stage import (KIND_WEIGHTED, bump, lazy_counter, single_batch_stager, staged_attr,
+                     stager_for)
 from .compressed_tensors_utils import compress_layers
 from .gptq_utils import _compensate
 from .graph_utils import run_graph, validate_tensors
@@ -103,7 +104,7 @@ class G2PTQ:
     @torch.no_grad()
     def add_batch(self, idx, inp, out):
         """g2ptq_utils.py:182-201: H[g] ← H[g]·k/(k+1) + Σ_t s_tg x xᵀ / (T·(k+1))."""
-        X = _core.as_bf16_tokens(inp)
+        X, dt = _core.as_tokens(inp)
         n_tokens = X.shape[0]
         sal = self.saliencies[idx][0].to(self.dev).float()
         del self.saliencies[idx][0]
@@ -115,10 +116,7 @@ class G2PTQ:
         tt += n_tokens
         self._tt[idx] = tt
         act_alpha = _core.f32(1 / tt)
-        st = self._stagers[idx]
-        if st is None:
-            st = self._stagers[idx] = GramStager(self.columns, X.device, KIND_WEIGHTED,
-                                                 self.num_groups)
+        st = stager_for(self, idx, X.device, KIND_WEIGHTED, self.num_groups, dt)
         if not st.fits(n_tokens):
             self._flush_staged(idx)
             if st.can_stage(n_tokens):
@@ -130,8 +128,16 @@ class G2PTQ:
         else:
             # a batch larger than the staging budget: update directly
             k0 = self._k_flushed[idx]
-            _core.weighted_update(self._H[idx], X, sal, _core.f32(1 / (n_tokens * k)),
-                                  _core.f32(k0 / k), self.act_square[idx], act_alpha, act_beta)
+            if dt == 0:
+                _core.weighted_update(self._H[idx], X, sal, _core.f32(1 / (n_tokens * k)),
+                                      _core.f32(k0 / k), self.act_square[idx], act_alpha,
+                                      act_beta)
+            else:
+                one = single_batch_stager(self.columns, X.device, KIND_WEIGHTED,
+                                          self.num_groups, dt, n_tokens)
+                one.stage(X, S=sal, s_scale=_core.f32(1 / n_tokens), act=self.act_square[idx],
+                          act_alpha=act_alpha, act_beta=act_beta)
+                one.flush(self._H[idx], _core.f32(1 / k), _core.f32(k0 / k))
             self._k_flushed[idx] = k
         self._k[idx] = k
         bump(self, "index", idx, 1)

@@ -9,7 +9,8 @@ block, ``+Q·P`` in the block tail) run in libg2ptq_hip.so.
 import torch
 
 from . import _core, _lib
-from ._stage import KIND_GPTAQ, GramStager, bump, lazy_counter, staged_attr
+from ._stage import (KIND_GPTAQ, bump, lazy_counter, single_batch_stager, staged_attr,
+                     stager_for)
 from .compressed_tensors_utils import compress_layers
 from .gptq_utils import _compensate
 from .graph_utils import run_graph, validate_tensors
@@ -74,14 +75,12 @@ class GPTAQ:
         H and dXXT ← ·n/(n+t) + (2/(n+t))·(XᵀX, (X_fp − X)ᵀX), staged."""
         fp = self.fp_inp[idx][0].to(inp.device, non_blocking=True)
         tmp = 1 if inp.dim() == 2 else inp.shape[0]  # a 2-D input is one sequence
-        X = _core.as_bf16_tokens(inp)
-        Xfp = _core.as_bf16_tokens(fp.to(inp.dtype))
+        X, dt = _core.as_tokens(inp)
+        Xfp, _ = _core.as_tokens(fp.to(inp.dtype))  # the reference's fp_inp.to(inp)
         if Xfp.shape != X.shape:
             raise ValueError(f"fp_inp shape {tuple(Xfp.shape)} != input {tuple(X.shape)}")
         T = X.shape[0]
-        st = self._stagers[idx]
-        if st is None:
-            st = self._stagers[idx] = GramStager(self.columns, X.device, KIND_GPTAQ)
+        st = stager_for(self, idx, X.device, KIND_GPTAQ, 0, dt)
         if not st.fits(T):
             self._flush_staged(idx)
             if st.can_stage(T):
@@ -92,8 +91,14 @@ class GPTAQ:
         else:
             # a batch larger than the staging budget: update directly
             n0 = self._n_flushed[idx]
-            _core.gptaq_update(self._H[idx], self._dXXT[idx], X, Xfp, _core.sqrt_scale_sq(n),
-                               _core.f32(n0 / n))
+            if dt == 0:
+                _core.gptaq_update(self._H[idx], self._dXXT[idx], X, Xfp, _core.sqrt_scale_sq(n),
+                                   _core.f32(n0 / n))
+            else:
+                one = single_batch_stager(self.columns, X.device, KIND_GPTAQ, 0, dt, T)
+                one.stage(X, Xfp)
+                one.flush(self._H[idx], _core.sqrt_scale_sq(n), _core.f32(n0 / n),
+                          self._dXXT[idx])
             self._n_flushed[idx] = n
         self._n[idx] = n
         bump(self, "nsamples", idx, tmp)

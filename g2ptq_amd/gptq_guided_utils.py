@@ -7,7 +7,7 @@ G2PTQ) and GPTQ's compensation, inherited unchanged.
 import torch
 
 from . import _core, _lib
-from ._stage import KIND_WEIGHTED, GramStager, bump, lazy_counter
+from ._stage import KIND_WEIGHTED, bump, lazy_counter, single_batch_stager, stager_for
 from .compressed_tensors_utils import compress_layers
 from .gptq_utils import GPTQ, _compensate
 
@@ -64,14 +64,11 @@ class GPTQGuided(GPTQ):
         sal = self.saliencies[idx][k:k + bsz].to(self.dev)
         self._k[idx] = k + bsz
         bump(self, "index", idx, bsz)
-        X = _core.as_bf16_tokens(inp)
+        X, dt = _core.as_tokens(inp)
         sal = sal.reshape(-1, sal.shape[-1]).float().contiguous()
         n_tokens = X.shape[0]
         act_alpha = _core.f32(1 / n_tokens)
-        st = self._stagers[idx]
-        if st is None:
-            st = self._stagers[idx] = GramStager(self.columns, X.device, KIND_WEIGHTED,
-                                                 self.num_groups)
+        st = stager_for(self, idx, X.device, KIND_WEIGHTED, self.num_groups, dt)
         if not st.fits(n_tokens):
             self._flush_staged(idx)
             if st.can_stage(n_tokens):
@@ -81,8 +78,15 @@ class GPTQGuided(GPTQ):
                      act_beta=1.0)
         else:
             # a batch larger than the staging budget: update directly
-            _core.weighted_update(self._H[idx], X, sal, 1.0, 1.0, self.act_square[idx],
-                                  act_alpha, 1.0)
+            if dt == 0:
+                _core.weighted_update(self._H[idx], X, sal, 1.0, 1.0, self.act_square[idx],
+                                      act_alpha, 1.0)
+            else:
+                one = single_batch_stager(self.columns, X.device, KIND_WEIGHTED,
+                                          self.num_groups, dt, n_tokens)
+                one.stage(X, S=sal, s_scale=1.0, act=self.act_square[idx], act_alpha=act_alpha,
+                          act_beta=1.0)
+                one.flush(self._H[idx], 1.0, 1.0)
 
     def fasterquant(self, blocksize=128, percdamp=0.01, groupsize=-1, actorder=False,
                     static_groups=False, export_compressed_tensors=False, backend="hip",

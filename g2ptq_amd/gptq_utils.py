@@ -9,7 +9,8 @@ the fused lazy-batch compensation in libg2ptq_hip.so.
 import torch
 
 from . import _core, _lib
-from ._stage import GramStager, bump, lazy_counter, staged_attr
+from ._stage import (KIND_GPTQ, bump, lazy_counter, single_batch_stager, staged_attr,
+                     stager_for)
 from .compressed_tensors_utils import compress_layers
 from .graph_utils import run_graph, validate_tensors
 
@@ -70,11 +71,9 @@ class GPTQ:
         # slot copies made by a shared finalize are stale now
         self.__dict__.pop("_h_alias", None)
         tmp = 1 if inp.dim() == 2 else inp.shape[0]  # a 2-D input is one sequence
-        X = _core.as_bf16_tokens(inp)
+        X, dt = _core.as_tokens(inp)
         T = X.shape[0]
-        st = self._stagers[idx]
-        if st is None:
-            st = self._stagers[idx] = GramStager(self.columns, X.device)
+        st = stager_for(self, idx, X.device, KIND_GPTQ, 0, dt)
         fits = st.fits(T)
         if not fits:
             self._flush_staged(idx)
@@ -87,7 +86,12 @@ class GPTQ:
         else:
             # a batch larger than the staging budget: update H directly
             n0 = self._n_flushed[idx]
-            _core.hessian_update(self._H[idx], X, _core.sqrt_scale_sq(n), _core.f32(n0 / n))
+            if dt == 0:
+                _core.hessian_update(self._H[idx], X, _core.sqrt_scale_sq(n), _core.f32(n0 / n))
+            else:
+                one = single_batch_stager(self.columns, X.device, KIND_GPTQ, 0, dt, T)
+                one.stage(X)
+                one.flush(self._H[idx], _core.sqrt_scale_sq(n), _core.f32(n0 / n))
             self._n_flushed[idx] = n
         self._n[idx] = n
         bump(self, "nsamples", idx, tmp)

@@ -163,6 +163,33 @@ int g2ptq_weighted_gram(void* stream, uint16_t* XT, int64_t ldt, int64_t K, int6
                         float alpha, float beta, float* H, int64_t ldh, int64_t sH, void* ws,
                         size_t ws_bytes);
 
+/* Staged accumulation of any of the three kinds (kind 0 Hessian, 1 GPTAQ,
+ * 2 weighted) for activations of dtype code 0 (bf16), 1 (fp16) or 2 (fp32):
+ * the reference takes any float input and accumulates in fp32
+ * (inp.float(), gptq_utils/gptq_utils.py:125, gptaq_utils.py:139-146,
+ * g2ptq_utils.py:193-201).  X (and Xfp) are T × C of that dtype.  Xᵀ is
+ * staged as P bf16 planes that sum to it exactly (P = 1, 2, 3), followed by
+ * the kind's planes as above (GPTAQ: hi, lo of X_fp − X; weighted: hi, lo
+ * of x·S[t,g]·s_scale per group); g2ptq_hessian_stage_planes gives their
+ * count.  g2ptq_hessian_gram_ex runs each product once per plane of Xᵀ as
+ * its column operand (the plain Hessian's row operand is all P planes),
+ * accumulating: the same H / Dx / H[g] updates as g2ptq_hessian_gram,
+ * g2ptq_gptaq_gram and g2ptq_weighted_gram (whose bf16 paths these equal
+ * bit for bit), at P times their work for GPTAQ's cross term and the
+ * weighted kind and P² times for the plain Hessian.  Same alignment and
+ * padding rules as g2ptq_hessian_stage / _gram; act (kind 2) as in
+ * g2ptq_weighted_stage. */
+int g2ptq_hessian_stage_planes(int kind, int dtype, int64_t G, int64_t* planes);
+int g2ptq_hessian_stage_ex(void* stream, int kind, int dtype, const void* X, const void* Xfp,
+                           int64_t T, int64_t C, int64_t ldx, int64_t ldxf, const float* S,
+                           int64_t G, int64_t lds, float s_scale, uint16_t* XT, int64_t ldt,
+                           int64_t t_off, float* act, float act_alpha, float act_beta);
+int g2ptq_hessian_gram_ex_workspace(int kind, int dtype, int64_t K, int64_t C, int64_t G,
+                                    size_t* bytes);
+int g2ptq_hessian_gram_ex(void* stream, int kind, int dtype, uint16_t* XT, int64_t ldt, int64_t K,
+                          int64_t C, int64_t G, float alpha, float beta, float* H, int64_t ldh,
+                          int64_t sH, float* Dx, int64_t ldd, void* ws, size_t ws_bytes);
+
 /* ------------------------------------------------------------------------
  * Hessian preparation and factor
  * ---------------------------------------------------------------------- */
