@@ -783,7 +783,7 @@ __global__ __launch_bounds__(256) void sweep4_kernel(SweepArgs a) {
     // fails, the wave reloads the panel and sweeps it again with
     // div_rn_recip, which takes the IEEE division where needed.  The results
     // therefore equal a sweep with div_rn_recip on every column.
-    float xo[NS];
+    float xo[NS], xs[(V == 1) ? NS : 1];
     auto sweep_panel = [&](auto exact_tag, int sub, int rr, int p0) __attribute__((always_inline)) {
       constexpr bool EXACT = decltype(exact_tag)::value;
       float dcol[PW], ycol[PW];
@@ -817,7 +817,13 @@ __global__ __launch_bounds__(256) void sweep4_kernel(SweepArgs a) {
         const float sc = sv[sl];
         const float z0 = zv[sl];
         const float t = EXACT ? div_rn_recip(x, sc, ysv[sl]) : div_markstein(x, sc, ysv[sl]);
-        const float q = clamp_nan(__fadd_rn(rintf(t), z0), minq, fmaxq);
+        // The fast pass clamps with max/min (no compare-and-select hazard on
+        // the column chain): they differ from the NaN-propagating clamp only
+        // for a NaN, and a NaN anywhere in a column's quotients fails the
+        // owner's range test after the panel, which sweeps the panel again
+        // with the exact pass.
+        const float qv = __fadd_rn(rintf(t), z0);
+        const float q = EXACT ? clamp_nan(qv, minq, fmaxq) : fminf(fmaxf(qv, minq), fmaxq);
         const float deq = __fmul_rn(sc, __fsub_rn(q, z0));
         const float d = dcol[jj];
         const float yd = ycol[jj];
@@ -831,12 +837,8 @@ __global__ __launch_bounds__(256) void sweep4_kernel(SweepArgs a) {
         ib[sl] = own ? q : ib[sl];
         eb[sl] = own ? err0 : eb[sl];
         if (!EXACT) xo[sl] = own ? x : xo[sl];
+        if (V == 1) xs[sl] = own ? x : xs[sl];
         if (V == 2) gb[sl] = own ? gh[sl] : gb[sl];
-        if (sub == 0) {
-          e_s[j * RW + rr] = err;
-          if (V == 1) t_s[j * RW + rr] = xb;
-          if (V == 2) z_s[j * RW + rr] = zj;
-        }
         if (jj == PW - 1) last_x = xb;
         // With 16 lanes every column of a slot that is not wholly done takes
         // the update, the done ones too (the owner's and earlier columns):
@@ -894,6 +896,17 @@ __global__ __launch_bounds__(256) void sweep4_kernel(SweepArgs a) {
         load_panel(sub2, rr2, p02);
         sweep_panel(ExactTag<true>{}, sub2, rr2, p02);
       }
+    }
+    // The panel's errors (and GPTAQ's x, G2PTQ's z), read by the replay of
+    // later panels and by the near tails: each lane stores the columns it
+    // owns, once, after the panel (the column chain broadcasts them between
+    // lanes and never reads them back from LDS).
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const int j = p0 + L * s + sub;
+      e_s[j * RW + rr] = eb[s];
+      if (V == 1) t_s[j * RW + rr] = xs[s];
+      if (V == 2) z_s[j * RW + rr] = zg[s];
     }
     // ---- panel outputs ------------------------------------------------------
     if (act) {
