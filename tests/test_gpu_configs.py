@@ -13,6 +13,13 @@
   independent given U and P, so 64 rows of the HIP flow are compared with the
   oracle's compensation (gptaq_utils.py:193-261) run from the HIP's own U
   and P; and P (gptaq_utils.py:349-352) on sampled entries against fp64.
+* Config 3's down_proj at its full width (C = 14336, 4096 rows in 4 row
+  groups, G2PTQ W3 g128, α = 0.1, saliency-weighted Hessians, Student-t(3)
+  gradient rows), sampled rows: β, Z and GH are row-local given U, so 16 rows
+  of each group are checked against the oracle's trust region
+  (g2ptq_utils.py:459-476) evaluated in fp64 on the HIP's U, and their codes
+  against the oracle's compensation (g2ptq_utils.py:252-347) run from the
+  HIP's own U, Z and GH (stage A).
 * Config 4 at its own shapes: 32 experts' gate/up (768×2048) in one 64-slot
   launch whose Hessians come from SharedInputHessian slot copies, and 64
   experts' down_proj (2048×768: a 512-column super-block and a ragged one of
@@ -31,6 +38,11 @@ from oracle.parity import check_flow, check_stage_b, element_params, stage_b, su
 from tests._util import gen
 
 pytestmark = [pytest.mark.gpu, pytest.mark.timeout(900)]
+
+# β = mean_j(1 − √(1 − x_j)) in fp32 cancels for x_j ≪ 1: each term carries a
+# few ulps of 1 whatever x_j's accuracy, so β is held to 1e-3 relative plus
+# 2 ulps of 1.
+BETA_FLOOR = 2 * torch.finfo(torch.float32).eps
 
 
 def _tokens(n, C, g, dev, chunk=16384):
@@ -173,6 +185,127 @@ def test_config5_full_width_sampled_rows(dev):
     check_stage_b(rep)
     Qd = lin.weight.detach()[rs.to(dev)].float().cpu()
     qh = (S[rs] * (codes - Z[rs]).float()).bfloat16().float()
+    assert torch.equal(Qd, qh)
+
+
+def _g2ptq_hip_inputs(gq, q, G, gs, alpha):
+    """U, the RTN estimate Q0, β, Z and GH of G2PTQ.fasterquant's trust-region
+    step (g2ptq_utils.py:380-476), formed by the same library calls on copies
+    of the layer's state (deterministic: the flow recomputes the same bits)."""
+    from g2ptq_amd import _core, _lib, make_group_quantizers
+    from g2ptq_amd.common_utils import fake_quantize_grouped
+    W = gq.layers[0].weight.detach().float()
+    R, C = W.shape
+    Rg = R // G
+    W_sub = W.view(G, Rg, C).clone()
+    grads = gq.gradients.view(G, Rg, C).clone()
+    H = gq.H.view(G, C, C).clone()
+    _core.prepare_hessian(H, W_sub, Grad=grads)
+    qs = make_group_quantizers(q, C, gs)
+    for i, qq in enumerate(qs):
+        qq.find_params(W_sub[:, :, i * gs:(i + 1) * gs].reshape(R, -1))
+    Q0 = fake_quantize_grouped(qs, W_sub, gs).contiguous()
+    U, damps = _core.factor(H, 0.01)
+    del H
+    beta = torch.empty(R, device=W.device)
+    Z, GH = torch.empty_like(W_sub), torch.empty_like(W_sub)
+    ws = torch.empty(_lib.query_size("g2ptq_trust_region_workspace", G, Rg, C),
+                     dtype=torch.uint8, device=W.device)
+    _lib.call("g2ptq_trust_region", _core.stream(), _lib.ptr(grads), _lib.ptr(U), _lib.ptr(Q0),
+              _lib.ptr(W_sub), G, Rg, C, _core.f32(alpha), 1, _lib.ptr(beta), _lib.ptr(Z),
+              _lib.ptr(GH), _lib.ptr(ws), ws.numel())
+    torch.cuda.synchronize()
+    return W_sub, grads, U, damps, Q0, beta.view(G, Rg), Z, GH
+
+
+def test_config3_down_proj_full_width_sampled_rows(dev):
+    from g2ptq_amd import G2PTQ, WeightQuantizer, make_group_quantizers
+    R, C, G, N, tb, bits, gs, alpha = 4096, 14336, 4, 32768, 4096, 3, 128, 0.1
+    Rg, per = R // G, 16
+    print(f"config 3 down_proj: G2PTQ W{bits} g{gs}, {R}x{C} in {G} row groups, {N} tokens, "
+          f"alpha {alpha}", flush=True)
+    g = torch.Generator(device=dev).manual_seed(49)
+    X, _ = _tokens(N, C, g, dev, chunk=8192)
+    sal = torch.exp(0.5 * torch.randn(N, 1, device=dev, generator=g)) * \
+        torch.rand(N, G, device=dev, generator=g)
+    lin = torch.nn.Linear(C, R, bias=False, device=dev, dtype=torch.bfloat16)
+    with torch.no_grad():
+        lin.weight.copy_(torch.randn(R, C, device=dev, generator=g) * 0.02)
+    # per-output-channel gradients 1e-3·N(0,1) with Student-t(3) row scales
+    chi = torch.randn(3, R, 1, device=dev, generator=g).pow(2).sum(0)
+    tau = (torch.randn(R, 1, device=dev, generator=g) / torch.sqrt(chi / 3)).abs()
+    grads = 1e-3 * torch.randn(R, C, device=dev, generator=g) * tau
+    batches = range(0, N, tb)
+    gq = G2PTQ([lin], [[sal[i:i + tb] for i in batches]], [grads], G)
+    q = WeightQuantizer()
+    q.configure(bits, perchannel=True, sym=True)
+    gq.quantizer = make_group_quantizers(q, C, gs)
+    for i in batches:
+        gq.add_batch(0, X[i:i + tb].unsqueeze(0), None)
+    del X, sal
+    W_sub, Gr, U, damps, Q0, beta, Z, GH = _g2ptq_hip_inputs(gq, q, G, gs, alpha)
+    assert damps == [0.01] * G
+    gi = gen(50)
+    local = torch.stack([torch.sort(torch.randperm(Rg, generator=gi)[:per]).values
+                         for _ in range(G)])                     # (G, per)
+    rows = (local + Rg * torch.arange(G)[:, None]).flatten()     # rows of the layer
+    li = local.to(dev)
+
+    def pick(t):
+        return torch.stack([t[k, li[k]] for k in range(G)])    # (G, per, C)
+
+    Wr, Grr, Q0r, Zr, GHr = (pick(t) for t in (W_sub, Gr, Q0, Z, GH))
+    br = torch.stack([beta[k, li[k]] for k in range(G)])
+    del W_sub, Gr, Q0, Z, GH
+    # (1) the trust region on the sampled rows against the oracle in fp64 on
+    # the same U (β, Z and GH are row-local given U)
+    ze, ge, be = 0.0, 0.0, 0.0
+    for k in range(G):
+        U64 = U[k].double()
+        Ainv = (U64.T @ U64).cpu()
+        b64, Z64, GH64 = oflows.g2ptq_trust_region(
+            Grr[k:k + 1].double().cpu(), Ainv[None], U64.cpu()[None], Q0r[k:k + 1].double().cpu(),
+            Wr[k:k + 1].double().cpu(), alpha, True)
+        del Ainv, U64
+        b = br[k].double().cpu()
+        be = max(be, float(((b - b64[0]).abs() / (1e-3 * b64[0].abs() + BETA_FLOOR)).max()))
+        for got, ref, acc in ((Zr[k], Z64[0], "z"), (GHr[k], GH64[0], "g")):
+            # Z/β = Grad·Uᵀ and GH/β = Grad·A⁻¹, each row against its largest entry
+            got = got.double().cpu() / b[:, None]
+            ref = ref / b64[0][:, None]
+            e = ((got - ref).abs().amax(-1) / ref.abs().amax(-1)).max().item()
+            if acc == "z":
+                ze = max(ze, e)
+            else:
+                ge = max(ge, e)
+    print(f"trust region, {G}x{per} rows: beta range [{br.min():.4g}, {br.max():.4g}], "
+          f"|β − fp64| / (1e-3·β + floor) ≤ {be:.3g}; Z/β rel to row max {ze:.3g}, GH/β {ge:.3g}",
+          flush=True)
+    assert float(br.min()) > 0
+    assert be <= 1.0 and ze <= 1e-4 and ge <= 1e-4, (be, ze, ge)
+    # (2) the full HIP flow, then the sampled rows through the oracle's
+    # compensation with the HIP's U, Z and GH (stage A)
+    gq.fasterquant(blocksize=128, percdamp=0.01, groupsize=gs, alpha=alpha, backend="hip",
+                   export_compressed_tensors=True)
+    torch.cuda.synchronize()
+    assert torch.equal(gq._beta, beta), "the flow's β differs from the same calls' β"
+    codes = unpack_codes(lin._export_qparams["weight_packed"], bits, C)[rows]
+    S, Zq = element_params(gq.quantizer, R, C, gs, False)
+    Uc = U.cpu()
+    del U
+    oq = oquant.make_group_quantizers(
+        oquant.WeightQuantizer().configure(bits, perchannel=True, sym=True), C, gs)
+    rec = {}
+    Qr, Ir, _ = ocomp.g2ptq_compensation(Wr.cpu(), Uc, Zr.cpu(), GHr.cpu().clone(), oq, 128, gs,
+                                         False, None, None, record=rec)
+    n = G * per
+    so, zo = element_params(oq, n, C, gs, False)
+    rep = stage_b(codes, Ir.reshape(n, C), rec["X"].reshape(n, C), S[rows], so, Zq[rows], zo,
+                  Qr.reshape(n, C))
+    print(f"config 3 down_proj, {n} sampled rows, stage A: {summary(rep)}", flush=True)
+    check_stage_b(rep)
+    Qd = lin.weight.detach()[rows.to(dev)].float().cpu()
+    qh = (S[rows] * (codes - Zq[rows]).float()).bfloat16().float()
     assert torch.equal(Qd, qh)
 
 

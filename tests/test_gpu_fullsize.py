@@ -7,7 +7,9 @@ exact arithmetic fixes, evaluated in fp64:
   Hessian entries equal (2/n)·Σ_t x_ti·x_tj (gptq_utils.py:115-126); and the
   compensation is self-consistent — with E = (W − Q)·U⁻¹ (the GPTQ identity
   W − Q = E·U, gptq_utils.py:28-51, 180-230), every pre-quantization value
-  x_j = q_j + E_j·U_jj rounds to its code under its group's scale;
+  x_j = q_j + E_j·U_jj rounds to its code under its group's scale; and 64
+  sampled rows match the oracle's compensation run from the HIP's own U
+  (stage A: rows are independent given U);
 * config 2's q/k/v input (C = 4096, 262,144 tokens): every Hessian entry
   against fp64 sums; this Gram splits K 15 ways (the count that fills the
   last wave of workgroups), so the tokens are zero-padded to a multiple of
@@ -108,6 +110,23 @@ def test_down_proj_hessian_and_compensation_at_full_size(dev):
     lo = codes[rows] == -8
     hi = codes[rows] == 7
     assert (t[lo] <= 0.5 + 1e-3).all() and (t[hi] >= -0.5 - 1e-3).all()
+    # (3) stage A on 64 sampled rows: the oracle's compensation
+    # (gptq_utils.py:165-232) from the HIP's own U, rows being independent
+    # given U
+    from oracle import compensate as ocomp
+    from oracle import quant as oquant
+    from oracle.parity import check_stage_b, stage_b, summary
+    rs = torch.sort(torch.randperm(R, generator=gen(75))[:64]).values.to(dev)
+    oq = oquant.make_group_quantizers(
+        oquant.WeightQuantizer().configure(4, perchannel=True, sym=True), C, 128)
+    rec = {}
+    Qr, Ir, _ = ocomp.gptq_compensation(W0[rs].cpu().unsqueeze(0), U.cpu().unsqueeze(0), oq, 128,
+                                        128, False, None, None, record=rec)
+    so, zo = element_params(oq, 64, C, 128, False)
+    rep = stage_b(codes[rs], Ir.reshape(64, C), rec["X"].reshape(64, C), S[rs], so, Z[rs], zo,
+                  Qr.reshape(64, C))
+    print(f"down_proj, 64 sampled rows, stage A: {summary(rep)}", flush=True)
+    check_stage_b(rep)
 
 
 def test_qkv_hessian_at_full_size(dev):
