@@ -43,9 +43,10 @@ SIGNATURES = {
                                       _i64, _p, _f32, _f32, _p, _sz],
     "g2ptq_weighted_stage": [_p, _p, _i64, _i64, _i64, _p, _i64, _i64, _f32, _p, _i64, _i64, _p, _f32,
                              _f32],
-    "g2ptq_weighted_gram_workspace": [_i64, _i64, _szp],
+    "g2ptq_weighted_gram_workspace": [_i64, _i64, _i64, _szp],
     "g2ptq_weighted_gram": [_p, _p, _i64, _i64, _i64, _i64, _f32, _f32, _p, _i64, _i64, _p, _sz],
     "g2ptq_hessian_stage_planes": [_i32, _i32, _i64, ctypes.POINTER(ctypes.c_int64)],
+    "g2ptq_hessian_stage_height": [_i32, _i32, _i64, _i64, ctypes.POINTER(ctypes.c_int64)],
     "g2ptq_hessian_stage_ex": [_p, _i32, _i32, _p, _p, _i64, _i64, _i64, _i64, _p, _i64, _i64,
                                _f32, _p, _i64, _i64, _p, _f32, _f32],
     "g2ptq_hessian_gram_ex_workspace": [_i32, _i32, _i64, _i64, _i64, _szp],

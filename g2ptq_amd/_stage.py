@@ -15,11 +15,14 @@ when the Hessian is read, which amortises the Gram kernel's per-launch work
 long K runs.
 
 Planes per kind: 0 (GPTQ) Xᵀ; 1 (GPTAQ) Xᵀ and the bf16 hi/lo parts of
-(X_fp − X)ᵀ; 2 (weighted, G groups) Xᵀ and the hi/lo parts of (x·s[t,g])ᵀ.
-Activations that are not bf16 take P bf16 planes for Xᵀ that sum to it
-exactly (fp16: 2, fp32: 3; the reference's ``inp.float()``,
-gptq_utils.py:125): every Gram product then runs once per plane of its
-column operand (four, resp. nine times the bf16 Gram work for GPTQ).
+(X_fp − X)ᵀ; 2 (weighted, G groups) Xᵀ and G fp32 rows of per-token weights
+s[t,g]·(1/T_b), from which the Gram kernel forms x·s itself.  Activations
+that are not bf16 take P bf16 planes for Xᵀ that sum to it exactly (fp16: 2,
+fp32: 3; the reference's ``inp.float()``, gptq_utils.py:125), and the
+weighted kind then stages the hi/lo parts of (x·s[t,g])ᵀ as planes: every
+Gram product runs once per plane of its column operand (four, resp. nine
+times the bf16 Gram work for GPTQ).  The library gives each layout's height
+(``g2ptq_hessian_stage_height``).
 
 The first buffer holds 32 batches of the first batch's size (at least 65536
 tokens): a calibration run is typically 32 or more batches, so its whole set
@@ -92,13 +95,13 @@ class GramStager:
         self.kind = kind
         self.G = groups
         self.dtype = dtype
-        P = _X_PLANES[dtype]
-        self.planes = P + {KIND_GPTQ: 0, KIND_GPTAQ: 2, KIND_WEIGHTED: 2 * groups}[kind]
-        self.rows = _lib.query_size_i64("g2ptq_hessian_stage_rows", columns)
+        # rows of staged bf16 per token column
+        self.height = _lib.query_size_i64("g2ptq_hessian_stage_height", kind, dtype, columns,
+                                          groups if kind == KIND_WEIGHTED else 0)
         budget = budget_bytes if budget_bytes is not None else DEFAULT_BUDGET
         if budget is None:
             budget = min(_MAX_BUDGET, _device_memory(torch.device(device)) // 4)
-        per_token = self.planes * self.rows * 2
+        per_token = self.height * 2
         self.max_tokens = max(_GRAM_PAD * 2, budget // per_token // _GRAM_PAD * _GRAM_PAD)
         self.buf = None
         self.cap = 0        # token columns of buf
@@ -129,7 +132,7 @@ class GramStager:
         # group, the caller's tensors): shrink a large buffer rather than fail.
         # Buffers under _QUERY_BYTES skip the query (a device call per buffer:
         # the many small per-expert stagers of an MoE block would pay it often).
-        per_token = self.planes * self.rows * 2
+        per_token = self.height * 2
         if cap * per_token >= _QUERY_BYTES:
             free, _ = torch.cuda.mem_get_info(self.device)
             cached = (torch.cuda.memory_reserved(self.device)
@@ -138,8 +141,7 @@ class GramStager:
             if cap * per_token > avail:
                 cap = _ceil(max(need, avail // per_token - _PITCH_SKEW - _GRAM_PAD),
                             _GRAM_PAD) + _PITCH_SKEW
-        self.buf = torch.empty(self.planes, self.rows, cap, dtype=torch.bfloat16,
-                               device=self.device)
+        self.buf = torch.empty(self.height, cap, dtype=torch.bfloat16, device=self.device)
         self.cap = cap
 
     def stage(self, X, Xfp=None, S=None, s_scale=1.0, act=None, act_alpha=0.0, act_beta=1.0):
@@ -180,6 +182,8 @@ class GramStager:
         if self.dtype != DTYPE_BF16:
             nbytes = _lib.query_size("g2ptq_hessian_gram_ex_workspace", self.kind, self.dtype,
                                      self.k, self.C, self.G)
+        elif self.kind == KIND_WEIGHTED:
+            nbytes = _lib.query_size(_GRAM_WS[self.kind], self.k, self.C, self.G)
         else:
             nbytes = _lib.query_size(_GRAM_WS[self.kind], self.k, self.C)
         ws = _lib.workspace(nbytes, self.buf.device)

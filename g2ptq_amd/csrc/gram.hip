@@ -136,8 +136,8 @@ __device__ __forceinline__ void store_block(uint16_t* __restrict__ P, int64_t ld
 }
 
 // KIND 0: plane 0 = Xᵀ.  KIND 1 (GPTAQ): planes 0..2 = Xᵀ, hi and lo of
-// (X_fp − X)ᵀ.  KIND 2 (weighted): plane 0 = Xᵀ, planes 1 + 2g and 2 + 2g =
-// hi and lo of (x·s[t,g]·s_scale)ᵀ.
+// (X_fp − X)ᵀ.  KIND 2 (weighted): plane 0 = Xᵀ, then G rows of ldt fp32
+// token weights w[g][t] = S[t,g]·s_scale (wgram_kernel forms x·w itself).
 template <int KIND>
 __global__ __launch_bounds__(256) void stage_kernel(StageArgs s) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -164,20 +164,18 @@ __global__ __launch_bounds__(256) void stage_kernel(StageArgs s) {
     store_block(s.XT + s.plane, s.ldt, f0, col, h);
     store_block(s.XT + 2 * s.plane, s.ldt, f0, col, f);
   }
-  if (KIND == 2) {
-    for (int g = 0; g < s.G; ++g) {
-      float sv[8];
+  if (KIND == 2 && blockIdx.y == 0 && wave == 0) {
+    // the weights w[g][t] = S[t,g]·s_scale of this wave's 64 tokens, fp32 rows
+    // of ldt after plane 0 (lane: tokens t0..t0+7, groups fb, fb + 8, …)
+    float* W = reinterpret_cast<float*>(s.XT + s.plane);
+    for (int g = fb; g < s.G; g += 8) {
+      float wv[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i)
-        sv[i] = (t0 + i < s.T) ? s.S[(t0 + i) * s.lds + g] * s.s_scale : 0.f;
-      uint32_t h[8][4], l[8][4];
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-#pragma unroll
-        for (int w = 0; w < 4; ++w)
-          split2(lo_f32(r[i][w]) * sv[i], hi_f32(r[i][w]) * sv[i], h[i][w], l[i][w]);
-      store_block(s.XT + (1 + 2 * g) * s.plane, s.ldt, f0, col, h);
-      store_block(s.XT + (2 + 2 * g) * s.plane, s.ldt, f0, col, l);
+        wv[i] = (t0 + i < s.T) ? s.S[(t0 + i) * s.lds + g] * s.s_scale : 0.f;
+      float4* dst = reinterpret_cast<float4*>(W + g * s.ldt + col);
+      dst[0] = make_float4(wv[0], wv[1], wv[2], wv[3]);
+      dst[1] = make_float4(wv[4], wv[5], wv[6], wv[7]);
     }
   }
 }
@@ -349,6 +347,11 @@ struct G2Args {
   float alpha, beta;
   float* H; int64_t ldh;
   float* P;        // split partials: (tile * S + s) * TT*TT
+  // weighted products (wgram_kernel): per-group token weights and outputs
+  const float* W;  // G rows of ldw fp32 weights, one per staged token
+  int64_t ldw;
+  int64_t G;       // groups (1 for the other products)
+  int64_t sH;      // stride between the groups' outputs
 };
 
 // Upper-triangle tile number idx → (I, J), in row-major order.
@@ -404,6 +407,98 @@ __device__ __forceinline__ void grid_tile(int64_t idx, int64_t nt, int64_t& I, i
   const int64_t h = nt - g0 < GB ? nt - g0 : GB;
   I = g0 + r % h;
   J = r / h;
+}
+
+// Epilogue of a 256×256 tile of 8 waves (2 × 4 wave grid, 128×64 per wave):
+// H (one output matrix) = beta·H + alpha·acc, mirrored for symmetric products
+// (diagonal tiles store their upper triangle both ways), or the raw tile to
+// the split partials Pt when K is split (a.S > 1).
+template <bool HAS_BETA, bool FULL>
+__device__ __forceinline__ void store_tile(const G2Args& a, float* H, float* Pt,
+                                           f32x16 (&acc)[4][2], int64_t I, int64_t J, bool diag,
+                                           int wm, int wn, int lh, int lr) {
+  // 32×32 MFMA output: lane holds rows 8*(v/4) + 4*(lane/32) + v%4, column lane%32.
+  // Mirror stores: the four rows v..v+3 of one lane are four consecutive
+  // columns of the transposed element row, stored as one 16-byte vector.
+  // With beta != 0 the 32 H values of one m-slice are loaded together before
+  // any of them is stored (the compiler cannot prove that stores to H do not
+  // alias later loads, so interleaved read-modify-writes would serialise one
+  // memory round trip per element).
+  if (FULL && a.S == 1) {
+    const int64_t i0 = I * TT, j0 = J * TT;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      float hv[2][16];
+#pragma unroll
+      for (int n = 0; n < 2; ++n)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int64_t i = i0 + wm * 128 + m * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+          const int64_t j = j0 + wn * 64 + n * 32 + lr;
+          hv[n][v] = (HAS_BETA && i < a.C && j < a.C) ? H[i * a.ldh + j] : 0.f;
+        }
+#pragma unroll
+      for (int n = 0; n < 2; ++n)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int64_t i = i0 + wm * 128 + m * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+          const int64_t j = j0 + wn * 64 + n * 32 + lr;
+          if (i < a.C && j < a.C)
+            H[i * a.ldh + j] = (HAS_BETA ? a.beta * hv[n][v] : 0.f) + a.alpha * acc[m][n][v];
+        }
+    }
+  } else if (a.S == 1) {
+    const int64_t i0 = I * TT, j0 = J * TT;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      float hv[2][16];
+#pragma unroll
+      for (int n = 0; n < 2; ++n)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int64_t i = i0 + wm * 128 + m * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+          const int64_t j = j0 + wn * 64 + n * 32 + lr;
+          hv[n][v] = (HAS_BETA && i < a.C && j < a.C) ? H[i * a.ldh + j] : 0.f;
+        }
+#pragma unroll
+      for (int n = 0; n < 2; ++n)
+#pragma unroll
+        for (int vq = 0; vq < 4; ++vq) {
+          const int64_t ib = i0 + wm * 128 + m * 32 + 8 * vq + 4 * lh;  // rows ib..ib+3
+          const int64_t j = j0 + wn * 64 + n * 32 + lr;
+          float val[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int64_t i = ib + u;
+            val[u] = (HAS_BETA ? a.beta * hv[n][4 * vq + u] : 0.f) + a.alpha * acc[m][n][4 * vq + u];
+            if (i >= a.C || j >= a.C || (diag && i > j)) continue;
+            H[i * a.ldh + j] = val[u];
+          }
+          if (j >= a.C) continue;
+          if (!diag && ib + 3 < a.C && (a.ldh & 3) == 0) {
+            *reinterpret_cast<float4*>(H + j * a.ldh + ib) =
+                make_float4(val[0], val[1], val[2], val[3]);
+          } else {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              const int64_t i = ib + u;
+              if (i < a.C && i < j) H[j * a.ldh + i] = val[u];
+            }
+          }
+        }
+    }
+  } else {
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+      for (int n = 0; n < 2; ++n)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int il = wm * 128 + m * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+          const int jl = wn * 64 + n * 32 + lr;
+          Pt[il * TT + jl] = acc[m][n][v];
+        }
+  }
 }
 
 template <bool HAS_BETA, bool FULL>
@@ -558,89 +653,207 @@ __global__ __launch_bounds__(NTH) void gram256_kernel(G2Args a) {
 #undef G2_STORE
 #undef G2_MMA
 
-  // 32×32 MFMA output: lane holds rows 8*(v/4) + 4*(lane/32) + v%4, column lane%32.
-  // Mirror stores: the four rows v..v+3 of one lane are four consecutive
-  // columns of the transposed element row, stored as one 16-byte vector.
-  // With beta != 0 the 32 H values of one m-slice are loaded together before
-  // any of them is stored (the compiler cannot prove that stores to H do not
-  // alias later loads, so interleaved read-modify-writes would serialise one
-  // memory round trip per element).
-  if (FULL && a.S == 1) {
-    const int64_t i0 = I * TT, j0 = J * TT;
+  store_tile<HAS_BETA, FULL>(a, a.H, a.S == 1 ? nullptr : a.P + (tile * a.S + split) * (int64_t)(TT * TT),
+                             acc, I, J, diag, wm, wn, lh, lr);
+}
+
+// Weighted Hessians of bf16 activations, the split formed on the way into LDS:
+//   H[g] = beta·H[g] + alpha·Σ_t x_t·(x_t·w[g][t])ᵀ,   w[g][t] = S[t,g]·s_scale,
+// over the upper tiles of every group g, one launch for all groups.  The row
+// operand is Xᵀ (panel I).  The column operand v = x·w (panel J) is formed per
+// stage from Xᵀ and the staged weights, split in registers into bf16
+// hi = bf16(v) and lo = bf16(v − hi) (the values the hi/lo planes of the
+// plane-staged path hold), written to LDS as two tiles, and both are
+// multiplied into the same accumulator.  One workgroup = one (tile, group,
+// split); a tile's groups are consecutive in the work list, so they run
+// together on one XCD and read the same two panels through its L2.
+//   * 8 waves in a 2 × 4 grid, 128×64 per wave (the gram256 epilogue);
+//   * a stage is WKS = 32 tokens: three 256 × 32 bf16 tiles (Xᵀ_I, hi, lo),
+//     48 KiB, double buffered; LDS rows are 64 bytes (four 16-byte chunks),
+//     chunk c of row r at c ^ swz4(r), conflict free for the fragment reads
+//     (16 consecutive rows, one chunk) and the stage writes (4 rows × 4
+//     chunks) on 32- and 64-bank LDS;
+//   * per 16-token k-step a wave reads 4 row and 2 + 2 column fragments for
+//     16 MFMAs (the plane-staged path reads 6 for 8).
+constexpr int WKS = 32;
+
+__device__ __forceinline__ int swz4(int r) { return ((r >> 1) & 3) ^ ((r >> 3) & 1); }
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Two fp32 values → packed bf16 (round to nearest even, v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+}
+
+// Eight bf16 x (tokens t..t+7 of one feature) times their weights → the hi
+// and lo chunks of v = x·w: hi = bf16(fl(x·w)), lo = bf16(x·w − hi) with the
+// residual formed by one fused multiply-add from the exact product, so
+// hi + lo carries x·w to 16 significant bits.
+__device__ __forceinline__ void split_chunk(const uint4& x, const float4& w0, const float4& w1,
+                                            uint4& h, uint4& l) {
+  const uint32_t xw[4] = {x.x, x.y, x.z, x.w};
+  const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+  uint32_t hw[4], lw[4];
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      float hv[2][16];
-#pragma unroll
-      for (int n = 0; n < 2; ++n)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int64_t i = i0 + wm * 128 + m * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
-          const int64_t j = j0 + wn * 64 + n * 32 + lr;
-          hv[n][v] = (HAS_BETA && i < a.C && j < a.C) ? a.H[i * a.ldh + j] : 0.f;
-        }
-#pragma unroll
-      for (int n = 0; n < 2; ++n)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int64_t i = i0 + wm * 128 + m * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
-          const int64_t j = j0 + wn * 64 + n * 32 + lr;
-          if (i < a.C && j < a.C)
-            a.H[i * a.ldh + j] = (HAS_BETA ? a.beta * hv[n][v] : 0.f) + a.alpha * acc[m][n][v];
-        }
-    }
-  } else if (a.S == 1) {
-    const int64_t i0 = I * TT, j0 = J * TT;
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      float hv[2][16];
-#pragma unroll
-      for (int n = 0; n < 2; ++n)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int64_t i = i0 + wm * 128 + m * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
-          const int64_t j = j0 + wn * 64 + n * 32 + lr;
-          hv[n][v] = (HAS_BETA && i < a.C && j < a.C) ? a.H[i * a.ldh + j] : 0.f;
-        }
-#pragma unroll
-      for (int n = 0; n < 2; ++n)
-#pragma unroll
-        for (int vq = 0; vq < 4; ++vq) {
-          const int64_t ib = i0 + wm * 128 + m * 32 + 8 * vq + 4 * lh;  // rows ib..ib+3
-          const int64_t j = j0 + wn * 64 + n * 32 + lr;
-          float val[4];
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const int64_t i = ib + u;
-            val[u] = (HAS_BETA ? a.beta * hv[n][4 * vq + u] : 0.f) + a.alpha * acc[m][n][4 * vq + u];
-            if (i >= a.C || j >= a.C || (diag && i > j)) continue;
-            a.H[i * a.ldh + j] = val[u];
-          }
-          if (j >= a.C) continue;
-          if (!diag && ib + 3 < a.C && (a.ldh & 3) == 0) {
-            *reinterpret_cast<float4*>(a.H + j * a.ldh + ib) =
-                make_float4(val[0], val[1], val[2], val[3]);
-          } else {
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-              const int64_t i = ib + u;
-              if (i < a.C && i < j) a.H[j * a.ldh + i] = val[u];
-            }
-          }
-        }
-    }
-  } else {
-    float* P = a.P + (tile * a.S + split) * (int64_t)(TT * TT);
-#pragma unroll
-    for (int m = 0; m < 4; ++m)
-#pragma unroll
-      for (int n = 0; n < 2; ++n)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int il = wm * 128 + m * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
-          const int jl = wn * 64 + n * 32 + lr;
-          P[il * TT + jl] = acc[m][n][v];
-        }
+  for (int k = 0; k < 4; ++k) {
+    const float x0 = lo_f32(xw[k]), x1 = hi_f32(xw[k]);
+    hw[k] = pk_bf16(x0 * wv[2 * k], x1 * wv[2 * k + 1]);
+    lw[k] = pk_bf16(__builtin_fmaf(x0, wv[2 * k], -lo_f32(hw[k])),
+                    __builtin_fmaf(x1, wv[2 * k + 1], -hi_f32(hw[k])));
   }
+  h = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+  l = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+}
+
+template <bool HAS_BETA>
+__global__ __launch_bounds__(NTH) void wgram_kernel(G2Args a) {
+  __shared__ __attribute__((aligned(16))) uint16_t Lw[2][3][TT * WKS];  // [buf][Xᵀ_I / hi / lo]
+
+  // XCD-contiguous renumbering as in gram256_kernel; the work list is
+  // split-major, then band-ordered tiles, then groups.
+  const int64_t nwg = gridDim.x, bid = blockIdx.x;
+  const int64_t q8 = nwg >> 3, r8 = nwg & 7, xcd = bid & 7;
+  const int64_t id = xcd * q8 + (xcd < r8 ? xcd : r8) + (bid >> 3);
+  const int64_t grp = id % a.G, rest = id / a.G;
+  const int split = (int)(rest / a.tiles);
+  const int64_t tile_ord = rest - (int64_t)split * a.tiles;
+  int64_t I, J;
+  band_tile(tile_ord, a.nt, I, J);
+  const int64_t tile = I * a.nt - I * (I - 1) / 2 + (J - I);
+  const bool diag = I == J;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 2, wn = wave & 3;
+
+  const uint16_t* Ag = a.B + (I * TT) * a.ldt + (int64_t)split * a.kc;
+  const uint16_t* Bg = a.B + (J * TT) * a.ldt + (int64_t)split * a.kc;
+  // Chunk q = tid + i*512 of a stage tile: row q >> 2, 16-byte chunk q & 3.
+  const int qrow = tid >> 2, qc = tid & 3;  // chunk i adds 128 rows
+  const float* Wg = a.W + grp * a.ldw + (int64_t)split * a.kc + qc * 8;
+  const int64_t goff = (int64_t)qrow * a.ldt + qc * 8;
+  const int64_t gstep = (int64_t)128 * a.ldt;
+  const int nk = (int)(a.kc / WKS);
+  uint4 xa0, xa1, xb0, xb1, ya0, ya1, yb0, yb1;
+  float4 xw0, xw1, yw0, yw1;
+#define W_LOAD(R, st)                                                                   \
+  do {                                                                                  \
+    const int64_t k0_ = (int64_t)((st) < nk ? (st) : nk - 1) * WKS;                     \
+    R##a0 = *reinterpret_cast<const uint4*>(Ag + goff + k0_);                           \
+    R##a1 = *reinterpret_cast<const uint4*>(Ag + goff + gstep + k0_);                   \
+    R##b0 = *reinterpret_cast<const uint4*>(Bg + goff + k0_);                           \
+    R##b1 = *reinterpret_cast<const uint4*>(Bg + goff + gstep + k0_);                   \
+    R##w0 = *reinterpret_cast<const float4*>(Wg + k0_);                                 \
+    R##w1 = *reinterpret_cast<const float4*>(Wg + k0_ + 4);                             \
+  } while (0)
+  // rows qrow and qrow + 128 share swz4 (bits 1..3 of the row)
+  const int lpos = qrow * WKS + ((qc ^ swz4(qrow)) << 3);
+#define W_STORE(R, buf)                                                                 \
+  do {                                                                                  \
+    uint4 h0_, l0_, h1_, l1_;                                                           \
+    split_chunk(R##b0, R##w0, R##w1, h0_, l0_);                                         \
+    split_chunk(R##b1, R##w0, R##w1, h1_, l1_);                                         \
+    uint16_t* la = &Lw[(buf)][0][lpos];                                                 \
+    uint16_t* lh_ = &Lw[(buf)][1][lpos];                                                \
+    uint16_t* ll_ = &Lw[(buf)][2][lpos];                                                \
+    *reinterpret_cast<uint4*>(la) = R##a0;                                              \
+    *reinterpret_cast<uint4*>(la + 128 * WKS) = R##a1;                                  \
+    *reinterpret_cast<uint4*>(lh_) = h0_;                                               \
+    *reinterpret_cast<uint4*>(lh_ + 128 * WKS) = h1_;                                   \
+    *reinterpret_cast<uint4*>(ll_) = l0_;                                               \
+    *reinterpret_cast<uint4*>(ll_ + 128 * WKS) = l1_;                                   \
+  } while (0)
+
+  f32x16 acc[4][2];
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+#pragma unroll
+    for (int n = 0; n < 2; ++n)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[m][n][v] = 0.f;
+
+  const int lr = lane & 31, lh = lane >> 5;
+#define W_MMA(buf)                                                                      \
+  do {                                                                                  \
+    const uint16_t* As = Lw[(buf)][0];                                                  \
+    const uint16_t* Bh = Lw[(buf)][1];                                                  \
+    const uint16_t* Bl = Lw[(buf)][2];                                                  \
+    _Pragma("unroll") for (int ks = 0; ks < WKS / 16; ++ks) {                           \
+      const int c = ks * 2 + lh;                                                        \
+      bf16x8 av[4], bh[2], bl[2];                                                       \
+      _Pragma("unroll") for (int m = 0; m < 4; ++m) {                                   \
+        const int row = wm * 128 + m * 32 + lr;                                         \
+        av[m] = *reinterpret_cast<const bf16x8*>(As + row * WKS + ((c ^ swz4(row)) << 3)); \
+      }                                                                                 \
+      _Pragma("unroll") for (int n = 0; n < 2; ++n) {                                   \
+        const int row = wn * 64 + n * 32 + lr;                                          \
+        const int off = row * WKS + ((c ^ swz4(row)) << 3);                             \
+        bh[n] = *reinterpret_cast<const bf16x8*>(Bh + off);                             \
+        bl[n] = *reinterpret_cast<const bf16x8*>(Bl + off);                             \
+      }                                                                                 \
+      _Pragma("unroll") for (int m = 0; m < 4; ++m)                                     \
+      _Pragma("unroll") for (int n = 0; n < 2; ++n)                                     \
+        acc[m][n] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[m], bh[n], acc[m][n], 0, 0, 0); \
+      _Pragma("unroll") for (int m = 0; m < 4; ++m)                                     \
+      _Pragma("unroll") for (int n = 0; n < 2; ++n)                                     \
+        acc[m][n] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[m], bl[n], acc[m][n], 0, 0, 0); \
+    }                                                                                   \
+  } while (0)
+
+  // nk is a multiple of 4 (the host pads every split to an even number of
+  // 64-token stages); loads past the last stage re-read it and go unused.
+  // Stage kt is multiplied out of buffer kt&1 while the registers holding
+  // stage kt+1 are split and written to the other buffer and refilled with
+  // stage kt+3; one barrier per stage.
+  // Per stage: 16 fragment reads, 32 MFMAs, the split's VALU work, 6 LDS
+  // writes and 6 global loads, spread so that every group of four MFMAs
+  // carries a share of the other work.
+#define W_PATTERN()                                                                     \
+  do {                                                                                  \
+    __builtin_amdgcn_sched_group_barrier(0x100, 8, 0); /* DS read  */                   \
+    _Pragma("unroll") for (int r_ = 0; r_ < 8; ++r_) {                                  \
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); /* MFMA */                     \
+      __builtin_amdgcn_sched_group_barrier(0x002, 10, 0); /* VALU */                    \
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                \
+      if (r_ < 6) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0); /* DS write */     \
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                \
+      if (r_ < 6) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0); /* VMEM read */    \
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                                \
+      if (r_ < 4) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);                    \
+    }                                                                                   \
+  } while (0)
+  W_LOAD(x, 0);
+  W_STORE(x, 0);
+  W_LOAD(x, 1);
+  W_LOAD(y, 2);
+  __syncthreads();
+  for (int kt = 0; kt < nk; kt += 2) {
+    __builtin_amdgcn_sched_barrier(0);
+    W_MMA(0);
+    W_STORE(x, 1);
+    W_LOAD(x, kt + 3);
+    W_PATTERN();
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+    W_MMA(1);
+    W_STORE(y, 0);
+    W_LOAD(y, kt + 4);
+    W_PATTERN();
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+  }
+#undef W_PATTERN
+  __builtin_amdgcn_sched_barrier(0);
+#undef W_LOAD
+#undef W_STORE
+#undef W_MMA
+
+  store_tile<HAS_BETA, false>(
+      a, a.H + grp * a.sH,
+      a.S == 1 ? nullptr : a.P + ((grp * a.tiles + tile) * a.S + split) * (int64_t)(TT * TT), acc,
+      I, J, diag, wm, wn, lh, lr);
 }
 
 // H[I,J] = beta·H + alpha·Σ_s partial_s (fixed order), mirrored for symmetric
@@ -650,7 +863,7 @@ __global__ __launch_bounds__(NTH) void gram256_kernel(G2Args a) {
 template <bool FULL>
 __global__ __launch_bounds__(256) void gram_reduce_kernel(G2Args a) {
   __shared__ float tr[64][65];
-  const int64_t tile = blockIdx.y;
+  const int64_t tile = blockIdx.y, grp = blockIdx.z;  // grp: weighted products' group
   int64_t I, J;
   if (FULL) {
     I = tile / a.nt;
@@ -662,8 +875,8 @@ __global__ __launch_bounds__(256) void gram_reduce_kernel(G2Args a) {
   const int bi = blockIdx.x >> 2, bj = blockIdx.x & 3;  // 64×64 block within the tile
   if (diag && bi > bj) return;                          // strictly below the diagonal
   const bool full = !diag || bi < bj;                    // no element on or below the diagonal
-  const float* __restrict__ P = a.P + tile * a.S * (int64_t)(TT * TT);
-  float* __restrict__ Hm = a.H;
+  const float* __restrict__ P = a.P + (grp * a.tiles + tile) * a.S * (int64_t)(TT * TT);
+  float* __restrict__ Hm = a.H + grp * a.sH;
   const int tid = threadIdx.x;
   const int cq = tid & 15, r0 = tid >> 4;
   const int64_t ti = I * TT + bi * 64, tj = J * TT + bj * 64;  // global block origin
@@ -745,7 +958,7 @@ constexpr int64_t kCUs = 256;  // MI355X
 // Share of the workgroup slots that a grid of n workgroups keeps busy over its waves.
 double wave_fill(int64_t n) { return (double)n / (double)(cdiv(n, kCUs) * kCUs); }
 
-GramPlan gram_plan(int64_t tiles, int64_t K, int halves) {
+GramPlan gram_plan(int64_t tiles, int64_t K, int halves, int64_t max_chain = 0) {
   const int64_t K1 = std::max<int64_t>(K, 1);
   const int64_t smax = std::max<int64_t>(1, std::min<int64_t>(16 / halves, K1 / (KS * 16)));
   int s = 1;
@@ -756,6 +969,7 @@ GramPlan gram_plan(int64_t tiles, int64_t K, int halves) {
       if (wave_fill(tiles * halves * c) > wave_fill(tiles * halves * best) + 1e-9) best = c;
     s = best;
   }
+  while (max_chain > 0 && s * 2 <= smax && cdiv(K1, s) > max_chain) s *= 2;
   const int64_t step = (int64_t)2 * KS * s;
   GramPlan p;
   p.S = s * halves;
@@ -799,21 +1013,46 @@ int64_t product_width(int64_t K, int64_t C, Product pr) {
   return gram_plan(n_tiles(C, pr.full), K, pr.halves).Kp;
 }
 
-// Planes staged per kind (0 Hessian, 1 GPTAQ, 2 weighted with G groups) for
-// an activation of P planes.
+// The weighted kind of bf16 activations runs all G groups in one
+// wgram_kernel launch over tiles·G work items (no operand halves); with P > 1
+// activation planes it stages the hi/lo planes of x·w and runs SYM2 products.
+bool fused_weighted(int kind, int P) { return kind == 2 && P == 1; }
+// Each split of a weighted product is also cut to at most kWChain tokens: its
+// fp32 accumulators take two MFMA updates (hi, lo) per 16 tokens, and the
+// rounding error grows with the chain (measured on MI355X at C = 14336 over
+// 65536 tokens: 6.8e-6 of fp64 for one 65536-token chain; 32768-token
+// chains keep it at the plane-staged path's level).
+constexpr int64_t kWChain = 32768;
+GramPlan wplan(int64_t K, int64_t C, int64_t G) {
+  return gram_plan(n_tiles(C, false) * G, K, 1, kWChain);
+}
+
+// Feature planes (Cp rows) staged per kind (0 Hessian, 1 GPTAQ, 2 weighted
+// with G groups) for an activation of P planes.
 int64_t kind_planes(int kind, int64_t G, int P = 1) {
+  if (fused_weighted(kind, P)) return 1;
   return P + (kind == 1 ? 2 : kind == 2 ? 2 * G : 0);
 }
 
+int64_t padded_features(int64_t C) { return cdiv(C, TT) * TT; }
+
+// Rows of ldt bf16 elements a kind's staged buffer holds: its planes, and for
+// the fused weighted kind the G fp32 weight rows (2G bf16 rows) after them.
+int64_t kind_height(int kind, int64_t C, int64_t G, int P = 1) {
+  return kind_planes(kind, G, P) * padded_features(C) + (fused_weighted(kind, P) ? 2 * G : 0);
+}
+
 // Staged token width and Gram workspace a kind needs for K tokens.
-int64_t kind_width(int kind, int64_t K, int64_t C, int P = 1) {
+int64_t kind_width(int kind, int64_t K, int64_t C, int P = 1, int64_t G = 1) {
   if (kind == 0) return product_width(K, C, x_product(P));
   if (kind == 1) return std::max(product_width(K, C, x_product(P)), product_width(K, C, FULL2));
+  if (fused_weighted(kind, P)) return wplan(K, C, G).Kp;
   return product_width(K, C, SYM2);
 }
-size_t kind_gram_ws(int kind, int64_t K, int64_t C, int P = 1) {
+size_t kind_gram_ws(int kind, int64_t K, int64_t C, int P = 1, int64_t G = 1) {
   if (kind == 0) return product_ws(K, C, x_product(P));
   if (kind == 1) return std::max(product_ws(K, C, x_product(P)), product_ws(K, C, FULL2));
+  if (fused_weighted(kind, P)) return plan_ws_bytes(n_tiles(C, false) * G, wplan(K, C, G));
   return product_ws(K, C, SYM2);
 }
 
@@ -842,6 +1081,7 @@ int run_product(hipStream_t st, Product pr, const uint16_t* A1, const uint16_t* 
   G2Args a{};
   a.A1 = A1; a.A2 = A2; a.A3 = A3; a.B = B; a.ldt = ldt; a.kc = p.kc; a.nt = nt; a.tiles = tiles; a.C = C;
   a.S = p.S; a.halves = pr.halves; a.alpha = alpha; a.beta = beta; a.H = out; a.ldh = ldo;
+  a.G = 1;
   if (p.S > 1) {
     const size_t need = plan_ws_bytes(tiles, p);
     G2PTQ_CHECK(ws != nullptr && ws_bytes >= need, "hessian gram: workspace %zu < %zu", ws_bytes,
@@ -868,7 +1108,42 @@ int run_product(hipStream_t st, Product pr, const uint16_t* A1, const uint16_t* 
   return G2PTQ_OK;
 }
 
-int64_t padded_features(int64_t C) { return cdiv(C, TT) * TT; }
+// H[g] = beta·H[g] + alpha·Σ_t x_t·(x_t·w[g][t])ᵀ for the G groups, from
+// Xᵀ and the weight rows W (G × ldw fp32); both zero from token
+// roundup(K, 64) up to wplan(K, C, G).Kp.
+int run_wproduct(hipStream_t st, const uint16_t* XT, const float* W, int64_t ldw, int64_t ldt,
+                 int64_t K, int64_t C, int64_t G, float alpha, float beta, float* H, int64_t ldh,
+                 int64_t sH, void* ws, size_t ws_bytes) {
+  const int64_t nt = cdiv(C, TT);
+  const int64_t tiles = n_tiles(C, false);
+  const GramPlan p = wplan(K, C, G);
+  G2PTQ_CHECK(p.Kp <= ldt && p.Kp <= ldw, "hessian gram: staged operand too narrow (%lld < %lld)",
+              (long long)std::min(ldt, ldw), (long long)p.Kp);
+  G2PTQ_CHECK(tiles * G * p.S < (1ll << 31) && tiles < 65536 && G <= 65535,
+              "hessian gram: grid too large");
+  G2PTQ_CHECK((reinterpret_cast<uintptr_t>(W) & 15) == 0 && ldw % 4 == 0,
+              "hessian gram: weights must be 16-byte aligned with ldw a multiple of 4");
+  G2Args a{};
+  a.B = XT; a.ldt = ldt; a.kc = p.kc; a.nt = nt; a.tiles = tiles; a.C = C;
+  a.S = p.S; a.halves = 1; a.alpha = alpha; a.beta = beta; a.H = H; a.ldh = ldh;
+  a.W = W; a.ldw = ldw; a.G = G; a.sH = sH;
+  if (p.S > 1) {
+    const size_t need = plan_ws_bytes(tiles * G, p);
+    G2PTQ_CHECK(ws != nullptr && ws_bytes >= need, "hessian gram: workspace %zu < %zu", ws_bytes,
+                need);
+    a.P = static_cast<float*>(ws);
+  }
+  const dim3 grid((unsigned)(tiles * G * p.S));
+  if (p.S == 1 && beta != 0.f) hipLaunchKernelGGL(wgram_kernel<true>, grid, dim3(NTH), 0, st, a);
+  else hipLaunchKernelGGL(wgram_kernel<false>, grid, dim3(NTH), 0, st, a);
+  G2PTQ_LAUNCHED();
+  if (p.S > 1) {
+    hipLaunchKernelGGL(gram_reduce_kernel<false>, dim3(16, (unsigned)tiles, (unsigned)G), dim3(256),
+                       0, st, a);
+    G2PTQ_LAUNCHED();
+  }
+  return G2PTQ_OK;
+}
 
 int stage(hipStream_t st, int kind, const uint16_t* X, const uint16_t* F, const float* S,
           int64_t T, int64_t C, int64_t ldx, int64_t ldf, int64_t G, int64_t lds, float s_scale,
@@ -932,10 +1207,16 @@ int gram_kind(hipStream_t st, int kind, uint16_t* XT, int64_t ldt, int64_t K, in
   G2PTQ_TRY(check_gram_args(XT, ldt, K, C));
   const int64_t Cp = padded_features(C);
   const int64_t plane = Cp * ldt;
-  const int64_t width = kind_width(kind, K, C, P);
+  const int64_t width = kind_width(kind, K, C, P, G);
   G2PTQ_CHECK(width <= ldt, "hessian gram: staged operand too narrow (%lld < %lld)",
               (long long)ldt, (long long)width);
   G2PTQ_TRY(zero_pad(st, XT, ldt, kind_planes(kind, G, P) * Cp, K, width));
+  if (fused_weighted(kind, P)) {
+    // the weight rows, as 2G rows of 2·ldt bf16 elements
+    G2PTQ_TRY(zero_pad(st, XT + plane, 2 * ldt, G, 2 * K, 2 * width));
+    return run_wproduct(st, XT, reinterpret_cast<const float*>(XT + plane), ldt, ldt, K, C, G,
+                        alpha, beta, H, ldh, sH, ws, ws_bytes);
+  }
   const uint16_t* Xq[3] = {XT, XT + plane, XT + 2 * plane};
   // every product over the column planes q = 0..P−1: the first applies beta,
   // the others add to it
@@ -960,11 +1241,10 @@ int gram_kind(hipStream_t st, int kind, uint16_t* XT, int64_t ldt, int64_t K, in
 // One-shot updates (stage + Gram) through a caller workspace laid out as
 // [staged planes: planes × Cp × width bf16][split partials].
 size_t staged_bytes(int kind, int64_t T, int64_t C, int64_t G, int P = 1) {
-  return ((size_t)kind_planes(kind, G, P) * padded_features(C) * kind_width(kind, T, C, P) * 2 +
-          255) / 256 * 256;
+  return ((size_t)kind_height(kind, C, G, P) * kind_width(kind, T, C, P, G) * 2 + 255) / 256 * 256;
 }
 size_t update_ws_bytes(int kind, int64_t T, int64_t C, int64_t G) {
-  return staged_bytes(kind, T, C, G) + kind_gram_ws(kind, T, C);
+  return staged_bytes(kind, T, C, G) + kind_gram_ws(kind, T, C, 1, G);
 }
 
 }  // namespace
@@ -1028,7 +1308,7 @@ extern "C" int g2ptq_weighted_hessian_update(void* stream, const uint16_t* X, in
   G2PTQ_CHECK(ws != nullptr && ws_bytes >= need, "weighted_hessian_update: workspace %zu < %zu",
               ws_bytes, need);
   hipStream_t st = as_stream(stream);
-  const int64_t ldt = kind_width(2, T, C);
+  const int64_t ldt = kind_width(2, T, C, 1, G);
   uint16_t* XT = static_cast<uint16_t*>(ws);
   const size_t xt = staged_bytes(2, T, C, G);
   G2PTQ_TRY(stage(st, 2, X, nullptr, S, T, C, ldx, 0, G, lds, 1.f, XT, ldt, 0));
@@ -1096,9 +1376,10 @@ extern "C" int g2ptq_weighted_stage(void* stream, const uint16_t* X, int64_t T, 
   return act_square(st, XT, ldt, t_off, T, C, act, act_alpha, act_beta);
 }
 
-extern "C" int g2ptq_weighted_gram_workspace(int64_t K, int64_t C, size_t* bytes) {
-  G2PTQ_CHECK(bytes != nullptr && C > 0 && K >= 0, "weighted_gram_workspace: bad arguments");
-  *bytes = kind_gram_ws(2, K, C);
+extern "C" int g2ptq_weighted_gram_workspace(int64_t K, int64_t C, int64_t G, size_t* bytes) {
+  G2PTQ_CHECK(bytes != nullptr && C > 0 && K >= 0 && G >= 1 && G <= 64,
+              "weighted_gram_workspace: bad arguments");
+  *bytes = kind_gram_ws(2, K, C, 1, G);
   return G2PTQ_OK;
 }
 
@@ -1117,6 +1398,15 @@ extern "C" int g2ptq_hessian_stage_planes(int kind, int dtype, int64_t G, int64_
                   (kind != 2 || (G >= 1 && G <= 64)),
               "hessian_stage_planes: bad arguments");
   *planes = kind_planes(kind, G, dtype_planes(dtype));
+  return G2PTQ_OK;
+}
+
+extern "C" int g2ptq_hessian_stage_height(int kind, int dtype, int64_t C, int64_t G,
+                                          int64_t* rows) {
+  G2PTQ_CHECK(rows != nullptr && kind >= 0 && kind <= 2 && dtype >= 0 && dtype <= 2 && C > 0 &&
+                  C <= (1ll << 20) && (kind != 2 || (G >= 1 && G <= 64)),
+              "hessian_stage_height: bad arguments");
+  *rows = kind_height(kind, C, G, dtype_planes(dtype));
   return G2PTQ_OK;
 }
 
@@ -1142,9 +1432,9 @@ extern "C" int g2ptq_hessian_stage_ex(void* stream, int kind, int dtype, const v
 extern "C" int g2ptq_hessian_gram_ex_workspace(int kind, int dtype, int64_t K, int64_t C,
                                                int64_t G, size_t* bytes) {
   G2PTQ_CHECK(bytes != nullptr && kind >= 0 && kind <= 2 && dtype >= 0 && dtype <= 2 && C > 0 &&
-                  K >= 0,
+                  K >= 0 && (kind != 2 || (G >= 1 && G <= 64)),
               "hessian_gram_ex_workspace: bad arguments");
-  *bytes = kind_gram_ws(kind, K, C, dtype_planes(dtype));
+  *bytes = kind_gram_ws(kind, K, C, dtype_planes(dtype), G);
   return G2PTQ_OK;
 }
 

@@ -146,19 +146,22 @@ int g2ptq_weighted_hessian_update(void* stream, const uint16_t* X, int64_t T, in
                                   float* act, float act_alpha, float act_beta,
                                   void* ws, size_t ws_bytes);
 
-/* Staged weighted accumulation.  XT holds 1 + 2G contiguous planes of
- * rows × ldt bf16: Xᵀ, then for each group g the bf16 high and low parts of
- * (x·S[t,g]·s_scale)ᵀ; s_scale folds a per-batch factor (G2PTQ's 1/T_b)
- * into the staged tokens.  g2ptq_weighted_stage also applies the act update
- * of g2ptq_weighted_hessian_update for the batch.  g2ptq_weighted_gram
- * applies H[g] = beta·H[g] + alpha·Σ over the first K staged columns.  Same
+/* Staged weighted accumulation.  XT holds Xᵀ (rows × ldt bf16, rows =
+ * g2ptq_hessian_stage_rows(C)) followed by G rows of ldt fp32 token weights
+ * w[g][t] = S[t,g]·s_scale (the memory of 2G more bf16 rows:
+ * g2ptq_hessian_stage_height(2, 0, C, G, ·) rows of ldt bf16 in all); s_scale
+ * folds a per-batch factor (G2PTQ's 1/T_b) into the staged tokens.
+ * g2ptq_weighted_stage also applies the act update of
+ * g2ptq_weighted_hessian_update for the batch.  g2ptq_weighted_gram applies
+ * H[g] = beta·H[g] + alpha·Σ_t x_t·(x_t·w[g][t])ᵀ over the first K staged
+ * columns, all G groups in one launch, and its workspace depends on G.  Same
  * alignment and padding rules as g2ptq_hessian_stage / _gram.  Replace the
  * per-batch updates of G2PTQ.add_batch (gptq_utils/g2ptq_utils.py:182-201)
  * and GPTQGuided.add_batch (gptq_utils/gptq_guided_utils.py:59-81). */
 int g2ptq_weighted_stage(void* stream, const uint16_t* X, int64_t T, int64_t C, int64_t ldx,
                          const float* S, int64_t G, int64_t lds, float s_scale, uint16_t* XT,
                          int64_t ldt, int64_t t_off, float* act, float act_alpha, float act_beta);
-int g2ptq_weighted_gram_workspace(int64_t K, int64_t C, size_t* bytes);
+int g2ptq_weighted_gram_workspace(int64_t K, int64_t C, int64_t G, size_t* bytes);
 int g2ptq_weighted_gram(void* stream, uint16_t* XT, int64_t ldt, int64_t K, int64_t C, int64_t G,
                         float alpha, float beta, float* H, int64_t ldh, int64_t sH, void* ws,
                         size_t ws_bytes);
@@ -169,9 +172,12 @@ int g2ptq_weighted_gram(void* stream, uint16_t* XT, int64_t ldt, int64_t K, int6
  * (inp.float(), gptq_utils/gptq_utils.py:125, gptaq_utils.py:139-146,
  * g2ptq_utils.py:193-201).  X (and Xfp) are T × C of that dtype.  Xᵀ is
  * staged as P bf16 planes that sum to it exactly (P = 1, 2, 3), followed by
- * the kind's planes as above (GPTAQ: hi, lo of X_fp − X; weighted: hi, lo
- * of x·S[t,g]·s_scale per group); g2ptq_hessian_stage_planes gives their
- * count.  g2ptq_hessian_gram_ex runs each product once per plane of Xᵀ as
+ * the kind's planes as above (GPTAQ: hi, lo of X_fp − X; weighted with
+ * P > 1: hi, lo of x·S[t,g]·s_scale per group; weighted bf16: the weight
+ * rows of g2ptq_weighted_stage); g2ptq_hessian_stage_planes gives the count
+ * of feature planes (rows × ldt each) and g2ptq_hessian_stage_height the
+ * buffer's height in rows of ldt bf16 (planes × rows, plus the bf16
+ * weighted kind's 2G).  g2ptq_hessian_gram_ex runs each product once per plane of Xᵀ as
  * its column operand (the plain Hessian's row operand is all P planes),
  * accumulating: the same H / Dx / H[g] updates as g2ptq_hessian_gram,
  * g2ptq_gptaq_gram and g2ptq_weighted_gram (whose bf16 paths these equal
@@ -180,6 +186,7 @@ int g2ptq_weighted_gram(void* stream, uint16_t* XT, int64_t ldt, int64_t K, int6
  * padding rules as g2ptq_hessian_stage / _gram; act (kind 2) as in
  * g2ptq_weighted_stage. */
 int g2ptq_hessian_stage_planes(int kind, int dtype, int64_t G, int64_t* planes);
+int g2ptq_hessian_stage_height(int kind, int dtype, int64_t C, int64_t G, int64_t* rows);
 int g2ptq_hessian_stage_ex(void* stream, int kind, int dtype, const void* X, const void* Xfp,
                            int64_t T, int64_t C, int64_t ldx, int64_t ldxf, const float* S,
                            int64_t G, int64_t lds, float s_scale, uint16_t* XT, int64_t ldt,

@@ -55,25 +55,34 @@ def test_size_queries(lib):
     assert _lib.query_size("g2ptq_trust_region_workspace", 4, 256, 4096) > 0
     assert _lib.query_size("g2ptq_hessian_workspace", 8192, 4096, 0, 0) > 0
     assert _lib.query_size("g2ptq_hessian_gram_workspace", 32768, 4096) >= 0
-    # GPTAQ stages 3 planes and the weighted update 1 + 2G; both need split partials
+    # GPTAQ stages 3 planes and the weighted update Xᵀ plus G weight rows; both
+    # need split partials (the weighted ones for all G groups)
     h = _lib.query_size("g2ptq_hessian_workspace", 8192, 4096, 0, 0)
     assert _lib.query_size("g2ptq_hessian_workspace", 8192, 4096, 1, 0) > h
     assert (_lib.query_size("g2ptq_hessian_workspace", 8192, 4096, 2, 4)
             > _lib.query_size("g2ptq_hessian_workspace", 8192, 4096, 2, 1))
     assert _lib.query_size("g2ptq_gptaq_gram_workspace", 32768, 4096) > 0
-    assert _lib.query_size("g2ptq_weighted_gram_workspace", 32768, 4096) > 0
+    assert (_lib.query_size("g2ptq_weighted_gram_workspace", 32768, 4096, 4)
+            > _lib.query_size("g2ptq_weighted_gram_workspace", 32768, 4096, 1) > 0)
     rows = _lib.query_size_i64("g2ptq_hessian_stage_rows", 4096)
     assert rows >= 4096 and rows % 256 == 0
     # any-dtype staging: Xᵀ takes 1 / 2 / 3 bf16 planes for bf16 / fp16 / fp32
     planes = lambda kind, dt, G=0: _lib.query_size_i64("g2ptq_hessian_stage_planes", kind, dt, G)
     assert [planes(0, dt) for dt in (0, 1, 2)] == [1, 2, 3]
     assert [planes(1, dt) for dt in (0, 1, 2)] == [3, 4, 5]
-    assert [planes(2, dt, 4) for dt in (0, 1, 2)] == [9, 10, 11]
+    assert [planes(2, dt, 4) for dt in (0, 1, 2)] == [1, 10, 11]
+    # buffer heights in rows of bf16: planes × rows, and the bf16 weighted
+    # kind's G fp32 weight rows (2G bf16 rows)
+    height = lambda kind, dt, G=0: _lib.query_size_i64("g2ptq_hessian_stage_height", kind, dt,
+                                                       4096, G)
+    assert [height(0, dt) for dt in (0, 1, 2)] == [rows, 2 * rows, 3 * rows]
+    assert height(1, 0) == 3 * rows
+    assert [height(2, dt, 4) for dt in (0, 1, 2)] == [rows + 8, 10 * rows, 11 * rows]
     ex = lambda kind, dt: _lib.query_size("g2ptq_hessian_gram_ex_workspace", kind, dt, 32768, 4096,
                                           4 if kind == 2 else 0)
     assert ex(0, 0) == _lib.query_size("g2ptq_hessian_gram_workspace", 32768, 4096)
     assert ex(1, 0) == _lib.query_size("g2ptq_gptaq_gram_workspace", 32768, 4096)
-    assert ex(2, 0) == _lib.query_size("g2ptq_weighted_gram_workspace", 32768, 4096)
+    assert ex(2, 0) == _lib.query_size("g2ptq_weighted_gram_workspace", 32768, 4096, 4)
     assert ex(0, 1) > 0 and ex(0, 2) > 0
 
 
@@ -83,6 +92,8 @@ def test_size_queries(lib):
     ("g2ptq_weighted_gram", (None, None, 64, 0, 128, 0, 1.0, 0.0, None, 128, 0, None, 0)),
     ("g2ptq_gptaq_stage", (None, None, None, 8, 128, 128, 128, None, 64, 0)),
     ("g2ptq_hessian_stage_planes", (0, 3, 0, None)),
+    ("g2ptq_hessian_stage_height", (2, 0, 4096, 0, None)),
+    ("g2ptq_weighted_gram_workspace", (4096, 4096, 0, None)),
     ("g2ptq_hessian_stage_ex", (None, 0, 5, None, None, 8, 128, 128, 128, None, 0, 0, 1.0, None,
                                 64, 0, None, 0.0, 1.0)),
     ("g2ptq_hessian_stage_ex", (None, 1, 1, None, None, 8, 128, 128, 128, None, 0, 0, 1.0, None,

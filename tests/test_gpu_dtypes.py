@@ -168,11 +168,13 @@ def test_any_dtype_entry_points_equal_bf16_ones(dev, kind):
     rows = _lib.query_size_i64("g2ptq_hessian_stage_rows", Ck)
     Gq = Gk if kind == 2 else 0
     planes = _lib.query_size_i64("g2ptq_hessian_stage_planes", kind, 0, Gq)
-    assert planes == {0: 1, 1: 3, 2: 1 + 2 * Gk}[kind]
+    assert planes == {0: 1, 1: 3, 2: 1}[kind]
+    height = _lib.query_size_i64("g2ptq_hessian_stage_height", kind, 0, Ck, Gq)
+    assert height == planes * rows + (2 * Gk if kind == 2 else 0)
     ldt = 8192
     outs = []
     for ex in (False, True):
-        XT = torch.zeros(planes, rows, ldt, dtype=torch.bfloat16, device=dev)
+        XT = torch.zeros(height, ldt, dtype=torch.bfloat16, device=dev)
         H = torch.full((max(Gq, 1), Ck, Ck), 0.5, device=dev)
         Dx = torch.full((Ck, Ck), 0.25, device=dev)
         act = torch.full((Ck,), 2.0, device=dev)
@@ -195,7 +197,8 @@ def test_any_dtype_entry_points_equal_bf16_ones(dev, kind):
                 _lib.call("g2ptq_weighted_stage", st, p(X), Tk, Ck, Ck, p(S), Gk, Gk, 0.5, p(XT),
                           ldt, 0, p(act), 0.25, 0.75)
                 name = "g2ptq_weighted_gram_workspace"
-            ws = torch.empty(max(_lib.query_size(name, Tk, Ck), 256), dtype=torch.uint8,
+            qargs = (Tk, Ck, Gk) if kind == 2 else (Tk, Ck)
+            ws = torch.empty(max(_lib.query_size(name, *qargs), 256), dtype=torch.uint8,
                              device=dev)
             if kind == 0:
                 _lib.call("g2ptq_hessian_gram", st, p(XT), ldt, Tk, Ck, 0.125, 0.5, p(H), Ck,

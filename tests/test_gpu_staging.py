@@ -85,10 +85,11 @@ def test_staged_hessian_feeds_fasterquant_and_free(dev):
     gq.free()
 
 
-def _small_budget(monkeypatch, C, planes, tokens=8192):
+def _small_budget(monkeypatch, C, kind, G=0, tokens=8192):
+    """A staging budget of ``tokens`` token columns of the kind's layout."""
     from g2ptq_amd import _lib, _stage
-    rows = _lib.query_size_i64("g2ptq_hessian_stage_rows", C)
-    monkeypatch.setattr(_stage, "DEFAULT_BUDGET", planes * rows * 2 * tokens)
+    height = _lib.query_size_i64("g2ptq_hessian_stage_height", kind, 0, C, G)
+    monkeypatch.setattr(_stage, "DEFAULT_BUDGET", height * 2 * tokens)
 
 
 # (bsz, T) batches: overflow the 8192-token staging buffer (flush), grow it, and
@@ -101,7 +102,7 @@ def test_staged_gptaq_across_flushes_growth_and_reads(dev, monkeypatch):
     reference's per-batch update of H and dXXT (gptaq_utils.py:130-148)."""
     from g2ptq_amd import GPTAQ
     C, B = 640, 2
-    _small_budget(monkeypatch, C, 3, tokens=4096)
+    _small_budget(monkeypatch, C, 1, tokens=4096)
     gq = GPTAQ(_layers(B, 64, C, dev))
     st = ohess.gptaq_state(B, C)
     g = gen(78)
@@ -134,11 +135,12 @@ def _weighted_close(Hd, Hr, what):
 
 
 def test_staged_g2ptq_across_flushes_growth_and_reads(dev, monkeypatch):
-    """G2PTQ.add_batch staged (per-batch 1/T_b folded into the hi/lo planes of
-    x·s) equals the reference's running per-batch mean (g2ptq_utils.py:182-201)."""
+    """G2PTQ.add_batch staged (per-batch 1/T_b folded into the staged token
+    weights) equals the reference's running per-batch mean
+    (g2ptq_utils.py:182-201)."""
     from g2ptq_amd import G2PTQ
     C, B, G = 384, 2, 4
-    _small_budget(monkeypatch, C, 1 + 2 * G, tokens=4096)
+    _small_budget(monkeypatch, C, 2, G, tokens=4096)
     g = gen(79)
     shapes = [(1, 700), (1, 2048), (1, 300), (1, 2500), (1, 5000), (1, 512), (1, 64), (1, 1)]
     xs = [(torch.randn(T, C, generator=g) * 2).bfloat16() for _, T in shapes]
@@ -168,7 +170,7 @@ def test_staged_guided_across_flushes(dev, monkeypatch):
     (gptq_guided_utils.py:59-81)."""
     from g2ptq_amd import GPTQGuided
     C, G, seq = 320, 2, 600
-    _small_budget(monkeypatch, C, 1 + 2 * G, tokens=4096)
+    _small_budget(monkeypatch, C, 2, G, tokens=4096)
     g = gen(80)
     N = 12
     x = torch.randn(N, seq, C, generator=g).bfloat16()
