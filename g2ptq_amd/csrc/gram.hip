@@ -958,9 +958,11 @@ constexpr int64_t kCUs = 256;  // MI355X
 // Share of the workgroup slots that a grid of n workgroups keeps busy over its waves.
 double wave_fill(int64_t n) { return (double)n / (double)(cdiv(n, kCUs) * kCUs); }
 
-GramPlan gram_plan(int64_t tiles, int64_t K, int halves, int64_t max_chain = 0) {
+GramPlan gram_plan(int64_t tiles, int64_t K, int halves, int64_t max_chain = 0,
+                   int64_t max_s = 16) {
   const int64_t K1 = std::max<int64_t>(K, 1);
-  const int64_t smax = std::max<int64_t>(1, std::min<int64_t>(16 / halves, K1 / (KS * 16)));
+  const int64_t smax =
+      std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(16 / halves, max_s), K1 / (KS * 16)));
   int s = 1;
   while (s * 2 <= smax && tiles * halves * s < 4096) s *= 2;
   {
@@ -1021,10 +1023,16 @@ bool fused_weighted(int kind, int P) { return kind == 2 && P == 1; }
 // fp32 accumulators take two MFMA updates (hi, lo) per 16 tokens, and the
 // rounding error grows with the chain (measured on MI355X at C = 14336 over
 // 65536 tokens: 6.8e-6 of fp64 for one 65536-token chain; 32768-token
-// chains keep it at the plane-staged path's level).
+// chains keep it at the plane-staged path's level).  The split partials of
+// one flush stay within kWBudget (config 3's C = 14336 flush: 8 splits,
+// 13.4 GB): a wider product (many groups at a large C) takes fewer, longer
+// splits, down to one with no partials at all.
 constexpr int64_t kWChain = 32768;
+constexpr int64_t kWBudget = int64_t(16) << 30;
 GramPlan wplan(int64_t K, int64_t C, int64_t G) {
-  return gram_plan(n_tiles(C, false) * G, K, 1, kWChain);
+  const int64_t items = n_tiles(C, false) * G;
+  const int64_t max_s = std::max<int64_t>(1, kWBudget / (items * TT * TT * 4));
+  return gram_plan(items, K, 1, kWChain, max_s);
 }
 
 // Feature planes (Cp rows) staged per kind (0 Hessian, 1 GPTAQ, 2 weighted
