@@ -10,11 +10,13 @@
 // batch into planes of (Cp × ldt) bf16 (features × tokens, zero padded: Cp a
 // multiple of 256, staged token counts multiples of 64), so both MFMA operands
 // of an output tile read K-contiguous rows.  Plane 0 is Xᵀ.  Operands that are
-// not bf16-exact are staged as two bf16 planes, hi = bf16(v) and
+// not bf16-exact are split into two bf16 parts, hi = bf16(v) and
 // lo = bf16(v − hi), which carry 16 significant bits (the residual is below
-// 2⁻¹⁶·|v|): for GPTAQ v = x_fp − x (exact in fp32), for the weighted
-// Hessians v = x·s[t,g]·s_scale.  A product v·x is then the two exact bf16
-// products hi·x + lo·x, accumulated in fp32.
+// 2⁻¹⁶·|v|): GPTAQ stages v = x_fp − x (exact in fp32) as two planes; the
+// weighted Hessians stage one fp32 weight per (group, token) and
+// wgram_kernel forms v = x·s[t,g]·s_scale and its split on the way into LDS
+// (fp16/fp32 activations stage the split as planes).  A product v·x is then
+// the two exact bf16 products hi·x + lo·x, accumulated in fp32.
 //
 // Kernel shape (gram256_kernel):
 //   * one workgroup = 8 wave64s = one 256×256 output tile; wave (wm, wn) in a
@@ -662,9 +664,8 @@ __global__ __launch_bounds__(NTH) void gram256_kernel(G2Args a) {
 // over the upper tiles of every group g, one launch for all groups.  The row
 // operand is Xᵀ (panel I).  The column operand v = x·w (panel J) is formed per
 // stage from Xᵀ and the staged weights, split in registers into bf16
-// hi = bf16(v) and lo = bf16(v − hi) (the values the hi/lo planes of the
-// plane-staged path hold), written to LDS as two tiles, and both are
-// multiplied into the same accumulator.  One workgroup = one (tile, group,
+// hi = bf16(v) and lo = bf16(v − hi) (split_chunk), written to LDS as two
+// tiles, and both are multiplied into the same accumulator.  One workgroup = one (tile, group,
 // split); a tile's groups are consecutive in the work list, so they run
 // together on one XCD and read the same two panels through its L2.
 //   * 8 waves in a 2 × 4 grid, 128×64 per wave (the gram256 epilogue);
