@@ -24,7 +24,10 @@
 // Shape: a workgroup (4 wave64s, two per CU) computes a 128×128 tile (64×64
 // for small grids); each wave a quadrant made of 32×32 MFMA blocks.  K advances
 // in slabs of 32 through double-buffered LDS with 16-byte global loads for
-// two slabs in flight, interleaved with the MFMAs of the current slab.
+// two slabs in flight, interleaved with the MFMAs of the current slab.  Large
+// split products with B given N×K (a grid of at least 256 tiles of 256×256,
+// K >= 384) take an 8-wave 256×256 workgroup instead, which halves the LDS
+// reads and barriers per MFMA and sums the same products in the same order.
 //
 // Operand layout: a 32x32x2 MFMA takes one k per lane half, so a slab's k
 // order is permuted: for k-octet o, lane half h holds k = 8o + 4h + j in the
@@ -552,6 +555,209 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmF32 g, int64_t tm,
   }
 }
 
+// Large split products (K >= 384, B given N×K, no triangular skipping, a grid
+// of at least a wave of 256×256 tiles): one workgroup of 8 waves computes a
+// 256×256 tile, each wave 128×64 (4×2 blocks of 32×32), from 16-k stages of
+// both operands split into three bf16 planes as they are stored to LDS.  Per
+// stage a wave reads 12 row and 6 column fragments for 48 MFMAs (the 128×128
+// kernel: 12 for 24) and a workgroup splits 16 elements per thread for twice
+// the MFMAs per barrier.  Each accumulator receives the same six products in
+// the same order, stage by stage, as gemm_f32_kernel's split path, so the
+// results equal it bit for bit.
+constexpr int S2T = 256;  // tile edge
+template <bool VEC>
+__global__ __launch_bounds__(512) void gemm_s256_kernel(GemmF32 g, int64_t tm, int64_t tn) {
+  constexpr int PL = S2T * SP;  // bf16 per plane
+  __shared__ __attribute__((aligned(16))) __bf16 Ap[2][3][PL];
+  __shared__ __attribute__((aligned(16))) __bf16 Bp[2][3][PL];
+
+  const int z = blockIdx.z;
+  const int64_t b1 = z / g.batch2, b2 = z % g.batch2;
+  if (g.skip && g.skip[b1]) return;
+  const int64_t nwg = gridDim.x, bid = blockIdx.x;
+  const int64_t q8 = nwg >> 3, r8 = nwg & 7, xcd = bid & 7;
+  const int64_t id = xcd * q8 + (xcd < r8 ? xcd : r8) + (bid >> 3);
+  int64_t im, in;
+  tile_of(id, tm, tn, im, in);
+  const int64_t m0 = im * S2T, n0 = in * S2T;
+  if (g.uplo == 1 && n0 > m0 + S2T - 1) return;
+  if (g.uplo == 2 && m0 > n0 + S2T - 1) return;
+
+  const float* __restrict__ A = g.A + b1 * g.sA + b2 * g.sA2;
+  const float* __restrict__ B = g.B + b1 * g.sB + b2 * g.sB2;
+  const int64_t M = g.M, N = g.N, K = g.K;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 2, wn = wave & 3;
+
+  auto ld4 = [&](const float* base, int64_t ld, int64_t r, int64_t c, int64_t R, int64_t Ccols) {
+    if (VEC) {
+      const bool ok = r < R && c < Ccols;
+      const uint4 w = *reinterpret_cast<const uint4*>(base + (ok ? r * ld + c : 0));
+      const uint32_t m = ok ? 0xffffffffu : 0u;
+      return make_float4(__uint_as_float(w.x & m), __uint_as_float(w.y & m),
+                         __uint_as_float(w.z & m), __uint_as_float(w.w & m));
+    }
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (r < R) {
+      const float* p = base + r * ld + c;
+      if (c < Ccols) v.x = p[0];
+      if (c + 1 < Ccols) v.y = p[1];
+      if (c + 2 < Ccols) v.z = p[2];
+      if (c + 3 < Ccols) v.w = p[3];
+    }
+    return v;
+  };
+
+  // Stage = 16 k: row r of a tile as four 4-k quads; thread tid holds quads
+  // (tid >> 2) + 128 i of both operands.
+  const int sa_row = tid >> 2, sa_kq = (tid & 3) * 4;
+  float4 xa0, xa1, xb0, xb1, ya0, ya1, yb0, yb1;
+#define S2_LOAD(R, st)                                                                         \
+  do {                                                                                         \
+    const int64_t k0_ = (int64_t)(st) * SK;                                                    \
+    R##a0 = ld4(A, g.lda, m0 + sa_row, k0_ + sa_kq, M, K);                                     \
+    R##a1 = ld4(A, g.lda, m0 + sa_row + 128, k0_ + sa_kq, M, K);                               \
+    R##b0 = ld4(B, g.ldb, n0 + sa_row, k0_ + sa_kq, N, K);                                     \
+    R##b1 = ld4(B, g.ldb, n0 + sa_row + 128, k0_ + sa_kq, N, K);                               \
+  } while (0)
+#define S2_PUT(P, buf, row, v)                                                                 \
+  do {                                                                                         \
+    bf16x4 h_, m_, l_;                                                                         \
+    split4((v), h_, m_, l_);                                                                   \
+    const int o_ = (row) * SP + sa_kq;                                                         \
+    *reinterpret_cast<bf16x4*>(&P[(buf)][0][o_]) = h_;                                         \
+    *reinterpret_cast<bf16x4*>(&P[(buf)][1][o_]) = m_;                                         \
+    *reinterpret_cast<bf16x4*>(&P[(buf)][2][o_]) = l_;                                         \
+  } while (0)
+#define S2_STORE(R, buf)                                                                       \
+  do {                                                                                         \
+    S2_PUT(Ap, buf, sa_row, R##a0);                                                            \
+    S2_PUT(Ap, buf, sa_row + 128, R##a1);                                                      \
+    S2_PUT(Bp, buf, sa_row, R##b0);                                                            \
+    S2_PUT(Bp, buf, sa_row + 128, R##b1);                                                      \
+  } while (0)
+
+  f32x16 acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  const int lr = lane & 31, lh = lane >> 5;
+  // The six cross products in gemm_f32_kernel's order, per accumulator.
+#define S2_MMA(buf)                                                                            \
+  do {                                                                                         \
+    bf16x8 bh[2], bm[2], bl[2];                                                                \
+    _Pragma("unroll") for (int j = 0; j < 2; ++j) {                                            \
+      const int o_ = (wn * 64 + j * 32 + lr) * SP + lh * 8;                                    \
+      bh[j] = *reinterpret_cast<const bf16x8*>(&Bp[(buf)][0][o_]);                             \
+      bm[j] = *reinterpret_cast<const bf16x8*>(&Bp[(buf)][1][o_]);                             \
+      bl[j] = *reinterpret_cast<const bf16x8*>(&Bp[(buf)][2][o_]);                             \
+    }                                                                                          \
+    _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                            \
+      const int o_ = (wm * 128 + i * 32 + lr) * SP + lh * 8;                                   \
+      const bf16x8 ah = *reinterpret_cast<const bf16x8*>(&Ap[(buf)][0][o_]);                   \
+      const bf16x8 am = *reinterpret_cast<const bf16x8*>(&Ap[(buf)][1][o_]);                   \
+      const bf16x8 al = *reinterpret_cast<const bf16x8*>(&Ap[(buf)][2][o_]);                   \
+      _Pragma("unroll") for (int j = 0; j < 2; ++j) {                                          \
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bh[j], acc[i][j], 0, 0, 0);     \
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bl[j], acc[i][j], 0, 0, 0);     \
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, bm[j], acc[i][j], 0, 0, 0);     \
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, bh[j], acc[i][j], 0, 0, 0);     \
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bm[j], acc[i][j], 0, 0, 0);     \
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bh[j], acc[i][j], 0, 0, 0);     \
+      }                                                                                        \
+    }                                                                                          \
+  } while (0)
+
+  // Stage t is multiplied out of buffer t&1 while stage t+1 goes from its
+  // register set to the other buffer and that set loads stage t+3; stages
+  // past K load zeros and skip their MFMAs.  One barrier per stage.
+  const int nk = (int)cdiv(K, (int64_t)SK);
+  S2_LOAD(x, 0);
+  S2_STORE(x, 0);
+  S2_LOAD(x, 1);
+  S2_LOAD(y, 2);
+  __syncthreads();
+  for (int kt = 0; kt < nk; kt += 2) {
+    __builtin_amdgcn_sched_barrier(0);
+    S2_MMA(0);
+    S2_STORE(x, 1);
+    S2_LOAD(x, kt + 3);
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+    if (kt + 1 < nk) {
+      __builtin_amdgcn_sched_barrier(0);
+      S2_MMA(1);
+      S2_STORE(y, 0);
+      S2_LOAD(y, kt + 4);
+      __builtin_amdgcn_sched_barrier(0);
+      __syncthreads();
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#undef S2_LOAD
+#undef S2_PUT
+#undef S2_STORE
+#undef S2_MMA
+
+  // Epilogue as gemm_f32_kernel's: the inputs of a row of blocks are loaded
+  // before any of its outputs is stored (C / X may alias D).
+  const float* C = g.C ? g.C + b1 * g.sC + b2 * g.sC2 : nullptr;
+  const float* X = g.X ? g.X + b1 * g.sX + b2 * g.sX2 : nullptr;
+  float* D = g.D + b1 * g.sD + b2 * g.sD2;
+  const bool use_c = g.beta != 0.f, use_x = g.gamma != 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float cv[2][16];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int64_t n = n0 + wn * 64 + j * 32 + lr;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t m = m0 + wm * 128 + i * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+        const bool ok = m < M && n < N;
+        cv[j][v] = (use_c && ok) ? C[m * g.ldc + n] : 0.f;
+      }
+    }
+    if (use_x) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int64_t n = n0 + wn * 64 + j * 32 + lr;
+        float xv[16];
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int64_t m = m0 + wm * 128 + i * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+          xv[v] = (m < M && n < N) ? X[m * g.ldx + n] : 0.f;
+        }
+#pragma unroll
+        for (int v = 0; v < 16; ++v) cv[j][v] = g.beta * cv[j][v] + g.gamma * xv[v];
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) cv[j][v] = g.beta * cv[j][v];
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int64_t n = n0 + wn * 64 + j * 32 + lr;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t m = m0 + wm * 128 + i * 32 + 8 * (v >> 2) + 4 * lh + (v & 3);
+        const float val = g.alpha * acc[i][j][v] + cv[j][v];
+        if (m >= M || n >= N) continue;
+        if (g.uplo == 1 && n > m) continue;
+        if (g.uplo == 2 && m > n) continue;
+        D[m * g.ldd + n] = val;
+      }
+    }
+  }
+}
+
 template <int TILE, bool SPLIT>
 void launch_variant(hipStream_t stream, const GemmF32& g, bool vec, dim3 grid, int64_t tm,
                     int64_t tn) {
@@ -610,8 +816,17 @@ int gemm_f32(hipStream_t stream, const GemmF32& g) {
   G2PTQ_CHECK(!split || g.b_kcontig || g.ldb < (1ll << 27),
               "gemm_f32: ldb %lld too large for the split path's 32-bit row offsets",
               (long long)g.ldb);
-  if (t128 * nz >= 512) launch_gemm<128>(stream, g, vec, nz, split);
-  else launch_gemm<64>(stream, g, vec, nz, split);
+  const int64_t t256 = cdiv(g.M, (int64_t)S2T) * cdiv(g.N, (int64_t)S2T);
+  if (split && g.b_kcontig && g.tri == 0 && g.K >= 384 && t256 * nz >= 256) {
+    const int64_t tm = cdiv(g.M, (int64_t)S2T), tn = cdiv(g.N, (int64_t)S2T);
+    const dim3 grid((unsigned)(tm * tn), 1, (unsigned)nz);
+    if (vec) hipLaunchKernelGGL(gemm_s256_kernel<true>, grid, dim3(512), 0, stream, g, tm, tn);
+    else hipLaunchKernelGGL(gemm_s256_kernel<false>, grid, dim3(512), 0, stream, g, tm, tn);
+  } else if (t128 * nz >= 512) {
+    launch_gemm<128>(stream, g, vec, nz, split);
+  } else {
+    launch_gemm<64>(stream, g, vec, nz, split);
+  }
   G2PTQ_LAUNCHED();
   return G2PTQ_OK;
 }

@@ -711,3 +711,38 @@ def test_fake_quantize_grouped_matches_oracle(dev, sym, groupsize, C):
     got = fake_quantize_grouped(hq, Wd, groupsize)
     exp = oq.fake_quantize_grouped(oqs, W, groupsize)
     assert_bitexact(got, exp, "fake_quantize_grouped")
+
+
+@pytest.mark.parametrize("M,N,K,batch", [(4096, 4096, 512, 1), (4100, 4000, 400, 1),
+                                         (2048, 2048, 1000, 4)])
+def test_gemm_f32_256_tiles_equal_128_tiles(dev, M, N, K, batch):
+    """Split products with B given N×K, K >= 384 and a grid of at least 256
+    tiles of 256×256 run on 8-wave 256×256 workgroups; every output receives
+    the same six bf16 products per 16-k step, in the same order, as on the
+    128×128 workgroups.  The same product computed in 256-row slices (each a
+    grid too small for the large tiles) must equal it bit for bit, ragged M,
+    N and K included, and both hold fp32 accuracy against fp64."""
+    from g2ptq_amd import _lib
+    g = gen(9100 + M + K)
+    A = (torch.randn(batch, M, K, generator=g) * 0.5).to(dev)
+    Bm = torch.randn(batch, N, K, generator=g).to(dev)
+    Cm = torch.randn(batch, M, N, generator=g).to(dev)
+    st, p = _lib.stream_ptr(), _lib.ptr
+
+    def run(m0, m1, D):
+        # D[:, m0:m1] = -A·Bᵀ + 0.5·C through the C ABI (b_trans = 1)
+        _lib.call("g2ptq_gemm_f32", st, m1 - m0, N, K, batch, p(A[:, m0:]), K, M * K, p(Bm), K,
+                  N * K, 1, p(Cm[:, m0:]), N, M * N, p(D[:, m0:]), N, M * N, -1.0, 0.5)
+
+    Dbig = torch.empty(batch, M, N, device=dev)
+    run(0, M, Dbig)
+    Dsl = torch.empty_like(Dbig)
+    for m0 in range(0, M, 256):
+        run(m0, min(M, m0 + 256), Dsl)
+    torch.cuda.synchronize()
+    assert torch.equal(Dbig, Dsl)
+    Bt = Bm.double().transpose(1, 2).contiguous()
+    ref = 0.5 * Cm.double() - torch.bmm(A.double(), Bt)
+    bound = torch.bmm(A.double().abs(), Bt.abs()) + 0.5 * Cm.double().abs()
+    err = ((Dbig.double() - ref).abs() / bound).max().item()
+    assert err <= 4e-7, err
