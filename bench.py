@@ -59,6 +59,8 @@ def parse():
                         "(per-linear Hessians, per-instance fasterquant)")
     p.add_argument("--no-g2ptq", action="store_true",
                    help="skip the config-3 G2PTQ block reported beside the benchmark line")
+    p.add_argument("--no-config1", action="store_true",
+                   help="skip config 1 (one fp32 linear) reported beside the benchmark line")
     p.add_argument("--tokens", type=int, default=N_TOKENS)
     p.add_argument("--calibrate-copy", action="store_true",
                    help="run one 1 GiB device copy first (the known-size reference kernel "
@@ -827,8 +829,9 @@ def main():
         del acts, layers, w0
         torch.cuda.empty_cache()
         out["g2ptq_block"] = g2ptq_block(dev)
-    out["config1"] = config1_gpu(dev)
-    if out["cpu_baseline"]:
+    if not args.no_config1:
+        out["config1"] = config1_gpu(dev)
+    if out["cpu_baseline"] and "config1" in out:
         out["config1"]["cpu_over_gpu"] = round(
             out["cpu_baseline"]["config1"]["value"] / out["config1"]["sec_per_layer"], 1)
     print(json.dumps(out), flush=True)
