@@ -17,7 +17,8 @@
 //   3. the triangular inverse X = L̂⁻¹ panel by panel, as soon as each is
 //      factored, on a third stream beside the Cholesky: the diagonal block
 //      by recursive doubling from the NB inverses, then the block row
-//      X[p, 0:p] = −X_pp·(L[p, 0:p]·X[0:p, 0:p]) as two GEMMs
+//      X[p, 0:p] = −X_pp·(L[p, 0:p]·X[0:p, 0:p]) as two GEMMs, the first
+//      reading X[0:p, 0:p] from a transposed copy kept as the rows finish
 //   4. un-reverse into U (upper, zeros below) with the reference's NaN check.
 #include <map>
 #include <mutex>
@@ -389,8 +390,39 @@ __global__ void unreverse_kernel(const float* __restrict__ WA, int64_t C, const 
   if (nan) atomicCAS(&info[b], 0, -1);
 }
 
+// XT[n][k + m] = X[k + m][n] for the block row [k, k + kb) of X = L̂⁻¹ and
+// columns n < k + kb (zeros where n > k + m): the inverse kept transposed, so
+// that the next block row's product reads it as a k-contiguous operand.  A
+// 64×64 tile per workgroup through LDS (coalesced reads of X's rows, writes
+// of XT's rows).
+__global__ __launch_bounds__(256) void xt_store_kernel(const float* __restrict__ WA, int64_t C,
+                                                       int64_t k, int64_t kb, const int* st,
+                                                       float* __restrict__ XT) {
+  __shared__ float tile[64][65];
+  const int64_t b = blockIdx.z;
+  if (st[b]) return;
+  const int64_t n0 = (int64_t)blockIdx.x * 64, m0 = (int64_t)blockIdx.y * 64;
+  const int64_t kend = k + kb;
+  const float* Wb = WA + b * C * C;
+  float* Xb = XT + b * C * C;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int64_t m = m0 + ty * 16 + r, n = n0 + tx;  // X[k + m][n]
+    float v = 0.f;
+    if (m < kb && n < kend && n <= k + m) v = Wb[(k + m) * C + n];
+    tile[ty * 16 + r][tx] = v;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int64_t n = n0 + ty * 16 + r, m = m0 + tx;  // XT[n][k + m]
+    if (n < kend && m < kb) Xb[n * C + k + m] = tile[tx][ty * 16 + r];
+  }
+}
+
 struct FactorWs {
-  size_t wa, wt, ti, lp, sums, st, total;
+  size_t wa, wt, ti, lp, xt, sums, st, total;
 };
 
 FactorWs factor_ws(int64_t B, int64_t C) {
@@ -401,9 +433,10 @@ FactorWs factor_ws(int64_t B, int64_t C) {
   w.wt = al((size_t)B * half * half * 4 + 4);        // in-panel inverse products
   w.ti = al((size_t)B * NBO * C * 4 + 4);            // inverse block-row products
   w.lp = al((size_t)B * C * NBO * 4);                // a panel's L until its last step
+  w.xt = al((size_t)B * C * C * 4);                  // the inverse's finished block rows, transposed
   w.sums = al((size_t)B * 4);
   w.st = al((size_t)B * 4);
-  w.total = w.wa + w.wt + w.ti + w.lp + w.sums + w.st;
+  w.total = w.wa + w.wt + w.ti + w.lp + w.xt + w.sums + w.st;
   return w;
 }
 
@@ -450,8 +483,9 @@ extern "C" int g2ptq_inv_chol_upper(void* stream, const float* H, int64_t B, int
   float* WT = reinterpret_cast<float*>(base + w.wa);
   float* TI = reinterpret_cast<float*>(base + w.wa + w.wt);
   float* Lp = reinterpret_cast<float*>(base + w.wa + w.wt + w.ti);
-  float* sums = reinterpret_cast<float*>(base + w.wa + w.wt + w.ti + w.lp);
-  int* st = reinterpret_cast<int*>(base + w.wa + w.wt + w.ti + w.lp + w.sums);
+  float* XT = reinterpret_cast<float*>(base + w.wa + w.wt + w.ti + w.lp);
+  float* sums = reinterpret_cast<float*>(base + w.wa + w.wt + w.ti + w.lp + w.xt);
+  int* st = reinterpret_cast<int*>(base + w.wa + w.wt + w.ti + w.lp + w.xt + w.sums);
   const int64_t CC = C * C;
 
   hipLaunchKernelGGL(diag_sum_kernel, dim3((unsigned)B), dim3(256), 0, s, H, C, skip, sums, st,
@@ -518,7 +552,10 @@ extern "C" int g2ptq_inv_chol_upper(void* stream, const float* H, int64_t B, int
   //   the panel's diagonal block (recursive doubling from the NB inverses,
   //   in place), then, in block-row order so that X[0:k, 0:k] is final,
   //   TI = L[k:kend, 0:k] · X[0:k, 0:k];  X[k:kend, 0:k] = −X_kk · TI,
-  //   written over L[k:kend, 0:k].
+  //   written over L[k:kend, 0:k], and the finished block row copied
+  //   transposed into XT, from which the next block rows' TI products read
+  //   X[0:k, 0:k] as a k-contiguous operand (each element still receives the
+  //   same products in the same order, so X is unchanged to the bit).
   // The Cholesky reads neither the diagonal block nor the block row again:
   // the trailing updates that read the block row completed before the panel
   // was factored, and those of the panel itself read only the rows below it.
@@ -560,12 +597,12 @@ extern "C" int g2ptq_inv_chol_upper(void* stream, const float* H, int64_t B, int
     inv_pending = true;
     G2PTQ_TRY(trtri_levels(side.stream2, k, kb, NB, NBO));
     if (k > 0) {
-      GemmF32 t;
+      GemmF32 t;  // B = X[0:k, 0:k] read as its transpose XT (N×K, k-contiguous)
       t.M = kb; t.N = k; t.K = k; t.batch = B;
       t.A = WA + k * C; t.lda = C; t.sA = CC;
-      t.B = WA; t.ldb = C; t.sB = CC;
+      t.B = XT; t.ldb = C; t.sB = CC; t.b_kcontig = 1;
       t.D = TI; t.ldd = C; t.sD = NBO * C;
-      t.tri = 2;  // X lower triangular
+      t.tri = 2;  // X lower triangular: XT[n][kk] = 0 for kk < n
       t.skip = st;
       G2PTQ_TRY(gemm_f32(side.stream2, t));
       GemmF32 x;
@@ -576,6 +613,12 @@ extern "C" int g2ptq_inv_chol_upper(void* stream, const float* H, int64_t B, int
       x.alpha = -1.f; x.tri = 1;  // X_kk lower triangular
       x.skip = st;
       G2PTQ_TRY(gemm_f32(side.stream2, x));
+    }
+    if (k + kb < C) {  // later block rows read this one (and its diagonal block) from XT
+      hipLaunchKernelGGL(xt_store_kernel, dim3((unsigned)cdiv(k + kb, 64), (unsigned)cdiv(kb, 64),
+                                               (unsigned)B),
+                         dim3(256), 0, side.stream2, WA, C, k, kb, st, XT);
+      G2PTQ_LAUNCHED();
     }
     return G2PTQ_OK;
   };
