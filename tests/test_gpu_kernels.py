@@ -714,7 +714,8 @@ def test_fake_quantize_grouped_matches_oracle(dev, sym, groupsize, C):
 
 
 @pytest.mark.parametrize("M,N,K,batch", [(4096, 4096, 512, 1), (4100, 4000, 400, 1),
-                                         (2048, 2048, 1000, 4)])
+                                         (2048, 2048, 1000, 4),
+                                         (4096, 4100, 401, 1)])  # K % 4 != 0: per-element loads
 def test_gemm_f32_256_tiles_equal_128_tiles(dev, M, N, K, batch):
     """Split products with B given N×K, K >= 384 and a grid of at least 256
     tiles of 256×256 run on 8-wave 256×256 workgroups; every output receives
