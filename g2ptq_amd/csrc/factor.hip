@@ -86,7 +86,7 @@ __global__ __launch_bounds__(256) void potrf_diag_kernel(float* WA, int64_t C, i
   const int64_t b = blockIdx.x;
   __shared__ __attribute__((aligned(16))) float Xs[POT_NB * XP];
   __shared__ __attribute__((aligned(16))) float Lm[POT_NB * LP];
-  __shared__ __attribute__((aligned(16))) float rdv[POT_NB];
+  __shared__ __attribute__((aligned(16))) float rdv[POT_NB + PB * PB];  // + the panels' multipliers
   __shared__ int fail_s;
   float* Wb = WA + b * C * C + k * C + k;
   const int i = threadIdx.x & 63, w = threadIdx.x >> 6;

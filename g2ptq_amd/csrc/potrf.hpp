@@ -15,8 +15,11 @@ namespace {
 //   panel p (wave 0, lane i = row i): the 16 pivots of columns
 //     [16p, 16p + 16) in turn, each d = A[j][j] read from lane j,
 //     l_ij = A[i][j]·rsqrt(d), and the rank-1 update of the panel's own
-//     later columns with the multipliers of rows j + 1.. broadcast from
-//     their lanes (no LDS round trip, no barrier);
+//     later columns: the next two with the multipliers of their rows read
+//     from those lanes (v_readlane, on the pivot chain), the rest with the
+//     multipliers the panel rows wrote to LDS (one store and a few
+//     broadcast reads instead of a v_readlane per column; no barrier, the
+//     wave's LDS accesses complete in order);
 //   trailing update (all waves): A[i][c] −= Σ_t l_it·l_ct over the panel's
 //     16 columns for 16p + 16 <= c <= i, 4×2 or 2×2 entries per thread;
 //   inverse rows [16p, 16p + 16) (one of waves 1 to 3, lane i = column i,
@@ -46,6 +49,8 @@ __device__ __forceinline__ float lane_val(float v, int lane) {
 template <int P>
 __device__ __forceinline__ void pot_panel(const float* As, float* Lm, float* rdv, int i, int& fail) {
   constexpr int k0 = P * PB;
+  constexpr int LA = 2;  // columns after the pivot updated through v_readlane
+  float* Mb = rdv + POT_NB;  // per pivot, the panel rows' multipliers (LDS)
   float a[PB], l[PB];
   float rdl = 0.f;  // lane j: 1/sqrt of pivot k0 + j
 #pragma unroll
@@ -58,8 +63,12 @@ __device__ __forceinline__ void pot_panel(const float* As, float* Lm, float* rdv
     const float m = (i > k0 + j) ? a[j] * rd : 0.f;
     l[j] = m;
     rdl = (i == j) ? rd : rdl;
+    if (j + LA + 1 < PB && i >= k0 && i < k0 + PB) Mb[j * PB + (i - k0)] = m;
 #pragma unroll
-    for (int c = j + 1; c < PB; ++c) a[c] = __builtin_fmaf(-m, lane_val(m, k0 + c), a[c]);
+    for (int c = j + 1; c < PB && c <= j + LA; ++c)
+      a[c] = __builtin_fmaf(-m, lane_val(m, k0 + c), a[c]);
+#pragma unroll
+    for (int c = j + LA + 1; c < PB; ++c) a[c] = __builtin_fmaf(-m, Mb[j * PB + c], a[c]);
   }
 #pragma unroll
   for (int c4 = 0; c4 < PB; c4 += 4)
@@ -168,7 +177,7 @@ __device__ __forceinline__ void pot_inv_fin(float (&acc)[PB], float* Xs, const f
 }
 
 // The factor of the block staged in Xs (lower triangle, identity padded),
-// by a 256-thread workgroup.  Lm (64·LP floats) and rdv (64) are scratch.
+// by a 256-thread workgroup.  Lm (64·LP floats) and rdv (64 + 16·16) are scratch.
 // Leaves X = L⁻¹ in Xs (rows, lower triangle; what lies above is not
 // defined) and returns the failing pivot index + 1, or 0.
 // Schedule (waves w0..w3, `|` a barrier; the trailing updates occupy the
