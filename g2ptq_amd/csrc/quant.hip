@@ -679,11 +679,30 @@ __global__ __launch_bounds__(256) void sweep4_kernel(SweepArgs a) {
       const int ge = min(p0 + (int)a.fuse, n);
       float mn = INFINITY, mx = -INFINITY;
       int nan = 0;
-      for (int j = p0 + sub; j < ge; j += L) {
-        const float v = Win[(int64_t)j * a.wc];
-        nan |= (v != v);
-        mn = fminf(mn, v);
-        mx = fmaxf(mx, v);
+      if constexpr (L == 16) {
+        // the lane's (at most eight) values loaded together, then reduced
+        constexpr int KG = kMaxBlock / L;
+        float v[KG];
+#pragma unroll
+        for (int k = 0; k < KG; ++k) {
+          const int j = p0 + sub + L * k;
+          v[k] = j < ge ? Win[(int64_t)j * a.wc] : 0.f;
+        }
+#pragma unroll
+        for (int k = 0; k < KG; ++k) {
+          if (p0 + sub + L * k < ge) {
+            nan |= (v[k] != v[k]);
+            mn = fminf(mn, v[k]);
+            mx = fmaxf(mx, v[k]);
+          }
+        }
+      } else {
+        for (int j = p0 + sub; j < ge; j += L) {
+          const float v = Win[(int64_t)j * a.wc];
+          nan |= (v != v);
+          mn = fminf(mn, v);
+          mx = fmaxf(mx, v);
+        }
       }
 #pragma unroll
       for (int o = L / 2; o > 0; o >>= 1) {
@@ -929,13 +948,22 @@ __global__ __launch_bounds__(256) void sweep4_kernel(SweepArgs a) {
       // holds the U slab, k-major), four consecutive columns per lane.
       float* Wr = a.Wsb + b * a.wb + r * a.wr;
       const float* Ub = a.U + b * a.ub + cofs * a.uj;
+      // A thread's eight 16-byte pieces of a slab are all loaded before any
+      // is stored: one memory round trip per slab, not eight.
+      static_assert(kMaxBlock * 16 == 8 * 256, "a slab is eight 16-byte pieces per thread");
+      // thread tid's piece i: row k = tid/16 + 16i of the slab, columns 4·(tid%16)..+3
+      const int k0 = tid >> 4, c4 = (tid & 15) * 4;
       for (int c0 = (int)cofs + kMaxBlock; c0 < nblk * kMaxBlock; c0 += 64) {
+        const float* us = Ub + (int64_t)k0 * a.uj + c0 + c4;
+        const int64_t st16 = 16 * a.uj;
+#define G2_LDU(i) const float4 u##i = *reinterpret_cast<const float4*>(us + (i) * st16)
+        G2_LDU(0); G2_LDU(1); G2_LDU(2); G2_LDU(3); G2_LDU(4); G2_LDU(5); G2_LDU(6); G2_LDU(7);
+#undef G2_LDU
         __syncthreads();  // the sweep's (or the previous slab's) LDS reads are done
-        for (int q = tid; q < kMaxBlock * 16; q += 256) {
-          const int k = q >> 4, c4 = (q & 15) * 4;
-          *reinterpret_cast<float4*>(&Us[k * 64 + c4]) =
-              *reinterpret_cast<const float4*>(Ub + (int64_t)k * a.uj + c0 + c4);
-        }
+        float* ud = &Us[k0 * 64 + c4];
+#define G2_STU(i) *reinterpret_cast<float4*>(ud + (i) * 16 * 64) = u##i
+        G2_STU(0); G2_STU(1); G2_STU(2); G2_STU(3); G2_STU(4); G2_STU(5); G2_STU(6); G2_STU(7);
+#undef G2_STU
         __syncthreads();
         if (act) {
           float4 w = *reinterpret_cast<const float4*>(Wr + c0 + 4 * sub);
