@@ -155,27 +155,57 @@ static_assert(SLP >= LP, "the panel step's tiles hold the potrf scratch");
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 // A 64×64 block of Â (rows row0.., columns col0.., only rows < nrows and
-// columns < ncols nonzero) into LDS [row][SLP].
-__device__ __forceinline__ void panel_load(float* Ls, const float* Wb, int64_t C, int64_t row0,
-                                           int64_t col0, int64_t nrows, int ncols, bool vec) {
+// columns < ncols nonzero): thread t's four 16-byte pieces (rows t/16 + 16q,
+// columns 4·(t%16)..+3) into registers, then into LDS [row][SLP] by
+// panel_put.  panel_fetch_vec (16-byte aligned rows, the thread's four
+// columns inside the block) issues its loads unconditionally: row0 is a row of
+// Â, so a piece below the block reads from row0, and panel_put zeroes it.  A
+// caller fetching several blocks calls it for all of them before putting any,
+// so their loads are in flight together.
+__device__ __forceinline__ void panel_fetch_vec(float4 (&v)[4], const float* Wb, int64_t C,
+                                                int64_t row0, int64_t col0, int64_t nrows) {
   const int t = threadIdx.x;
   const int c4 = (t & 15) * 4;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int r = (t >> 4) + 16 * q;
-    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    v[q] = *reinterpret_cast<const float4*>(Wb + (row0 + (r < nrows ? r : 0)) * C + col0 + c4);
+  }
+}
+
+__device__ __forceinline__ void panel_fetch_any(float4 (&v)[4], const float* Wb, int64_t C,
+                                                int64_t row0, int64_t col0, int64_t nrows,
+                                                int ncols) {
+  const int t = threadIdx.x;
+  const int c4 = (t & 15) * 4;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int r = (t >> 4) + 16 * q;
+    float4 x = make_float4(0.f, 0.f, 0.f, 0.f);
     if (r < nrows) {
       const float* p = Wb + (row0 + r) * C + col0 + c4;
-      if (vec && c4 + 3 < ncols) {
-        v = *reinterpret_cast<const float4*>(p);
-      } else {
-        if (c4 < ncols) v.x = p[0];
-        if (c4 + 1 < ncols) v.y = p[1];
-        if (c4 + 2 < ncols) v.z = p[2];
-        if (c4 + 3 < ncols) v.w = p[3];
-      }
+      if (c4 < ncols) x.x = p[0];
+      if (c4 + 1 < ncols) x.y = p[1];
+      if (c4 + 2 < ncols) x.z = p[2];
+      if (c4 + 3 < ncols) x.w = p[3];
     }
-    *reinterpret_cast<float4*>(&Ls[r * SLP + c4]) = v;
+    v[q] = x;
+  }
+}
+
+// Whether thread t's pieces take panel_fetch_vec.
+__device__ __forceinline__ bool panel_vec(bool vec, int ncols) {
+  return vec && (threadIdx.x & 15) * 4 + 3 < ncols;
+}
+
+__device__ __forceinline__ void panel_put(float* Ls, const float4 (&v)[4], int64_t nrows) {
+  const int t = threadIdx.x;
+  const int c4 = (t & 15) * 4;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int r = (t >> 4) + 16 * q;
+    *reinterpret_cast<float4*>(&Ls[r * SLP + c4]) =
+        r < nrows ? v[q] : make_float4(0.f, 0.f, 0.f, 0.f);
   }
 }
 
@@ -248,9 +278,21 @@ __global__ __launch_bounds__(256) void panel_step_kernel(PanelArgs p) {
   float* Wb = p.WA + b * C * C;
   const bool vec = (C & 3) == 0;
   const int64_t ri = r0 + 64 * i, rn = r0 + 64 * n;  // first row of each L block
-  panel_load(Xj, Wb, C, p.j, p.j, p.nbk, p.nbk, vec);
-  panel_load(Ai, Wb, C, ri, p.j, C - ri, p.nbk, vec);
-  if (n != i) panel_load(An, Wb, C, rn, p.j, C - rn, p.nbk, vec);
+  {
+    float4 vx[4], va[4], vn[4];
+    if (panel_vec(vec, p.nbk)) {
+      panel_fetch_vec(vx, Wb, C, p.j, p.j, p.nbk);
+      panel_fetch_vec(va, Wb, C, ri, p.j, C - ri);
+      panel_fetch_vec(vn, Wb, C, n != i ? rn : ri, p.j, C - (n != i ? rn : ri));
+    } else {
+      panel_fetch_any(vx, Wb, C, p.j, p.j, p.nbk, p.nbk);
+      panel_fetch_any(va, Wb, C, ri, p.j, C - ri, p.nbk);
+      panel_fetch_any(vn, Wb, C, n != i ? rn : ri, p.j, C - (n != i ? rn : ri), p.nbk);
+    }
+    panel_put(Xj, vx, p.nbk);
+    panel_put(Ai, va, C - ri);
+    if (n != i) panel_put(An, vn, C - rn);
+  }
   const int wave = threadIdx.x >> 6, wm = wave >> 1, wn = wave & 1;
   const int lane = threadIdx.x & 63, lr = lane & 31, lh = lane >> 5;
   // The update's Â operand, read with the raw blocks (nothing in this launch
@@ -335,22 +377,53 @@ __global__ __launch_bounds__(256) void panel_finish_kernel(PanelArgs p) {
   const int64_t cend = (R0 < p.pe ? R0 : p.j) - p.k;  // buffer columns to copy
   {
     const int nq = (int)(cend >> 2);  // cend is a multiple of 64
-    for (int q = threadIdx.x; q < 64 * nq; q += 256) {
-      const int64_t r = R0 + q / nq;
-      const int64_t c4 = (int64_t)(q % nq) * 4;
-      if (r >= C) continue;
-      const float* s = Lb + r * NBO + c4;
-      float* d = Wb + r * C + p.k + c4;
-      if (vec) {
-        *reinterpret_cast<float4*>(d) = *reinterpret_cast<const float4*>(s);
-      } else {
-        d[0] = s[0]; d[1] = s[1]; d[2] = s[2]; d[3] = s[3];
+    // eight 16-byte pieces per thread and pass, all loaded before any is stored
+    constexpr int U = 8;
+    for (int q0 = threadIdx.x; q0 < 64 * nq; q0 += 256 * U) {
+      float4 x[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int q = q0 + 256 * u;
+        const int64_t r = R0 + q / nq;
+        const int64_t c4 = (int64_t)(q % nq) * 4;
+        if (q < 64 * nq && r < C) {
+          const float* s = Lb + r * NBO + c4;
+          if (vec) {
+            x[u] = *reinterpret_cast<const float4*>(s);
+          } else {
+            x[u] = make_float4(s[0], s[1], s[2], s[3]);
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int q = q0 + 256 * u;
+        const int64_t r = R0 + q / nq;
+        const int64_t c4 = (int64_t)(q % nq) * 4;
+        if (q < 64 * nq && r < C) {
+          float* d = Wb + r * C + p.k + c4;
+          if (vec) {
+            *reinterpret_cast<float4*>(d) = x[u];
+          } else {
+            d[0] = x[u].x; d[1] = x[u].y; d[2] = x[u].z; d[3] = x[u].w;
+          }
+        }
       }
     }
   }
   if (R0 < p.pe) return;
-  panel_load(Xj, Wb, C, p.j, p.j, p.nbk, p.nbk, vec);
-  panel_load(Ai, Wb, C, R0, p.j, C - R0, p.nbk, vec);
+  {
+    float4 vx[4], va[4];
+    if (panel_vec(vec, p.nbk)) {
+      panel_fetch_vec(vx, Wb, C, p.j, p.j, p.nbk);
+      panel_fetch_vec(va, Wb, C, R0, p.j, C - R0);
+    } else {
+      panel_fetch_any(vx, Wb, C, p.j, p.j, p.nbk, p.nbk);
+      panel_fetch_any(va, Wb, C, R0, p.j, C - R0, p.nbk);
+    }
+    panel_put(Xj, vx, p.nbk);
+    panel_put(Ai, va, C - R0);
+  }
   __syncthreads();
   const int wave = threadIdx.x >> 6, wm = wave >> 1, wn = wave & 1;
   const int lane = threadIdx.x & 63, lr = lane & 31, lh = lane >> 5;
