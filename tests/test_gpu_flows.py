@@ -266,11 +266,11 @@ def test_flow_from_x_matches_oracle(dev, case):
 
 
 def test_flow_from_x_quad_lanes(dev):
-    """Config 2's GPTQ W4 sym g128 with 2 × 4200 rows: more than 8192 rows
+    """Config 2's GPTQ W4 sym g128 with 2 × 8400 rows: more than 16384 rows
     take the sweep with a quad of lanes per row (the gate/up projections'
     28672 rows do).  Against the oracle under the parity protocol."""
-    print("flow from X: gptq w4 sym g128, 2 x 4200 rows", flush=True)
-    layers, quantizers, ref, W0, H, gq = run_flow_from_x(dev, "gptq", 4, True, 128, R=4200,
+    print("flow from X: gptq w4 sym g128, 2 x 8400 rows", flush=True)
+    layers, quantizers, ref, W0, H, gq = run_flow_from_x(dev, "gptq", 4, True, 128, R=8400,
                                                          seed=395)
     assert_flow_parity("gptq quad lanes", layers, quantizers, ref, W0, H, 4, 128, False)
 

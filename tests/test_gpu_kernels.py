@@ -27,9 +27,11 @@ CASES = (
     ("symmetric_4bit_block32", 3, 32, 17, 7, False, 403),
     ("asymmetric_2bit_block64", 1, 64, 45, 1, True, 404),
     ("symmetric_8bit_block96", 2, 96, 70, 127, False, 405),
-    # more than 8192 rows in all: the quad-per-row sweep (fewer rows: 16 lanes per row)
-    ("symmetric_4bit_block64_many_rows", 2, 64, 4200, 7, False, 406),
-    ("asymmetric_3bit_block32_many_rows", 1, 32, 8500, 3, True, 407),
+    # more than 16384 rows in all: the quad-per-row sweep (fewer rows: 16 lanes per row)
+    ("symmetric_4bit_block64_many_rows", 2, 64, 8400, 7, False, 406),
+    ("asymmetric_3bit_block32_many_rows", 1, 32, 16500, 3, True, 407),
+    # 16 lanes per row with more rows than two waves per SIMD hold at once
+    ("symmetric_4bit_block128_12k_rows", 1, 128, 12000, 7, False, 408),
 )
 
 
