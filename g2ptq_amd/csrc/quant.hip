@@ -1014,7 +1014,8 @@ bool sweep_vec_ok(const SweepArgs& a) {
 // 16 lanes per row up to 16384 rows in the launch (four waves per SIMD at
 // two resident), a quad of lanes beyond: measured on GPTQ loops of 4096
 // columns, 16 lanes were 6–9 % faster at 12288 and 14336 rows and 12 % slower
-// at 28672.
+// at 28672 (GPTAQ loops: 10–13 % slower at 28672 and 57344).  G2PTQ takes 16
+// lanes at any row count (launch_variant).
 bool lanes16(int64_t B, int64_t R) { return B * R <= 16384; }
 
 template <int V>
@@ -1022,8 +1023,11 @@ void launch_variant(hipStream_t stream, const SweepArgs& a, dim3 grid, bool vec)
   const bool full = (a.n % 32) == 0;
   if (full) {
     // 16 lanes per row while that keeps the block within about two waves per
-    // SIMD (1024 SIMDs), else a quad per row.
-    if (lanes16(grid.y, a.R)) {
+    // SIMD (1024 SIMDs), else a quad per row.  G2PTQ always takes 16 lanes:
+    // its quad sweep needs 312–328 VGPRs (one workgroup per CU) where 16
+    // lanes need 244–249 (two), and its loops of 4096 columns ran 9–17 %
+    // faster with 16 lanes at 20000, 28672 and 57344 rows.
+    if (V == 2 || lanes16(grid.y, a.R)) {
       dim3 g16((unsigned)cdiv(a.R, (int64_t)16), grid.y);
       if constexpr (V == 0) {
         if (a.nblk > 1) {
@@ -1038,7 +1042,7 @@ void launch_variant(hipStream_t stream, const SweepArgs& a, dim3 grid, bool vec)
         hipLaunchKernelGGL((sweep4_kernel<V, 16, true>), g16, dim3(256), 0, stream, a);
       else
         hipLaunchKernelGGL((sweep4_kernel<V, 16, false>), g16, dim3(256), 0, stream, a);
-    } else {
+    } else if constexpr (V != 2) {
       dim3 g4((unsigned)cdiv(a.R, (int64_t)64), grid.y);
       if (a.fuse > 0)
         hipLaunchKernelGGL((sweep4_kernel<V, 4, true>), g4, dim3(256), 0, stream, a);

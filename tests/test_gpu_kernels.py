@@ -23,11 +23,12 @@ CASES = (
     # full 128-wide blocks (four register panels) with many rows
     ("asymmetric_4bit_block128", 2, 128, 300, 7, True, 401),
     ("symmetric_3bit_block100", 1, 100, 130, 3, False, 402),
-    # 32-column multiples (the quad-per-row sweep) with ragged row counts
+    # 32-column multiples (the panel sweep) with ragged row counts
     ("symmetric_4bit_block32", 3, 32, 17, 7, False, 403),
     ("asymmetric_2bit_block64", 1, 64, 45, 1, True, 404),
     ("symmetric_8bit_block96", 2, 96, 70, 127, False, 405),
-    # more than 16384 rows in all: the quad-per-row sweep (fewer rows: 16 lanes per row)
+    # more than 16384 rows in all: the quad-per-row sweep for GPTQ and GPTAQ (fewer
+    # rows, and G2PTQ at any row count: 16 lanes per row)
     ("symmetric_4bit_block64_many_rows", 2, 64, 8400, 7, False, 406),
     ("asymmetric_3bit_block32_many_rows", 1, 32, 16500, 3, True, 407),
     # 16 lanes per row with more rows than two waves per SIMD hold at once
