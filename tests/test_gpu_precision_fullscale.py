@@ -260,3 +260,57 @@ def test_gptaq_cross_term_at_config5_scale(dev):
                                      groupsize=gs, alpha=alpha, dtype=torch.float64)
     _bar("GPTAQ C=8192, 262144 tokens", [lin], gq.quantizer, [lin2], gq2.quantizer, ref, ref64,
          W0, He.unsqueeze(0), bits, gs)
+
+
+def test_g2ptq_more_than_16384_rows_in_one_loop(dev):
+    """Config 3's G2PTQ W3 g128 (α = 0.1, 4 row groups) over two layers of
+    8400 rows at C = 1024: 16800 rows in one compensation loop, where GPTQ and
+    GPTAQ take a quad of lanes per row and G2PTQ keeps 16.  Judged like the
+    cases above, against the fp32 and fp64 oracle flows from the same exact
+    Hessians."""
+    from g2ptq_amd import G2PTQ, WeightQuantizer, make_group_quantizers
+    B, C, G, R, bits, gs, alpha = 2, 1024, 4, 8400, 3, 128, 0.1
+    print(f"G2PTQ many rows: B={B} R={R} C={C} tokens={N_TOKENS} G={G}", flush=True)
+    X, _, g = _tokens(C, 701, dev)
+    sal = torch.exp(0.5 * torch.randn(N_TOKENS, 1, device=dev, generator=g)) * \
+        torch.rand(N_TOKENS, G, device=dev, generator=g)
+    lins = [_linear(R, C, 702 + b, dev) for b in range(B)]
+    W0 = torch.stack([lin.weight.detach().float().cpu() for lin in lins])
+    grads = 1e-3 * torch.randn(B, R, C, generator=gen(704)) * \
+        _student_t3((B, R, 1), gen(705)).abs()
+    batches = range(0, N_TOKENS, CHUNK)
+    gq = G2PTQ(lins, [[sal[i:i + CHUNK] for i in batches] for _ in range(B)],
+               [grads[b].to(dev) for b in range(B)], G)
+    q = WeightQuantizer()
+    q.configure(bits, perchannel=True, sym=True)
+    gq.quantizer = make_group_quantizers(q, C, gs)
+    for i in batches:
+        xb = X[i:i + CHUNK].unsqueeze(0)
+        for b in range(B):
+            gq.add_batch(b, xb, None)
+    # both layers read the same input: one exact set of weighted Hessians
+    He = torch.zeros(G, C, C, device=dev, dtype=torch.float64)
+    act = torch.zeros(C, device=dev, dtype=torch.float64)
+    for i in batches:
+        x = X[i:i + CHUNK].double()
+        for grp in range(G):
+            He[grp] += (x * sal[i:i + CHUNK, grp:grp + 1].double()).T @ x
+        act += (x * x).sum(0)
+    He64 = (He / N_TOKENS).cpu().unsqueeze(0).expand(B, G, C, C).contiguous()
+    He = He64.float()
+    act = (act / N_TOKENS).float().cpu().unsqueeze(0).expand(B, C).contiguous()
+    del X, sal
+    lins2 = [_linear(R, C, 702 + b, dev) for b in range(B)]
+    gq2 = G2PTQ(lins2, [[] for _ in range(B)], [grads[b].to(dev) for b in range(B)], G)
+    gq2.quantizer = make_group_quantizers(q, C, gs)
+    gq2.H.copy_(He.to(dev))
+    for inst in (gq, gq2):
+        inst.fasterquant(blocksize=128, percdamp=0.01, groupsize=gs, alpha=alpha, backend="hip",
+                         export_compressed_tensors=True)
+    torch.cuda.synchronize()
+    ref = oflows.g2ptq_fasterquant(W0, He.clone(), grads, act, bits, True, G, groupsize=gs,
+                                   alpha=alpha)
+    ref64 = oflows.g2ptq_fasterquant(W0, He64.clone(), grads, act.double(), bits, True, G,
+                                     groupsize=gs, alpha=alpha, dtype=torch.float64)
+    _bar("G2PTQ 2 x 8400 rows, C=1024", lins, gq.quantizer, lins2, gq2.quantizer, ref, ref64,
+         W0, He.reshape(B * G, C, C), bits, gs)
