@@ -449,7 +449,7 @@ def run_step_unchanged(acts, layers, w0, n_tokens, ev):
             xb = X[t0:t0 + step_tok].view(-1, SEQ, C)
             for gq in insts:
                 for i in range(gq.num_layers):
-                    gq.add_batch(i, xb, None)
+                    gq.add_batch(i, xb.data, None)  # each hook passes inp[0].data
         for gq in insts:
             gq.H  # the calibration pass ends: fold the staged tokens
         e1.record(stream)
@@ -489,7 +489,9 @@ def unchanged_driver(acts, layers, w0, n_tokens, steps=3, warmup=1):
             "stages_ms": {"hessian": round(h, 2), "factor_and_compensation": round(sum(qs) / steps, 2)},
             "hessian_tflops_per_linear": round(flops / (h / 1e3) / 1e12, 1),
             "note": "reference driver layout with only the backend switched: 7 per-linear "
-                    "Hessians, one instance per same-shape chunk, per-instance fasterquant"}
+                    "Hessians fed inp[0].data views, one instance per same-shape chunk, "
+                    "per-instance fasterquant (linears staged from the same inputs share "
+                    "Gram results after a device compare of their staged tokens)"}
 
 
 def _cpu_threads():

@@ -70,6 +70,7 @@ SIGNATURES = {
     "g2ptq_permute_sym": [_p, _p, _p, _i64, _i64, _p],
     "g2ptq_cast_check": [_p, _p, _p, _i64, _i32, _p],
     "g2ptq_to_f32": [_p, _p, _p, _i64, _i32],
+    "g2ptq_staged_equal": [_p, _p, _i64, _p, _i64, _i64, _i64, _p],
     "g2ptq_pack_quantized": [_p, _p, _i64, _p, _i64, _i64, _i64, _i32, _i64, _p, _i64, _p, _i32, _i64,
                              _p],
     "g2ptq_concat": [_p, _p, _p, _i64, _i64, _p],

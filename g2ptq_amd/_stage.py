@@ -38,8 +38,21 @@ multiple of 2 KiB): power-of-two-like pitches alias the rows of a Gram panel
 onto few memory channels (measured on MI355X, C = 14336, K = 204800: a
 528384-byte pitch, 512 KiB + 4 KiB, made the Gram 20 % slower than 518 to
 560 KiB pitches).
+
+Linears that read the same input (q/k/v, gate/up) get views of the same
+tensor from their forward hooks (``inp[0].data``), so a driver that keeps one
+Hessian per linear (gptq_utils.py:497-505) stages the same tokens once per
+linear.  Each staged GPTQ batch records where its tokens came from (address,
+count, row stride).  When a stager's first flush computes the Gram of a
+sequence of batches that other live stagers have staged from the same
+addresses, in the same order, the result and the staged tokens are kept for
+them; each of their flushes compares its staged tokens with the kept ones on
+the device (``g2ptq_staged_equal``) and copies the kept Gram only when they
+are bit-identical, else runs its own.  The Gram is deterministic, so every
+Hessian holds exactly the values it would have computed itself.
 """
 import os
+import weakref
 
 import torch
 
@@ -87,6 +100,33 @@ def _device_memory(device):
     return _MEMORY[idx]
 
 
+def batch_source(X):
+    """Where a (T, C) token matrix comes from: (address, T, row stride)."""
+    return (X.data_ptr(), X.shape[0], X.stride(0))
+
+
+# Gram results kept for stagers that staged from the same sources: key →
+# (H, the staged buffer, its pitch, the waiting stagers).  Stagers by the
+# first source they staged since their last flush, to find those that may
+# share a flush.
+_SHARED = {}
+_BY_FIRST = {}
+
+
+def _share_key(st, alpha):
+    return (st.device, st.C, st.k, float(alpha), tuple(st.ids))
+
+
+def _drop_waiter(st):
+    """``st`` will not read the results kept for it (released, or flushed
+    another way); results nobody waits for any more are freed."""
+    for key in [k for k, v in _SHARED.items() if st in v[3] or not v[3]]:
+        ws = _SHARED[key][3]
+        ws.discard(st)
+        if not ws:
+            del _SHARED[key]
+
+
 class GramStager:
     def __init__(self, columns, device, kind=KIND_GPTQ, groups=0, budget_bytes=None,
                  dtype=DTYPE_BF16):
@@ -106,6 +146,10 @@ class GramStager:
         self.buf = None
         self.cap = 0        # token columns of buf
         self.k = 0          # staged token columns (multiples of 64)
+        # batch_source of each batch staged since the last flush; None once a
+        # batch without one was staged
+        self.ids = []
+        self._first = None
 
     def fits(self, T):
         return self.buf is not None and self.k + _ceil(T, 64) + _GRAM_PAD <= self.cap
@@ -144,10 +188,22 @@ class GramStager:
         self.buf = torch.empty(self.height, cap, dtype=torch.bfloat16, device=self.device)
         self.cap = cap
 
-    def stage(self, X, Xfp=None, S=None, s_scale=1.0, act=None, act_alpha=0.0, act_beta=1.0):
+    def stage(self, X, Xfp=None, S=None, s_scale=1.0, act=None, act_alpha=0.0, act_beta=1.0,
+              share=False):
         """Append one (T, C) bf16 batch: X_fp for GPTAQ; the (T, G) fp32
-        saliencies, their scale and the act-square update for the weighted kind."""
+        saliencies, their scale and the act-square update for the weighted kind.
+        ``share``: record the batch's source (a GPTQ batch whose Gram may be
+        shared with other stagers of the same tokens)."""
         T, C = X.shape
+        if self.ids is not None:
+            if not share:
+                self.ids = None
+            else:
+                src = batch_source(X)
+                if not self.ids:
+                    _BY_FIRST.setdefault(src, weakref.WeakSet()).add(self)
+                    self._first = src
+                self.ids.append(src)
         st, xt = _lib.stream_ptr(), _lib.ptr(self.buf)
         if self.dtype != DTYPE_BF16:
             _lib.call("g2ptq_hessian_stage_ex", st, self.kind, self.dtype, _lib.ptr(X),
@@ -179,6 +235,23 @@ class GramStager:
         if not H.is_cuda or (Dx is not None and not Dx.is_cuda):
             raise RuntimeError("staged Hessian tokens need the Hessian on the GPU: call "
                                "add_batch inside the onload context of the Hessian")
+        # A first flush (beta = 0: H = alpha·Gram) of GPTQ batches staged from
+        # the sources whose Gram another stager computed with the same alpha
+        # copies it, once the device has found the staged tokens identical.
+        key = None
+        if (self.kind == KIND_GPTQ and self.dtype == DTYPE_BF16 and self.ids and beta == 0.0
+                and Dx is None):
+            key = _share_key(self, alpha)
+            kept = _SHARED.get(key)
+            if kept is not None and self in kept[3]:
+                Hk, buf, cap, _ = kept
+                equal = torch.ones(1, dtype=torch.int32, device=H.device)
+                _lib.call("g2ptq_staged_equal", _lib.stream_ptr(), _lib.ptr(self.buf), self.cap,
+                          _lib.ptr(buf), cap, self.height, self.k, _lib.ptr(equal))
+                if equal.item():
+                    H.copy_(Hk)
+                    self._flushed()
+                    return
         if self.dtype != DTYPE_BF16:
             nbytes = _lib.query_size("g2ptq_hessian_gram_ex_workspace", self.kind, self.dtype,
                                      self.k, self.C, self.G)
@@ -213,12 +286,36 @@ class GramStager:
         if TIMING is not None:
             e1.record()
             TIMING.append((e0, e1, flops, self.k, C))
+        if key is not None:
+            # the live stagers holding the same staged sequence, each not yet flushed
+            waiting = [st for st in list(_BY_FIRST.get(self.ids[0], ()))
+                       if st is not self and st.k > 0 and st.kind == KIND_GPTQ and
+                       st.dtype == self.dtype and st.ids == self.ids and
+                       _share_key(st, alpha) == key]
+            if waiting:
+                _SHARED[key] = (H.clone(), self.buf, self.cap, weakref.WeakSet(waiting))
+        self._flushed()
+
+    def _flushed(self):
+        """The buffer is empty: a new token sequence starts."""
+        _drop_waiter(self)
+        if self._first is not None:
+            ws = _BY_FIRST.get(self._first)
+            if ws is not None:
+                ws.discard(self)
+                if not ws:
+                    del _BY_FIRST[self._first]
+            self._first = None
+        if len(_BY_FIRST) > 4096:  # stagers collected while holding tokens
+            for t in [t for t, ws in _BY_FIRST.items() if not ws]:
+                del _BY_FIRST[t]
+        self.ids = []
         self.k = 0
 
     def release(self):
         self.buf = None
         self.cap = 0
-        self.k = 0
+        self._flushed()
 
 
 def stager_for(owner, idx, device, kind, groups, dtype):

@@ -1353,6 +1353,45 @@ extern "C" int g2ptq_hessian_gram(void* stream, uint16_t* XT, int64_t ldt, int64
                    ws_bytes);
 }
 
+// *equal = 0 where rows × cols of two staged buffers differ anywhere: the
+// check before a stager copies the Gram another stager computed from what
+// should be the same tokens (16-byte chunks; rows grid-strided).
+__global__ __launch_bounds__(256) void staged_equal_kernel(const uint16_t* __restrict__ A,
+                                                           int64_t lda,
+                                                           const uint16_t* __restrict__ B,
+                                                           int64_t ldb, int64_t rows,
+                                                           int64_t chunks, int* equal) {
+  int diff = 0;
+  for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
+    const uint4* a = reinterpret_cast<const uint4*>(A + r * lda);
+    const uint4* b = reinterpret_cast<const uint4*>(B + r * ldb);
+#pragma unroll 4
+    for (int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x; c < chunks;
+         c += (int64_t)gridDim.x * 256) {
+      const uint4 x = a[c], y = b[c];
+      diff |= (x.x != y.x) | (x.y != y.y) | (x.z != y.z) | (x.w != y.w);
+    }
+  }
+  if (diff) *equal = 0;
+}
+
+extern "C" int g2ptq_staged_equal(void* stream, const uint16_t* A, int64_t lda, const uint16_t* B,
+                                  int64_t ldb, int64_t rows, int64_t cols, int* equal) {
+  G2PTQ_CHECK(A && B && equal, "staged_equal: null pointer");
+  G2PTQ_CHECK(rows >= 0 && cols >= 0 && cols % 8 == 0 && lda % 8 == 0 && ldb % 8 == 0 &&
+                  cols <= lda && cols <= ldb && (reinterpret_cast<uintptr_t>(A) & 15) == 0 &&
+                  (reinterpret_cast<uintptr_t>(B) & 15) == 0,
+              "staged_equal: columns and pitches must be multiples of 8 (16-byte aligned rows)");
+  if (rows == 0 || cols == 0) return G2PTQ_OK;
+  const int64_t chunks = cols / 8;
+  const dim3 grid((unsigned)std::min<int64_t>(cdiv(chunks, (int64_t)256 * 8), 64),
+                  (unsigned)std::min<int64_t>(rows, 8192));
+  hipLaunchKernelGGL(staged_equal_kernel, grid, dim3(256), 0, as_stream(stream), A, lda, B, ldb,
+                     rows, chunks, equal);
+  G2PTQ_LAUNCHED();
+  return G2PTQ_OK;
+}
+
 extern "C" int g2ptq_gptaq_stage(void* stream, const uint16_t* X, const uint16_t* Xfp, int64_t T,
                                  int64_t C, int64_t ldx, int64_t ldxf, uint16_t* XT, int64_t ldt,
                                  int64_t t_off) {

@@ -9,7 +9,7 @@ the fused lazy-batch compensation in libg2ptq_hip.so.
 import torch
 
 from . import _core, _lib
-from ._stage import (KIND_GPTQ, bump, lazy_counter, single_batch_stager, staged_attr,
+from ._stage import (DTYPE_BF16, KIND_GPTQ, bump, lazy_counter, single_batch_stager, staged_attr,
                      stager_for)
 from .compressed_tensors_utils import compress_layers
 from .graph_utils import run_graph, validate_tensors
@@ -67,7 +67,11 @@ class GPTQ:
         return _core.onload_attrs(self, ("H",), enabled=self.offload_hessians, device=self.dev)
 
     def add_batch(self, idx, inp, out):
-        """gptq_utils.py:115-126: H ← H·n/(n+t) + (2/(n+t))·XᵀX, t = #sequences."""
+        """gptq_utils.py:115-126: H ← H·n/(n+t) + (2/(n+t))·XᵀX, t = #sequences.
+
+        A bf16 batch is staged with its source, so that linears fed the same
+        input tensors compute their common Gram once (not for the owner of a
+        ``SharedInputHessian``, which shares the Hessian itself)."""
         # slot copies made by a shared finalize are stale now
         self.__dict__.pop("_h_alias", None)
         tmp = 1 if inp.dim() == 2 else inp.shape[0]  # a 2-D input is one sequence
@@ -82,7 +86,7 @@ class GPTQ:
             fits = st.fits(T)
         n = self._n[idx] + tmp
         if fits:
-            st.stage(X)
+            st.stage(X, share=dt == DTYPE_BF16 and self.__dict__.get("_share_grams", True))
         else:
             # a batch larger than the staging budget: update H directly
             n0 = self._n_flushed[idx]

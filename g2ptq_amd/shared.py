@@ -36,6 +36,9 @@ class SharedInputHessian:
                                  f"{type(inst).__name__} Hessian depends on more than the input")
         self.members = list(members)
         self._factors = {}
+        # the group shares its Hessian itself: its owner's stager need not
+        # look for other stagers of the same batches
+        self.members[0][0].__dict__["_share_grams"] = False
 
     # The members' Hessians are bit-identical, and so are their dampened
     # inverse-Cholesky factors: the first member to factor stores it here and

@@ -114,6 +114,15 @@ int g2ptq_hessian_stage(void* stream, const uint16_t* X, int64_t T, int64_t C, i
 int g2ptq_hessian_gram_workspace(int64_t K, int64_t C, size_t* bytes);
 int g2ptq_hessian_gram(void* stream, uint16_t* XT, int64_t ldt, int64_t K, int64_t C, float alpha,
                        float beta, float* H, int64_t ldh, void* ws, size_t ws_bytes);
+/* Sets *equal = 0 where the first `cols` columns of `rows` rows of two staged
+ * buffers (pitches lda, ldb) differ; the caller sets *equal = 1 before.  No
+ * counterpart in the reference: the reference accumulates every linear's
+ * Hessian separately, and the Python layer uses this check before giving a
+ * linear the Gram another linear computed from tokens staged from the same
+ * input addresses (q/k/v, gate/up hooks), so the copy is taken only when the
+ * staged operands are bit-identical.  cols, lda and ldb multiples of 8. */
+int g2ptq_staged_equal(void* stream, const uint16_t* A, int64_t lda, const uint16_t* B,
+                       int64_t ldb, int64_t rows, int64_t cols, int* equal);
 
 /* GPTAQ: H = beta·H + alpha·XᵀX and Dx = beta·Dx + alpha·(X_fp − X)ᵀX, with
  * Dx[i][j] = Σ_t (x_fp − x)[t,i]·x[t,j].  Replaces GPTAQ.add_batch

@@ -216,3 +216,101 @@ def test_staging_buffer_shrinks_to_free_memory(dev, monkeypatch):
     assert 3000 <= cap < 32 * 3000, cap
     torch.cuda.synchronize()
     _close(gq.H[0], st["H"][0], "shrunk staging")
+
+
+def _shared_insts(dev, C, B):
+    from g2ptq_amd import GPTQ
+    return GPTQ(_layers(1, 64, C, dev)), GPTQ(_layers(B, 64, C, dev))
+
+
+def test_linears_fed_the_same_tensors_share_their_gram(dev):
+    """The reference's driver keeps one Hessian per linear (gptq_utils.py:497-505):
+    q and the k/v pair receive views of the same input tensors from their hooks
+    (``inp[0].data``).  Their first flushes run one Gram and copy it to the
+    others after the device compare of the staged tokens, bit for bit what each
+    computes on its own (a control fed clones of the same tensors, which stages
+    and multiplies by itself), and nothing is kept once every slot has read it."""
+    from g2ptq_amd import GPTQ, _stage
+    C = 768
+    g = gen(4101)
+    xs = [(torch.randn(2, 512, C, generator=g) * 2).bfloat16().to(dev) for _ in range(4)]
+    q, kv = _shared_insts(dev, C, 2)
+    ctl = GPTQ(_layers(1, 64, C, dev))
+    for x in xs:
+        q.add_batch(0, x.data, None)
+        kv.add_batch(0, x.data, None)
+        kv.add_batch(1, x.data, None)
+        ctl.add_batch(0, x.clone(), None)
+    old, _stage.TIMING = _stage.TIMING, []
+    try:
+        Hq, Hkv, Hc = q.H.clone(), kv.H.clone(), ctl.H.clone()
+        grams = len(_stage.TIMING)
+    finally:
+        _stage.TIMING = old
+    torch.cuda.synchronize()
+    assert grams == 2, grams  # q's (kept for the k/v slots) and the control's
+    assert torch.equal(Hq[0], Hc[0])
+    assert torch.equal(Hkv[0], Hc[0]) and torch.equal(Hkv[1], Hc[0])
+    assert not _stage._SHARED
+    # the result matches the reference's running average
+    st = ohess.gptq_state(1, C)
+    for x in xs:
+        ohess.gptq_add_batch(st, 0, x.cpu())
+    _close(Hc[0], st["H"][0], "shared Gram")
+
+
+def test_changed_or_different_batches_do_not_share(dev):
+    """A tensor changed in place after one linear staged it (same address, other
+    tokens: the device compare refuses the copy), a batch only one linear saw,
+    and a second flush (beta ≠ 0) each make the Hessians compute their own
+    Gram; a result kept for a linear that then flushes differently is freed."""
+    from g2ptq_amd import GPTQ, _stage
+    C = 512
+    g = gen(4102)
+    x1 = torch.randn(1, 1024, C, generator=g).bfloat16().to(dev)
+    x2 = torch.randn(1, 1024, C, generator=g).bfloat16().to(dev)
+    # changed in place between the two linears' hooks
+    a, b = _shared_insts(dev, C, 1)
+    a.add_batch(0, x1, None)
+    x1.mul_(2)
+    b.add_batch(0, x1, None)
+    old, _stage.TIMING = _stage.TIMING, []
+    try:
+        Ha, Hb = a.H.clone(), b.H.clone()
+        grams = len(_stage.TIMING)
+    finally:
+        _stage.TIMING = old
+    torch.cuda.synchronize()
+    assert grams == 2 and not _stage._SHARED
+    assert torch.equal(Hb[0], 4 * Ha[0])  # bf16 doubling and the Gram's sums are exact
+    # an extra batch on one linear: another sequence, nothing shared or kept
+    a, b = _shared_insts(dev, C, 1)
+    for inst in (a, b):
+        inst.add_batch(0, x2, None)
+    b.add_batch(0, x1, None)
+    old, _stage.TIMING = _stage.TIMING, []
+    try:
+        a.H, b.H  # noqa: B018 (reads flush)
+        grams = len(_stage.TIMING)
+    finally:
+        _stage.TIMING = old
+    assert grams == 2 and not _stage._SHARED
+    # same batches, but the second linear's own Hessian had an earlier flush
+    # (its next flush has beta ≠ 0): it computes its own Gram, and the result
+    # kept for it is freed when it does
+    a, b = _shared_insts(dev, C, 1)
+    b.add_batch(0, x1, None)
+    b.H  # noqa: B018
+    for inst in (a, b):
+        inst.add_batch(0, x2, None)
+    Ha, Hb = a.H.clone(), b.H.clone()
+    torch.cuda.synchronize()
+    assert not _stage._SHARED
+    ctl = GPTQ(_layers(1, 64, C, dev))
+    ctl.add_batch(0, x1.clone(), None)
+    ctl.H  # noqa: B018 (the same two flushes as the second linear's)
+    ctl.add_batch(0, x2.clone(), None)
+    assert torch.equal(Hb[0], ctl.H[0])
+    c2 = GPTQ(_layers(1, 64, C, dev))
+    c2.add_batch(0, x2.clone(), None)
+    assert torch.equal(Ha[0], c2.H[0])

@@ -319,3 +319,16 @@ def test_guided_gptq_reuses_gptq_compensation():
     from g2ptq_amd import GPTQ, GPTQGuided
     assert GPTQGuided._run_compensation_block is GPTQ._run_compensation_block
     assert GPTQGuided._run_compensation is GPTQ._run_compensation
+
+
+
+def test_batch_source_of_hook_views():
+    """The source a staged GPTQ batch records: a hook's ``inp[0].data`` view of
+    the same input gives the same source, other storage or another token count
+    another (a shared Gram is still taken only after the device has compared
+    the staged tokens)."""
+    from g2ptq_amd._stage import batch_source
+    x = torch.randn(8, 16)
+    assert batch_source(x.data) == batch_source(x) == batch_source(x.view(8, 16))
+    assert batch_source(x.clone()) != batch_source(x)
+    assert batch_source(x[:4]) != batch_source(x)
