@@ -229,9 +229,11 @@ class GramStager:
 
     def flush(self, H, alpha, beta, Dx=None):
         """H = beta·H + alpha·(Gram of the staged tokens) (and Dx for GPTAQ;
-        H is (G, C, C) for the weighted kind); empties the buffer."""
+        H is (G, C, C) for the weighted kind); empties the buffer.  Returns the
+        key of a Gram result shared with other stagers (kept for them, or
+        copied from one), else None."""
         if self.k == 0:
-            return
+            return None
         if not H.is_cuda or (Dx is not None and not Dx.is_cuda):
             raise RuntimeError("staged Hessian tokens need the Hessian on the GPU: call "
                                "add_batch inside the onload context of the Hessian")
@@ -251,7 +253,7 @@ class GramStager:
                 if equal.item():
                     H.copy_(Hk)
                     self._flushed()
-                    return
+                    return key
         if self.dtype != DTYPE_BF16:
             nbytes = _lib.query_size("g2ptq_hessian_gram_ex_workspace", self.kind, self.dtype,
                                      self.k, self.C, self.G)
@@ -294,7 +296,10 @@ class GramStager:
                        _share_key(st, alpha) == key]
             if waiting:
                 _SHARED[key] = (H.clone(), self.buf, self.cap, weakref.WeakSet(waiting))
+            else:
+                key = None
         self._flushed()
+        return key
 
     def _flushed(self):
         """The buffer is empty: a new token sequence starts."""

@@ -54,13 +54,28 @@ class GPTQ:
         stagers = getattr(self, "_stagers", None)
         if not stagers:
             return
+        src = self.__dict__.setdefault("_gram_src", [None] * self.num_layers)
+        flushed = False
         for i in (range(self.num_layers) if idx is None else (idx,)):
             st = stagers[i]
             if st is None or st.k == 0:
                 continue
             n, n0 = self._n[i], self._n_flushed[i]
-            st.flush(self._H[i], _core.sqrt_scale_sq(n), _core.f32(n0 / n))
+            src[i] = st.flush(self._H[i], _core.sqrt_scale_sq(n), _core.f32(n0 / n))
             self._n_flushed[i] = n
+            flushed = True
+        if flushed:
+            # slots whose Hessians are copies of one Gram result (their own or
+            # another stager's): the batched factor factors the first only
+            first, alias = {}, {}
+            for i, key in enumerate(src):
+                if key is not None:
+                    if key in first:
+                        alias[i] = first[key]
+                    else:
+                        first[key] = i
+            if alias:
+                self.__dict__.setdefault("_h_alias", {}).update(alias)
 
     def _maybe_onload_hessian(self, idx=None):
         """gptq_utils.py:109-113."""

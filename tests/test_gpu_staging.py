@@ -314,3 +314,44 @@ def test_changed_or_different_batches_do_not_share(dev):
     c2 = GPTQ(_layers(1, 64, C, dev))
     c2.add_batch(0, x2.clone(), None)
     assert torch.equal(Ha[0], c2.H[0])
+
+
+def test_slots_holding_one_shared_gram_factor_once(dev):
+    """A two-slot instance (gate/up) whose slots staged the same hook inputs: the
+    second slot copies the first's Gram, the instance records the slots as
+    copies, and its batched factor factors one of them; the quantized weights
+    equal those of an instance fed clones (two Grams, two factors) bit for bit."""
+    from g2ptq_amd import GPTQ, WeightQuantizer, make_group_quantizers, _stage
+    C, R = 512, 96
+    g = gen(4103)
+    xs = [(torch.randn(2, 256, C, generator=g) * torch.exp(torch.randn(C, generator=g)))
+          .bfloat16().to(dev) for _ in range(3)]
+    w = [(torch.randn(R, C, generator=g) * 0.02).bfloat16() for _ in range(2)]
+
+    def inst(clone):
+        lins = _layers(2, R, C, dev)
+        for lin, wi in zip(lins, w):
+            with torch.no_grad():
+                lin.weight.copy_(wi.to(dev))
+        gq = GPTQ(lins)
+        q = WeightQuantizer()
+        q.configure(4, perchannel=True, sym=True)
+        gq.quantizer = make_group_quantizers(q, C, 128)
+        # the control's clones all stay alive: no two at one address
+        inputs = [[x.clone() if clone else x.data for _ in range(2)] for x in xs]
+        for xb in inputs:
+            for b in range(2):
+                gq.add_batch(b, xb[b], None)
+        return gq, lins
+
+    a, la = inst(False)
+    c, lc = inst(True)
+    Ha, Hc = a.H.clone(), c.H.clone()
+    assert a.__dict__.get("_h_alias") == {1: 0}
+    assert "_h_alias" not in c.__dict__
+    assert torch.equal(Ha, Hc) and not _stage._SHARED
+    for gq in (a, c):
+        gq.fasterquant(blocksize=128, percdamp=0.01, groupsize=128, backend="hip")
+    torch.cuda.synchronize()
+    for x, y in zip(la, lc):
+        assert torch.equal(x.weight, y.weight)
