@@ -51,6 +51,7 @@ the device (``g2ptq_staged_equal``) and copies the kept Gram only when they
 are bit-identical, else runs its own.  The Gram is deterministic, so every
 Hessian holds exactly the values it would have computed itself.
 """
+import itertools
 import os
 import weakref
 
@@ -106,11 +107,12 @@ def batch_source(X):
 
 
 # Gram results kept for stagers that staged from the same sources: key →
-# (H, the staged buffer, its pitch, the waiting stagers).  Stagers by the
-# first source they staged since their last flush, to find those that may
-# share a flush.
+# (H, the staged buffer, its pitch, the waiting stagers, a serial number
+# unique to the result).  Stagers by the first source they staged since their
+# last flush, to find those that may share a flush.
 _SHARED = {}
 _BY_FIRST = {}
+_SERIALS = itertools.count(1)
 
 
 def _share_key(st, alpha):
@@ -230,8 +232,8 @@ class GramStager:
     def flush(self, H, alpha, beta, Dx=None):
         """H = beta·H + alpha·(Gram of the staged tokens) (and Dx for GPTAQ;
         H is (G, C, C) for the weighted kind); empties the buffer.  Returns the
-        key of a Gram result shared with other stagers (kept for them, or
-        copied from one), else None."""
+        serial number of a Gram result shared with other stagers (kept for
+        them, or copied from one), else None."""
         if self.k == 0:
             return None
         if not H.is_cuda or (Dx is not None and not Dx.is_cuda):
@@ -246,14 +248,14 @@ class GramStager:
             key = _share_key(self, alpha)
             kept = _SHARED.get(key)
             if kept is not None and self in kept[3]:
-                Hk, buf, cap, _ = kept
+                Hk, buf, cap, _, serial = kept
                 equal = torch.ones(1, dtype=torch.int32, device=H.device)
                 _lib.call("g2ptq_staged_equal", _lib.stream_ptr(), _lib.ptr(self.buf), self.cap,
                           _lib.ptr(buf), cap, self.height, self.k, _lib.ptr(equal))
                 if equal.item():
                     H.copy_(Hk)
                     self._flushed()
-                    return key
+                    return serial
         if self.dtype != DTYPE_BF16:
             nbytes = _lib.query_size("g2ptq_hessian_gram_ex_workspace", self.kind, self.dtype,
                                      self.k, self.C, self.G)
@@ -294,12 +296,14 @@ class GramStager:
                        if st is not self and st.k > 0 and st.kind == KIND_GPTQ and
                        st.dtype == self.dtype and st.ids == self.ids and
                        _share_key(st, alpha) == key]
+            serial = None
             if waiting:
-                _SHARED[key] = (H.clone(), self.buf, self.cap, weakref.WeakSet(waiting))
-            else:
-                key = None
+                serial = next(_SERIALS)
+                _SHARED[key] = (H.clone(), self.buf, self.cap, weakref.WeakSet(waiting), serial)
+            self._flushed()
+            return serial
         self._flushed()
-        return key
+        return None
 
     def _flushed(self):
         """The buffer is empty: a new token sequence starts."""
@@ -398,6 +402,7 @@ def staged_attr(name):
             # cached factor (or its slot copies) came from
             self.__dict__.pop("_shared_factor", None)
             self.__dict__.pop("_h_alias", None)
+            self.__dict__.pop("_gram_src", None)
         setattr(self, private, value)
         if value is None:
             for st in getattr(self, "_stagers", None) or ():

@@ -6,6 +6,8 @@ Drop-in for the ``GPTQ`` class and ``run_eager`` of gptq_utils/gptq_utils.py
 Gram kernel, ``fasterquant`` runs the dampened inverse-Cholesky factor and
 the fused lazy-batch compensation in libg2ptq_hip.so.
 """
+import collections
+
 import torch
 
 from . import _core, _lib
@@ -66,7 +68,8 @@ class GPTQ:
             flushed = True
         if flushed:
             # slots whose Hessians are copies of one Gram result (their own or
-            # another stager's): the batched factor factors the first only
+            # another stager's, by its serial number): the batched factor
+            # factors the first only
             first, alias = {}, {}
             for i, key in enumerate(src):
                 if key is not None:
@@ -173,8 +176,12 @@ class GPTQ:
                 H = _core.permute_sym(H, perm)
                 if H_diag is not None:
                     H_diag = _core.permute_cols(H_diag, perm)
-            Hinv, _ = _core.factor(H, percdamp, getattr(self, "_shared_factor", None),
-                                   key=bool(actorder), alias=self.__dict__.pop("_h_alias", None))
+            shared = getattr(self, "_shared_factor", None)
+            src = self.__dict__.get("_gram_src")
+            if shared is None and src and src[0] is not None and all(x == src[0] for x in src):
+                shared = _GramFactors(src[0])
+            Hinv, _ = _core.factor(H, percdamp, shared, key=bool(actorder),
+                                   alias=self.__dict__.pop("_h_alias", None))
         Q, W_int, Scale = _compensate(_lib.VARIANT_GPTQ, self.quantizer, W, Hinv, blocksize,
                                       groupsize, static_groups,
                                       perm if static_groups and actorder else None, flags, graph,
@@ -195,6 +202,28 @@ class GPTQ:
         self.Losses = None
         self.nsamples = None
         _lib.release_workspaces()
+
+
+class _GramFactors:
+    """The factor cache of Hessians that are copies of one shared Gram result
+    (by its serial number): every slot of an instance holding it, and every
+    instance, gets the same prepared Hessian, so the first to factor stores U
+    and the others reuse it.  The two most recent results are kept."""
+    _cache = collections.OrderedDict()
+
+    def __init__(self, serial):
+        self.serial = serial
+
+    def cached_factor(self, ck):
+        hit = self._cache.get((self.serial, ck))
+        if hit is not None:
+            self._cache.move_to_end((self.serial, ck))
+        return hit
+
+    def store_factor(self, ck, U, damp):
+        self._cache[(self.serial, ck)] = (U, damp)
+        while len(self._cache) > 2:
+            self._cache.popitem(last=False)
 
 
 def _compensate(variant, quantizers, W, U, blocksize, groupsize, static_groups, qparam_perm,

@@ -355,3 +355,55 @@ def test_slots_holding_one_shared_gram_factor_once(dev):
     torch.cuda.synchronize()
     for x, y in zip(la, lc):
         assert torch.equal(x.weight, y.weight)
+
+
+def test_instances_holding_one_shared_gram_factor_once(dev, monkeypatch):
+    """q and the k/v pair hold copies of one Gram result: q's fasterquant factors
+    it, the k/v instance reuses that factor (one factor launch for both), and
+    the quantized weights equal those of instances fed separate clones."""
+    from g2ptq_amd import GPTQ, WeightQuantizer, _lib, make_group_quantizers
+    C, R = 512, 80
+    g = gen(4104)
+    xs = [(torch.randn(2, 256, C, generator=g) * torch.exp(torch.randn(C, generator=g)))
+          .bfloat16().to(dev) for _ in range(3)]
+    w = [(torch.randn(R, C, generator=g) * 0.02).bfloat16() for _ in range(3)]
+
+    def make(ws):
+        lins = _layers(len(ws), R, C, dev)
+        for lin, wi in zip(lins, ws):
+            with torch.no_grad():
+                lin.weight.copy_(wi.to(dev))
+        gq = GPTQ(lins)
+        q = WeightQuantizer()
+        q.configure(4, perchannel=True, sym=True)
+        gq.quantizer = make_group_quantizers(q, C, 128)
+        return gq, lins
+
+    (q, lq), (kv, lkv) = make(w[:1]), make(w[1:])
+    (qc, lqc), (kvc, lkvc) = make(w[:1]), make(w[1:])
+    clones = [[x.clone() for _ in range(3)] for x in xs]  # all alive: distinct addresses
+    for x, cl in zip(xs, clones):
+        q.add_batch(0, x.data, None)
+        kv.add_batch(0, x.data, None)
+        kv.add_batch(1, x.data, None)
+        qc.add_batch(0, cl[0], None)
+        kvc.add_batch(0, cl[1], None)
+        kvc.add_batch(1, cl[2], None)
+    calls = []
+    real = _lib.call
+
+    def counting(name, *args):
+        if name == "g2ptq_inv_chol_upper":
+            calls.append(name)
+        return real(name, *args)
+
+    monkeypatch.setattr(_lib, "call", counting)
+    for gq in (q, kv):
+        gq.fasterquant(blocksize=128, percdamp=0.01, groupsize=128, backend="hip")
+    shared_factors = len(calls)
+    for gq in (qc, kvc):
+        gq.fasterquant(blocksize=128, percdamp=0.01, groupsize=128, backend="hip")
+    torch.cuda.synchronize()
+    assert shared_factors == 1 and len(calls) == 3, calls
+    for x, y in zip(lq + lkv, lqc + lkvc):
+        assert torch.equal(x.weight, y.weight)
