@@ -332,3 +332,20 @@ def test_batch_source_of_hook_views():
     assert batch_source(x.data) == batch_source(x) == batch_source(x.view(8, 16))
     assert batch_source(x.clone()) != batch_source(x)
     assert batch_source(x[:4]) != batch_source(x)
+
+
+def test_gram_factor_cache_keeps_two_results():
+    """The factor cache of shared Gram results: keyed by the result's serial
+    number and the factor options, the two most recently used kept."""
+    from g2ptq_amd.gptq_utils import _GramFactors
+    _GramFactors._cache.clear()
+    a, b, c = _GramFactors(1), _GramFactors(2), _GramFactors(3)
+    a.store_factor((0.01, False), "Ua", 0.01)
+    b.store_factor((0.01, False), "Ub", 0.01)
+    assert a.cached_factor((0.01, False)) == ("Ua", 0.01)  # a is now the most recent
+    assert a.cached_factor((0.01, True)) is None           # other options: not cached
+    c.store_factor((0.01, False), "Uc", 0.01)              # evicts b
+    assert b.cached_factor((0.01, False)) is None
+    assert a.cached_factor((0.01, False)) == ("Ua", 0.01)
+    assert c.cached_factor((0.01, False)) == ("Uc", 0.01)
+    _GramFactors._cache.clear()
