@@ -750,3 +750,31 @@ def test_gemm_f32_256_tiles_equal_128_tiles(dev, M, N, K, batch):
     bound = torch.bmm(A.double().abs(), Bt.abs()) + 0.5 * Cm.double().abs()
     err = ((Dbig.double() - ref).abs() / bound).max().item()
     assert err <= 4e-7, err
+
+
+@pytest.mark.parametrize("n", [4096, 4099])  # 16-byte steps; per element
+def test_bf16_conversions_match_torch(dev, n):
+    """g2ptq_cast_check (fp32 → bf16, round to nearest even, NaN flag; the
+    write-back) and g2ptq_to_f32 (bf16 → fp32; the weights read in) bit-exact
+    against torch's conversions: zeros of both signs, infinities, subnormals,
+    rounding ties of both parities and values over e^±30."""
+    from g2ptq_amd import _lib
+    g = gen(5100 + n)
+    x = torch.randn(n, generator=g) * torch.exp(10 * torch.randn(n, generator=g))
+    x[:6] = torch.tensor([0.0, -0.0, float("inf"), -float("inf"), 1e-40, -3e-39])
+    x[8:16] = (torch.arange(1, 9, dtype=torch.int32) * 0x10000 + 0x3F808000).view(torch.float32)
+    xd = x.to(dev)
+    out = torch.empty(n, dtype=torch.bfloat16, device=dev)
+    flags = torch.zeros(1, dtype=torch.int32, device=dev)
+    _lib.call("g2ptq_cast_check", _lib.stream_ptr(dev), _lib.ptr(xd), _lib.ptr(out), n, 0,
+              _lib.ptr(flags))
+    ref = x.bfloat16()
+    assert torch.equal(out.cpu().view(torch.int16), ref.view(torch.int16))
+    assert flags.item() == 0
+    back = torch.empty(n, device=dev)
+    _lib.call("g2ptq_to_f32", _lib.stream_ptr(dev), _lib.ptr(out), _lib.ptr(back), n, 0)
+    assert torch.equal(back.cpu().view(torch.int32), ref.float().view(torch.int32))
+    xd[n // 2] = float("nan")
+    _lib.call("g2ptq_cast_check", _lib.stream_ptr(dev), _lib.ptr(xd), _lib.ptr(out), n, 0,
+              _lib.ptr(flags))
+    assert flags.item() != 0 and torch.isnan(out[n // 2].float()).item()
